@@ -1,0 +1,244 @@
+"""Benchmark: fused paged decode over the packed RotorQuant cache on one MI355X.
+
+Workload: Llama-3-8B attention-layer shape (32 query / 8 kv
+heads, head_dim 128), IsoQuant fast 3-bit K and V, 64 sequences with context
+lengths uniform in [1024, 8192], block_size 16, seeded random block table; K/V
+drawn as N(0,1) * (1 + |N(0,3)|) per (head, channel) and pre-compressed into
+the cache by the library's own compress kernel; bf16 queries N(0,1).
+
+A step is one fused paged decode of the whole batch (rq_fused_decode: split-KV
+decode kernel + merge/back-rotation).  Three copies of the cache are rotated
+between steps so the 256 MB Infinity Cache cannot serve a step's reads from
+the previous one.
+
+Algorithmic bytes per step: sum_s L_s * 136 * H_kv (each packed KV byte once)
++ sum_s ceil(L_s/16) * 4 (block table) + B * H_q * D * 2 * 2 (q in, out) + 4 B.
+
+Prints one JSON line (rank 0).  --gpus > 1 is refused: this build targets one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "rotorquant-vllm_amd"), os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def config1_lens(B=64, cfg=1):
+    import torch
+    return torch.randint(1024, 8192 + 1, (B,), generator=torch.Generator().manual_seed(1000 * cfg + 4)).tolist()
+
+
+def build_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=3, v_bits=3, iso_mode="fast",
+                        copies=3):
+    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store."""
+    import numpy as np
+    import torch
+
+    from rotorquant_vllm import kernels as K
+    from rq_testlib import Params, paged_layout
+
+    dev = torch.device("cuda")
+    p = Params(mode, k_bits, v_bits, iso_mode=iso_mode, head_dim=D)
+    bt, NB, slots = paged_layout(lens, BS, cfg)
+    total_bytes = 256 * H
+    cache = torch.zeros(NB, BS, total_bytes, dtype=torch.uint8, device=dev)
+    slot_all = torch.from_numpy(np.concatenate(slots)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(1000 * cfg)
+    gs = torch.Generator(device=dev).manual_seed(1000 * cfg + 2)
+    k_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
+    v_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
+    rte, rto, kb, vb = (t.to(dev) for t in (p.rte, p.rto, p.kb, p.vb))
+    chunk = 32768
+    for s in range(0, slot_all.numel(), chunk):
+        n = min(chunk, slot_all.numel() - s)
+        k = (torch.randn(n, H, D, generator=g, device=dev) * k_scale).to(torch.float16)
+        v = (torch.randn(n, H, D, generator=g, device=dev) * v_scale).to(torch.float16)
+        K.compress_store(k, v, cache, slot_all[s:s + n], rte, rto, kb, vb, rot_block=p.blk)
+    caches = [cache] + [cache.clone() for _ in range(copies - 1)]
+    q = torch.randn(len(lens), HQ, D, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
+                    device=dev).to(torch.bfloat16)
+    return dict(p=p, caches=caches, bt=torch.from_numpy(bt).to(dev), lens=torch.tensor(lens, dtype=torch.int32,
+                device=dev), q=q, H=H, HQ=HQ, D=D, BS=BS, lens_host=list(lens), bt_host=bt, NB=NB)
+
+
+def decode_bytes(lens, H, HQ, D, BS):
+    B = len(lens)
+    return (sum(lens) * 136 * H * D // 128 + sum((L + BS - 1) // BS for L in lens) * 4 + B * HQ * D * 2 * 2 + 4 * B)
+
+
+def time_decode(inp, steps, warmup):
+    import torch
+
+    from rotorquant_vllm import kernels as K
+
+    p = inp["p"]
+    dev = inp["q"].device
+    kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
+    out = torch.empty_like(inp["q"])
+    max_len = max(inp["lens_host"])
+    caches = inp["caches"]
+
+    def step(i):
+        K.fused_paged_rq_decode(inp["q"], caches[i % len(caches)], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
+                                inp["D"], inp["BS"], out=out, max_seq_len=max_len)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        step(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return dict(wall_s=wall, avg_ms=sum(per) / len(per), median_ms=per[len(per) // 2], min_ms=per[0]), out
+
+
+def time_compress(n_tokens=32768, H=8, D=128, steps=20):
+    """rq_compress_store of n_tokens K+V (fp16) into random slots: bytes = N * (2*H*D*2 + 136*H + 8)."""
+    import torch
+
+    from rotorquant_vllm import kernels as K
+    from rq_testlib import Params
+
+    dev = torch.device("cuda")
+    p = Params("iso", 3, 3)
+    BS = 16
+    NB = n_tokens // BS + 8
+    cache = torch.zeros(NB, BS, 256 * H, dtype=torch.uint8, device=dev)
+    slots = torch.randperm(NB * BS, generator=torch.Generator().manual_seed(5))[:n_tokens].to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    k = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
+    v = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
+    args = (k, v, cache, slots, p.rte.to(dev), p.rto.to(dev), p.kb.to(dev), p.vb.to(dev))
+    for _ in range(3):
+        K.compress_store(*args, rot_block=4)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        K.compress_store(*args, rot_block=4)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    nbytes = n_tokens * (2 * H * D * 2 + 136 * H + 8)
+    return dict(tokens=n_tokens, us=ms * 1e3, GBps=nbytes / (ms * 1e-3) / 1e9)
+
+
+def cpu_baseline(inp, budget_s=15.0):
+    """CPU path on a bounded sample: oracle decompress of each sequence's blocks + torch fp32 attention."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    p = inp["p"]
+    cache = inp["caches"][0].cpu().numpy()
+    q = inp["q"].float().cpu()
+    R = p.R.numpy().astype(np.float64)
+    lens = inp["lens_host"]
+    H, HQ, D = inp["H"], inp["HQ"], inp["D"]
+    G = HQ // H
+    done_bytes = 0
+    n_seq = 0
+    t0 = time.perf_counter()
+    for b, L in enumerate(lens):
+        K_, V_ = O.gather_seq(cache, inp["bt_host"][b], L, H, D, p.kc.numpy(), p.vc.numpy())
+        Kt = torch.from_numpy(K_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
+        Vt = torch.from_numpy(V_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
+        qr = torch.from_numpy((q[b].numpy().astype(np.float64) @ R.T).astype(np.float32))
+        s = torch.einsum("hd,hld->hl", qr, Kt) / math.sqrt(D)
+        o = torch.einsum("hl,hld->hd", torch.softmax(s, -1), Vt)
+        _ = o.numpy() @ R.astype(np.float32)
+        done_bytes += decode_bytes([L], H, HQ, D, inp["BS"]) - 0
+        n_seq += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return dict(value=done_bytes / el / 1e9, unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{n_seq} of {len(lens)} config-1 sequences ({sum(lens[:n_seq])} tokens): oracle C "
+                       f"decompress + torch fp32 attention, {el:.1f} s", cpu=cpu_model(), os_cpu_count=os.cpu_count())
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-compress", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode path shards by (sequence, kv head) with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    lens = config1_lens()
+    inp = build_decode_inputs(lens)
+    torch.cuda.synchronize()
+    t, _ = time_decode(inp, args.steps, args.warmup)
+    nbytes = decode_bytes(lens, 8, 32, 128, 16)
+    step_s = t["avg_ms"] * 1e-3
+    gbs = nbytes / step_s / 1e9
+    result = {
+        "metric": "fused paged decode HBM GB/s (Llama-3-8B layer, iso fast 3-bit, B=64, L~U[1024,8192])",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t["wall_s"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*(1+|N(0,3)|) K/V compressed into the cache; N(0,1) bf16 q)",
+        "config": {"workload": "BASELINE config 1: fused paged decode, 32 q / 8 kv heads, D 128, B 64, "
+                               "L~U[1024,8192], block 16, iso fast 3-bit K/V",
+                   "batch": 64, "sum_ctx_tokens": int(sum(lens)), "algorithmic_bytes_per_step": int(nbytes),
+                   "cache_copies_rotated": len(inp["caches"])},
+        "decode_tok_per_s": round(64 / step_s, 1),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "step_ms": {k: round(v, 5) for k, v in t.items() if k != "wall_s"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rq_fused_decode (decode_kernel + decode_merge_kernel), HIP events per launch"},
+    }
+    if not args.no_compress:
+        result["compress"] = time_compress()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(inp)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

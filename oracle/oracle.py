@@ -1,0 +1,318 @@
+"""TEST INFRASTRUCTURE ONLY -- CPU oracle for the RotorQuant KV-cache hot path.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker.  The product (rotorquant-vllm_amd/) never
+calls it.
+
+Restates the reference (tpurtell/rotorquant-vllm) on the CPU:
+
+  compress / decompress ........ rq_oracle.c (bit-exact restatement, see there)
+  lloyd_max_closed_form ........ src/rotorquant_vllm/quantization/lloyd_max.py:32-86
+                                 (same schedule, exact Gaussian integrals)
+  slot layout .................. src/rotorquant_vllm/vllm/rq_backend.py:155-188, :482-490
+  compress_store ............... rq_backend.py:585-657
+  paged_decompress ............. rq_backend.py:737-852
+  decode_attention ............. src/rotorquant_vllm/triton/fused_paged_rq_decode.py:252-312
+                                 (math of the kernel :76-206 in fp64)
+  prefill_attention ............ src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:296-363
+                                 (math in fp64; causal position offset L - T + i)
+
+Pins (what each function is checked against, besides the product):
+  compress/decompress: golden vectors produced by executing the reference's
+    torch op sequence (tests/golden/make_golden.py) -- bit-exact.
+  lloyd_max_closed_form: the scipy-quad fixture (centroids bit-equal, all
+    boundaries but the middle one bit-equal), Max's 1960 table for 3 bits.
+  layout: the reference's KAT (tests/test_vllm_integration.py:44-62).
+  paged_decompress: closed form (sorted unique + per-row decompress).
+  decode/prefill attention: closed forms (L = 1 -> V row, identical keys ->
+    mean of V, zero context -> zeros) and a float64 softmax written
+    independently in the tests.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "build", "librq_oracle.so")
+_lib = None
+
+DTYPE_CODE = {"float16": 0, "bfloat16": 1, "float32": 2}
+
+
+def build() -> str:
+    """Compile rq_oracle.c (make) and return the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.rqo_compress.restype = ctypes.c_int64
+        L.rqo_compress.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.rqo_decompress.restype = None
+        L.rqo_decompress.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        L.rqo_row_norm.restype = ctypes.c_float
+        L.rqo_row_norm.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# Raw-bits helpers (numpy has no bfloat16; arrays hold uint16 bit patterns)
+# ---------------------------------------------------------------------------
+
+def to_bits(t) -> tuple[np.ndarray, str]:
+    """torch tensor (f16 / bf16 / f32, CPU) -> (contiguous numpy array of raw bits, dtype name)."""
+    import torch
+    name = str(t.dtype).replace("torch.", "")
+    t = t.detach().contiguous().cpu()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16).copy(), name
+    return t.float().numpy().copy(), "float32"
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round fp32 values to bf16 (nearest even) and return them as fp32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bfloat16":
+        return bf16_round(x)
+    if dtype == "float16":
+        with np.errstate(over="ignore"):  # values beyond fp16 range become inf, as torch's cast does
+            return x.astype(np.float32).astype(np.float16).astype(np.float32)
+    return x.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Compress / decompress (rq_oracle.c)
+# ---------------------------------------------------------------------------
+
+def compress(x_bits: np.ndarray, dtype: str, rot_t_even: np.ndarray, rot_t_odd: np.ndarray,
+             boundaries: np.ndarray, blk: int, want_ties: bool = False):
+    """(N, H, D) raw-bits input -> packed (N, H, D/2) u8, norms (N, H, 1) f32[, tie mask, tie count]."""
+    N, H, D = x_bits.shape
+    M = N * H
+    x = np.ascontiguousarray(x_bits)
+    re = np.ascontiguousarray(rot_t_even, dtype=np.float32)
+    ro = np.ascontiguousarray(rot_t_odd, dtype=np.float32)
+    b = np.ascontiguousarray(boundaries, dtype=np.float32)
+    packed = np.zeros((M, D // 2), np.uint8)
+    norms = np.zeros((M,), np.float32)
+    ties = np.zeros((M, D), np.uint8) if want_ties else None
+    n_ties = lib().rqo_compress(_ptr(x), DTYPE_CODE[dtype], M, D, _ptr(re), _ptr(ro), blk, _ptr(b), b.size,
+                                _ptr(packed), _ptr(norms), _ptr(ties) if want_ties else None)
+    out = (packed.reshape(N, H, D // 2), norms.reshape(N, H, 1))
+    if want_ties:
+        return out + (ties.reshape(N, H, D), int(n_ties))
+    return out
+
+
+def decompress_f32(packed: np.ndarray, norms: np.ndarray, centroids: np.ndarray) -> np.ndarray:
+    """(N, H, D/2) u8 + (N, H, 1) f32 -> (N, H, D) fp32 products centroid * norm (before the cast)."""
+    N, H, half = packed.shape
+    D = 2 * half
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    n = np.ascontiguousarray(norms, dtype=np.float32).reshape(-1)
+    c = np.ascontiguousarray(centroids, dtype=np.float32)
+    out = np.zeros((N * H, D), np.float32)
+    lib().rqo_decompress(_ptr(p), _ptr(n), N * H, D, _ptr(c), c.size, _ptr(out))
+    return out.reshape(N, H, D)
+
+
+def decompress(packed, norms, centroids, dtype: str) -> np.ndarray:
+    """Decompress and apply the reference's `.to(dtype)` cast; returns fp32 values of the rounded result."""
+    return round_to(decompress_f32(packed, norms, centroids), dtype)
+
+
+# ---------------------------------------------------------------------------
+# Lloyd-Max codebook, closed form (lloyd_max.py:32-86 schedule)
+# ---------------------------------------------------------------------------
+
+def lloyd_max_closed_form(d: int, bits: int, max_iter: int = 200, tol: float = 1e-10):
+    """Same iteration as the reference, with exact truncated-Gaussian means.
+
+    Centroid update: E[X | a < X < b] = sigma^2 (phi(a) - phi(b)) / (Phi(b) - Phi(a))
+    in units of sigma = 1/sqrt(d).  Returns float64 (centroids, boundaries, iterations).
+    """
+    n = 2 ** bits
+    sigma = 1.0 / math.sqrt(d)
+    lo, hi = -3.5 * sigma, 3.5 * sigma
+    c = [lo + (hi - lo) * (i + 0.5) / n for i in range(n)]
+    it = 0
+    for it in range(max_iter):
+        b = [(c[i] + c[i + 1]) / 2.0 for i in range(n - 1)]
+        edges = [lo * 3] + b + [hi * 3]
+        new = []
+        for i in range(n):
+            za, zb = edges[i] / sigma, edges[i + 1] / sigma
+            den = 0.5 * (math.erfc(-zb / math.sqrt(2)) - math.erfc(-za / math.sqrt(2)))
+            num = sigma * (math.exp(-0.5 * za * za) - math.exp(-0.5 * zb * zb)) / math.sqrt(2 * math.pi)
+            new.append(num / den if den > 1e-15 else c[i])
+        shift = max(abs(new[i] - c[i]) for i in range(n))
+        c = new
+        if shift < tol:
+            break
+    b = [(c[i] + c[i + 1]) / 2.0 for i in range(n - 1)]
+    return np.array(c), np.array(b), it + 1
+
+
+# ---------------------------------------------------------------------------
+# Slot layout (rq_backend.py:155-188, :482-490)
+# ---------------------------------------------------------------------------
+
+def slot_layout(num_kv_heads: int, head_dim: int) -> dict:
+    half = head_dim // 2
+    H = num_kv_heads
+    k_idx_end = H * half
+    k_norm_end = k_idx_end + 4 * H
+    v_idx_end = k_norm_end + H * half
+    v_norm_end = v_idx_end + 4 * H
+    per_head = 1 << (2 * (half + 4) - 1).bit_length()  # next_power_of_2(136) = 256
+    return dict(k_idx_end=k_idx_end, k_norm_end=k_norm_end, v_idx_end=v_idx_end,
+                v_norm_end=v_norm_end, total_bytes=H * per_head)
+
+
+def compress_store(cache: np.ndarray, slot_mapping: np.ndarray, k_packed, k_norms, v_packed, v_norms) -> None:
+    """Assemble rows [K idx | K norms | V idx | V norms | 0] and scatter (rq_backend.py:609-657).
+
+    cache: (NB, BS, total_bytes) uint8, modified in place.  Slots < 0 are
+    skipped (the reference would wrap them to the last slot).
+    """
+    N, H, half = k_packed.shape
+    lay = slot_layout(H, 2 * half)
+    rows = np.zeros((N, cache.shape[-1]), np.uint8)
+    rows[:, :lay["k_idx_end"]] = k_packed.reshape(N, -1)
+    rows[:, lay["k_idx_end"]:lay["k_norm_end"]] = np.ascontiguousarray(k_norms.reshape(N, H), np.float32).view(np.uint8)
+    rows[:, lay["k_norm_end"]:lay["v_idx_end"]] = v_packed.reshape(N, -1)
+    rows[:, lay["v_idx_end"]:lay["v_norm_end"]] = np.ascontiguousarray(v_norms.reshape(N, H), np.float32).view(np.uint8)
+    flat = cache.reshape(-1, cache.shape[-1])
+    for t in range(N):
+        s = int(slot_mapping[t])
+        if s >= 0:
+            flat[s] = rows[t]
+
+
+def read_slots(cache: np.ndarray, num_kv_heads: int, head_dim: int):
+    """Split a (NB, BS, total_bytes) cache into per-token K/V packed indices and norms."""
+    NB, BS, TB = cache.shape
+    H, half = num_kv_heads, head_dim // 2
+    lay = slot_layout(H, head_dim)
+    flat = cache.reshape(NB * BS, TB)
+    kp = flat[:, :lay["k_idx_end"]].reshape(-1, H, half)
+    kn = np.ascontiguousarray(flat[:, lay["k_idx_end"]:lay["k_norm_end"]]).view(np.float32).reshape(-1, H, 1)
+    vp = flat[:, lay["k_norm_end"]:lay["v_idx_end"]].reshape(-1, H, half)
+    vn = np.ascontiguousarray(flat[:, lay["v_idx_end"]:lay["v_norm_end"]]).view(np.float32).reshape(-1, H, 1)
+    return kp, kn, vp, vn
+
+
+def paged_decompress(cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, dtype):
+    """_decompress_cache_paged (rq_backend.py:763-852): unique referenced blocks, their
+    decompressed K/V (U, BS, H, D) and the remapped block table."""
+    NB, BS, _ = cache.shape
+    bt = np.asarray(block_table)
+    need = (np.asarray(seq_lens) + BS - 1) // BS
+    mask = np.arange(bt.shape[1])[None, :] < need[:, None]
+    uniq = np.unique(bt[mask])
+    sel = cache[uniq]
+    kp, kn, vp, vn = read_slots(sel, num_kv_heads, head_dim)
+    k = decompress(kp, kn, k_cb, dtype).reshape(len(uniq), BS, num_kv_heads, head_dim)
+    v = decompress(vp, vn, v_cb, dtype).reshape(len(uniq), BS, num_kv_heads, head_dim)
+    remap = np.zeros(NB, np.int32)
+    remap[uniq] = np.arange(len(uniq), dtype=np.int32)
+    return k, v, remap[bt], len(uniq)
+
+
+# ---------------------------------------------------------------------------
+# Attention references (float64 over the exact dequantized K/V)
+# ---------------------------------------------------------------------------
+
+def gather_seq(cache, block_table_row, L, num_kv_heads, head_dim, k_cb, v_cb):
+    """K, V (L, H, D) fp64 dequantized (centroid * norm in fp32) for one sequence."""
+    NB, BS, TB = cache.shape
+    pos = np.arange(L)
+    phys = np.asarray(block_table_row)[pos // BS]
+    slots = cache[phys, pos % BS]  # (L, TB)
+    kp, kn, vp, vn = read_slots(slots.reshape(L, 1, TB), num_kv_heads, head_dim)
+    K = decompress_f32(kp, kn, k_cb).astype(np.float64)
+    V = decompress_f32(vp, vn, v_cb).astype(np.float64)
+    return K, V
+
+
+def rotate_q(q_f32: np.ndarray, R: np.ndarray, dtype: str) -> np.ndarray:
+    """q_rot = (q.float() @ R^T).to(dtype) (fused_paged_rq_decode.py:271)."""
+    return round_to((q_f32.astype(np.float64) @ R.astype(np.float64).T).astype(np.float32), dtype)
+
+
+def unrotate_out(out_rot: np.ndarray, R: np.ndarray, dtype: str) -> np.ndarray:
+    """out = (out_rot.to(dtype).float() @ R).to(dtype) (fused_paged_rq_decode.py:201-206, :308)."""
+    o = round_to(out_rot.astype(np.float32), dtype).astype(np.float64)
+    return round_to((o @ R.astype(np.float64)).astype(np.float32), dtype)
+
+
+def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype):
+    """q: (B, HQ, D) fp32 values of the dtype-rounded query.  Returns (B, HQ, D) fp32 values."""
+    B, HQ, D = q.shape
+    G = HQ // num_kv_heads
+    out = np.zeros((B, HQ, D), np.float32)
+    for b in range(B):
+        L = int(seq_lens[b])
+        qr = rotate_q(q[b], R, dtype).astype(np.float64)  # (HQ, D)
+        if L == 0:
+            o_rot = np.zeros((HQ, D))
+        else:
+            K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
+            o_rot = np.zeros((HQ, D))
+            for h in range(HQ):
+                kvh = h // G
+                s = (K[:, kvh, :] @ qr[h]) * sm_scale
+                p = np.exp(s - s.max())
+                o_rot[h] = (p @ V[:, kvh, :]) / p.sum()
+        out[b] = unrotate_out(o_rot, R, dtype)
+    return out
+
+
+def prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
+                      sm_scale, dtype):
+    """Causal attention; query i of sequence b sits at position seq_lens[b] - q_len_b + i."""
+    T, HQ, D = q.shape
+    G = HQ // num_kv_heads
+    out = np.zeros((T, HQ, D), np.float32)
+    for b in range(len(seq_lens)):
+        s0, s1 = int(cu_seqlens[b]), int(cu_seqlens[b + 1])
+        L = int(seq_lens[b])
+        T_b = s1 - s0
+        if T_b == 0:
+            continue
+        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
+        qr = rotate_q(q[s0:s1].reshape(-1, D), R, dtype).reshape(T_b, HQ, D).astype(np.float64)
+        pos = L - T_b + np.arange(T_b)
+        o_rot = np.zeros((T_b, HQ, D))
+        for h in range(HQ):
+            kvh = h // G
+            S = (qr[:, h, :] @ K[:, kvh, :].T) * sm_scale  # (T_b, L)
+            S[np.arange(L)[None, :] > pos[:, None]] = -np.inf
+            S -= S.max(axis=1, keepdims=True)
+            P = np.exp(S)
+            o_rot[:, h, :] = (P @ V[:, kvh, :]) / P.sum(axis=1, keepdims=True)
+        out[s0:s1] = unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(T_b, HQ, D)
+    return out

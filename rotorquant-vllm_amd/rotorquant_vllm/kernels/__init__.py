@@ -1,0 +1,362 @@
+"""Op-level API of the gfx950 RotorQuant kernels.
+
+Same names, signatures and argument meaning as the reference's op exports
+(src/rotorquant_vllm/triton/__init__.py:1-15), backed by librq_hip.so through
+the C ABI (include/rq_abi.h).  Differences, all deliberate:
+
+* Inputs must be ROCm device tensors.  The reference silently takes a torch CPU
+  path when `not x.is_cuda` (isoquant_compress.py:128-129); here a CPU tensor
+  raises, so no result can come from anything but the HIP kernels.
+* compress reads only the diagonal blocks of R^T (2x2, 4x4 or 8x8; checked
+  once per rotation tensor) instead of a dense tiled product.
+* fused_paged_rq_int8_prefill accepts any number of sequences (the reference
+  raises ValueError for more than one, fused_paged_rq_int8_prefill.py:305-309)
+  through the keyword `cu_seqlens_q`; with one sequence and no keyword it
+  behaves as the reference: all q tokens are the sequence's last q_len tokens.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "iso_compress",
+    "iso_decompress",
+    "planar_compress",
+    "planar_decompress",
+    "fused_paged_rq_int8_prefill",
+    "fused_paged_rq_decode",
+    "compress_store",
+    "paged_decompress",
+    "rotation_block",
+]
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "rotorquant_vllm.kernels runs only on ROCm device tensors (got a "
+                f"{t.device.type} tensor); there is no CPU path")
+        dev = t.device if dev is None else dev
+    _lib.load()
+    return dev
+
+
+# ---------------------------------------------------------------------------
+# Rotation block structure (checked once per tensor)
+# ---------------------------------------------------------------------------
+
+_block_cache: dict = {}
+
+
+def _block_of(RT: torch.Tensor) -> int:
+    """Smallest width in (2, 4, 8) for which RT is block diagonal."""
+    D = RT.shape[0]
+    idx = torch.arange(D)
+    for blk in (2, 4, 8):
+        if D % blk:
+            continue
+        off = (idx[:, None] // blk) != (idx[None, :] // blk)
+        if not bool((RT[off] != 0).any()):
+            return blk
+    raise ValueError("rotation is not block diagonal with 2x2, 4x4 or 8x8 blocks; "
+                     "the HIP compress kernels read only the diagonal blocks")
+
+
+def rotation_block(rotation: torch.Tensor) -> int:
+    """Diagonal block width of a (D, D) rotation R (cached per tensor version)."""
+    key = ("R", rotation.data_ptr(), rotation._version, tuple(rotation.shape), str(rotation.device))
+    blk = _block_cache.get(key)
+    if blk is None:
+        blk = _block_of(rotation.detach().float().cpu())
+        _block_cache[key] = blk
+    return blk
+
+
+def _rt_block(rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor) -> int:
+    key = ("RT", rot_T_even.data_ptr(), rot_T_even._version, rot_T_odd.data_ptr(), rot_T_odd._version,
+           tuple(rot_T_even.shape), str(rot_T_even.device))
+    blk = _block_cache.get(key)
+    if blk is None:
+        e, o = rot_T_even.detach().float().cpu(), rot_T_odd.detach().float().cpu()
+        D = e.shape[0]
+        RT = torch.empty(D, D)
+        RT[:, 0::2] = e
+        RT[:, 1::2] = o
+        blk = _block_of(RT)
+        _block_cache[key] = blk
+    return blk
+
+
+def _f32(t: torch.Tensor, device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Compress / decompress
+# ---------------------------------------------------------------------------
+
+def _compress(x, rot_T_even, rot_T_odd, boundaries):
+    dev = _require_device(x)
+    N, H, D = x.shape
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be fp16, bf16 or fp32, got {x.dtype}")
+    blk = _rt_block(rot_T_even, rot_T_odd)
+    x_flat = x.reshape(N * H, D).contiguous()
+    re, ro, b = _f32(rot_T_even, dev), _f32(rot_T_odd, dev), _f32(boundaries, dev)
+    packed = torch.empty(N, H, D // 2, dtype=torch.uint8, device=dev)
+    norms = torch.empty(N, H, 1, dtype=torch.float32, device=dev)
+    rc = _lib.load().rq_compress(x_flat.data_ptr(), _lib.dtype_code(x.dtype), N * H, D, re.data_ptr(),
+                                 ro.data_ptr(), blk, b.data_ptr(), b.numel(), packed.data_ptr(),
+                                 norms.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_compress")
+    return packed, norms
+
+
+def iso_compress(x: torch.Tensor, rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor,
+                 boundaries: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(N, H, D) fp16/bf16 -> nibble-packed (N, H, D/2) uint8 + (N, H, 1) fp32 norms.
+
+    Reference: src/rotorquant_vllm/triton/isoquant_compress.py:104-158.
+    """
+    return _compress(x, rot_T_even, rot_T_odd, boundaries)
+
+
+def planar_compress(x: torch.Tensor, rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor,
+                    boundaries: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """PlanarQuant compress; reference: src/rotorquant_vllm/triton/planarquant_compress.py:100-154."""
+    return _compress(x, rot_T_even, rot_T_odd, boundaries)
+
+
+def _decompress(packed, norms, centroids, dtype):
+    dev = _require_device(packed, norms)
+    N, H, half = packed.shape
+    D = 2 * half
+    p = packed.reshape(N * H, half).contiguous()
+    n = norms.reshape(N * H).to(torch.float32).contiguous()
+    c = _f32(centroids, dev)
+    out = torch.empty(N, H, D, dtype=dtype, device=dev)
+    rc = _lib.load().rq_decompress(p.data_ptr(), n.data_ptr(), N * H, D, c.data_ptr(), c.numel(),
+                                   out.data_ptr(), _lib.dtype_code(dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_decompress")
+    return out
+
+
+def iso_decompress(packed: torch.Tensor, norms: torch.Tensor, centroids: torch.Tensor,
+                   dtype: torch.dtype) -> torch.Tensor:
+    """(N, H, D/2) uint8 + (N, H, 1) fp32 -> (N, H, D) rotated-space values.
+
+    Reference: src/rotorquant_vllm/triton/isoquant_decompress.py:63-100.
+    """
+    return _decompress(packed, norms, centroids, dtype)
+
+
+def planar_decompress(packed: torch.Tensor, norms: torch.Tensor, centroids: torch.Tensor,
+                      dtype: torch.dtype) -> torch.Tensor:
+    """Reference: src/rotorquant_vllm/triton/planarquant_decompress.py:63-101."""
+    return _decompress(packed, norms, centroids, dtype)
+
+
+# ---------------------------------------------------------------------------
+# Fused K+V compress into the paged cache
+# ---------------------------------------------------------------------------
+
+def compress_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                   rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor, k_boundaries: torch.Tensor,
+                   v_boundaries: torch.Tensor, rot_block: int | None = None) -> None:
+    """Compress key/value (N, H, D) and write full slots of kv_cache (NB, BS, total_bytes).
+
+    Replaces RQAttentionImpl._compress_and_store (rq_backend.py:585-657).
+    Slots < 0 are skipped.
+    """
+    dev = _require_device(key, value, kv_cache, slot_mapping)
+    N, H, D = key.shape
+    if value.shape != key.shape or value.dtype != key.dtype:
+        raise ValueError("key and value must have the same shape and dtype")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise ValueError("key/value must be contiguous over head_dim")
+    if kv_cache.dtype != torch.uint8 or kv_cache.dim() != 3:
+        raise ValueError("kv_cache must be a (num_blocks, block_size, total_bytes) uint8 tensor")
+    blk = rot_block if rot_block is not None else _rt_block(rot_T_even, rot_T_odd)
+    sm = slot_mapping.to(torch.int64).contiguous()
+    if sm.numel() < N:
+        raise ValueError("slot_mapping shorter than the number of tokens")
+    N = min(N, sm.numel())
+    NB, BS, TB = kv_cache.shape
+    rc = _lib.load().rq_compress_store(
+        key.data_ptr(), value.data_ptr(), _lib.dtype_code(key.dtype), N, key.stride(0), key.stride(1),
+        value.stride(0), value.stride(1), H, D, sm.data_ptr(), kv_cache.data_ptr(), NB, BS,
+        kv_cache.stride(0), kv_cache.stride(1), TB, _f32(rot_T_even, dev).data_ptr(),
+        _f32(rot_T_odd, dev).data_ptr(), blk, k_boundaries.data_ptr(), k_boundaries.numel(),
+        v_boundaries.data_ptr(), v_boundaries.numel(), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_compress_store")
+
+
+# ---------------------------------------------------------------------------
+# Paged decompress (non-fused path)
+# ---------------------------------------------------------------------------
+
+def paged_decompress(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     num_kv_heads: int, head_dim: int, k_centroids: torch.Tensor, v_centroids: torch.Tensor,
+                     dtype: torch.dtype, out_k: torch.Tensor | None = None, out_v: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None):
+    """Decompress the physical blocks referenced by block_table.
+
+    Returns (key_cache, value_cache, remapped_block_table, num_unique) with
+    key/value of shape (capacity, BS, H, D); the first num_unique blocks hold
+    the referenced physical blocks in ascending physical order, as the
+    reference's _decompress_cache_paged (rq_backend.py:737-852).  num_unique is
+    a 1-element device int32 tensor (no host sync).
+    """
+    dev = _require_device(kv_cache, block_table, seq_lens)
+    NB, BS, _ = kv_cache.shape
+    bt = block_table.to(torch.int32)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    sl = seq_lens.to(torch.int32).contiguous()
+    B, MB = bt.shape
+    cap = NB if out_k is None else out_k.shape[0]
+    if out_k is None:
+        out_k = torch.empty(cap, BS, num_kv_heads, head_dim, dtype=dtype, device=dev)
+    if out_v is None:
+        out_v = torch.empty_like(out_k)
+    need = _lib.load().rq_paged_decompress_workspace_bytes(NB)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    remapped = torch.empty(B, MB, dtype=torch.int32, device=dev)
+    count = torch.empty(1, dtype=torch.int32, device=dev)
+    kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
+    rc = _lib.load().rq_paged_decompress(
+        kv_cache.data_ptr(), NB, BS, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
+        bt.data_ptr(), B, MB, bt.stride(0), sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(),
+        vc.numel(), out_k.data_ptr(), out_v.data_ptr(), _lib.dtype_code(dtype), cap, remapped.data_ptr(),
+        count.data_ptr(), workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_paged_decompress")
+    return out_k, out_v, remapped, count
+
+
+# ---------------------------------------------------------------------------
+# Fused paged decode
+# ---------------------------------------------------------------------------
+
+_ws_cache: dict = {}
+
+
+def _workspace(dev, nbytes: int) -> torch.Tensor:
+    buf = _ws_cache.get(dev)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        _ws_cache[dev] = buf
+    return buf
+
+
+def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                          seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
+                          rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
+                          sm_scale: float | None = None, out: torch.Tensor | None = None,
+                          max_seq_len: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused paged decode attention; q (num_seqs, H_Q, D) in original space -> output in original space.
+
+    Reference: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312 (same
+    arguments; `max_seq_len` optionally bounds seq_lens and sizes the split-KV
+    grid, default block_table.shape[1] * block_size; `workspace` optionally
+    supplies the split-KV scratch, a uint8 device tensor).
+    """
+    num_seqs, H_Q, D = q.shape
+    assert D == head_dim, f"D={D} != head_dim={head_dim}"
+    assert H_Q % num_kv_heads == 0
+    assert kv_cache.dtype == torch.uint8
+    assert block_table.dtype == torch.int32
+    assert seq_lens.dtype == torch.int32
+    dev = _require_device(q, kv_cache, block_table, seq_lens)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    MB = block_table.shape[1]
+    if max_seq_len is None:
+        max_seq_len = MB * block_size
+    blk = rotation_block(rotation)
+    L = _lib.load()
+    need = L.rq_fused_decode_workspace_bytes(num_seqs, H_Q, head_dim, max_seq_len)
+    ws = workspace if workspace is not None and workspace.numel() >= need else _workspace(dev, need)
+    R = _f32(rotation, dev)
+    kc, vc = _f32(centroids_k, dev), _f32(centroids_v, dev)
+    sl = seq_lens.contiguous()
+    rc = L.rq_fused_decode(
+        q.data_ptr(), _lib.dtype_code(q.dtype), num_seqs, H_Q, q.stride(0), q.stride(1), kv_cache.data_ptr(),
+        kv_cache.shape[0], block_size, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
+        block_table.data_ptr(), MB, block_table.stride(0), sl.data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(),
+        vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0),
+        out.stride(1), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_fused_decode")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# INT8 prefill
+# ---------------------------------------------------------------------------
+
+def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                                seq_lens: torch.Tensor, k_centroids: torch.Tensor, v_centroids: torch.Tensor,
+                                rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
+                                sm_scale: float | None = None, out: torch.Tensor | None = None,
+                                cu_seqlens_q: torch.Tensor | None = None,
+                                max_q_len: int | None = None) -> torch.Tensor:
+    """Causal prefill attention from the packed cache with Q K^T and P V on int8 MFMA.
+
+    Reference: src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:247-363.
+    q: (num_tokens, H_Q, D); block_table (num_seqs, max_blocks) int32; seq_lens
+    (num_seqs,) int32 total context lengths (new tokens included).
+    cu_seqlens_q (num_seqs + 1,) int32 splits q among sequences; without it
+    there must be one sequence (as in the reference).
+    """
+    num_tokens, H_Q, D = q.shape
+    assert D == head_dim
+    assert H_Q % num_kv_heads == 0
+    assert kv_cache.dtype == torch.uint8
+    assert block_table.dtype == torch.int32
+    assert seq_lens.dtype == torch.int32
+    if cu_seqlens_q is None:
+        if seq_lens.numel() != 1:
+            raise ValueError(
+                f"fused_paged_rq_int8_prefill supports only a single sequence, "
+                f"but got seq_lens.numel() == {seq_lens.numel()}.")
+        cu_seqlens_q = torch.tensor([0, num_tokens], dtype=torch.int32, device=q.device)
+        max_q_len = num_tokens
+    dev = _require_device(q, kv_cache, block_table, seq_lens, cu_seqlens_q)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    bt = block_table if block_table.dim() == 2 else block_table.reshape(1, -1)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    num_seqs = seq_lens.numel()
+    if max_q_len is None:
+        max_q_len = num_tokens
+    blk = rotation_block(rotation)
+    R = _f32(rotation, dev)
+    kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
+    cu = cu_seqlens_q.to(torch.int32).contiguous()
+    rc = _lib.load().rq_int8_prefill(
+        q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
+        num_seqs, max_q_len, kv_cache.data_ptr(), kv_cache.shape[0], block_size, kv_cache.stride(0),
+        kv_cache.stride(1), num_kv_heads, head_dim, bt.data_ptr(), bt.shape[1], bt.stride(0),
+        seq_lens.contiguous().data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(), blk,
+        float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_int8_prefill")
+    return out

@@ -1,0 +1,560 @@
+"""RotorQuant compressed-KV attention backend for vLLM, on gfx950 HIP kernels.
+
+Drop-in for the reference plugin (src/rotorquant_vllm/vllm/rq_backend.py): same
+registration (`register_rq_backend`, the CUSTOM backend), the same RQ_* env
+configuration, the same packed uint8 (num_blocks, block_size, total_bytes)
+cache with per-token slots
+
+    [K idx (H x D/2) | K norms (H x fp32) | V idx | V norms | zero pad to H * next_pow2(D + 8)]
+
+and the same class / attribute names, so the reference's fake-based dispatch
+tests run unchanged against it.  The hot path underneath is the C ABI of
+librq_hip.so (include/rq_abi.h):
+
+    compress + store  -> rq_compress_store   (one fused K+V launch, writes slots)
+    decode            -> rq_fused_decode     (Q and output rotation inside)
+    prefill           -> rq_int8_prefill     (int8 MFMA, multi-sequence)
+    non-fused path    -> rq_paged_decompress + fp32 attention
+
+vLLM itself is imported lazily: without vLLM the module still imports (the
+classes then derive from small local stand-ins), which is how the tests run.
+"""
+from __future__ import annotations
+
+import enum
+import logging
+import os
+from dataclasses import dataclass
+from dataclasses import fields as dc_fields
+
+import torch
+
+from rotorquant_vllm.quantization.isoquant import IsoQuantMSE
+from rotorquant_vllm.quantization.planarquant import PlanarQuantMSE
+
+logger = logging.getLogger(__name__)
+
+# ---------------------------------------------------------------------------
+# Constants (reference: rq_backend.py:51-54)
+# ---------------------------------------------------------------------------
+
+RQ_DEFAULT_BITS = 3
+RQ_DEFAULT_MODE = "iso"
+RQ_SEED = 42
+RQ_NORM_BYTES = 4
+
+# ---------------------------------------------------------------------------
+# Env parsing (reference: rq_backend.py:62-109, :140-148); same messages
+# ---------------------------------------------------------------------------
+
+
+def _parse_rq_mode() -> str:
+    mode = os.environ.get("RQ_MODE", RQ_DEFAULT_MODE).lower()
+    if mode not in ("iso", "planar"):
+        raise ValueError(f"RQ_MODE must be 'iso' or 'planar', got '{mode}'")
+    return mode
+
+
+def _parse_rq_bits() -> int:
+    bits = int(os.environ.get("RQ_BITS", str(RQ_DEFAULT_BITS)))
+    if bits not in (3, 4):
+        raise ValueError(f"RQ_BITS must be 3 or 4, got '{bits}'")
+    return bits
+
+
+def _parse_kv_bits() -> tuple[int, int]:
+    default = _parse_rq_bits()
+    k_raw, v_raw = os.environ.get("RQ_K_BITS"), os.environ.get("RQ_V_BITS")
+    k_bits = int(k_raw) if k_raw else default
+    v_bits = int(v_raw) if v_raw else default
+    if k_bits not in (3, 4):
+        raise ValueError(f"RQ_K_BITS must be 3 or 4, got '{k_bits}'")
+    if v_bits not in (3, 4):
+        raise ValueError(f"RQ_V_BITS must be 3 or 4, got '{v_bits}'")
+    return k_bits, v_bits
+
+
+def _parse_iso_mode() -> str:
+    mode = os.environ.get("RQ_ISO_MODE", "fast").lower()
+    if mode not in ("fast", "full"):
+        raise ValueError(f"RQ_ISO_MODE must be 'fast' or 'full', got '{mode}'")
+    return mode
+
+
+def _parse_rq_fused_paged_env() -> bool:
+    return os.environ.get("RQ_USE_FUSED_PAGED", "").lower() in ("1", "true", "yes")
+
+
+# ---------------------------------------------------------------------------
+# Kernel feature gates (reference: rq_backend.py:118-138): on if librq_hip.so loads
+# ---------------------------------------------------------------------------
+
+_fused_paged_kernel_available = False
+_fused_prefill_kernel_available = False
+_fused_paged_rq_decode_fn = None
+_fused_paged_rq_int8_prefill_fn = None
+_compress_store_fn = None
+_paged_decompress_fn = None
+try:
+    from rotorquant_vllm import _lib as _rq_lib
+    from rotorquant_vllm.kernels import compress_store as _compress_store_fn
+    from rotorquant_vllm.kernels import fused_paged_rq_decode as _fused_paged_rq_decode_fn
+    from rotorquant_vllm.kernels import fused_paged_rq_int8_prefill as _fused_paged_rq_int8_prefill_fn
+    from rotorquant_vllm.kernels import paged_decompress as _paged_decompress_fn
+
+    _rq_lib.load()
+    _fused_paged_kernel_available = True
+    _fused_prefill_kernel_available = True
+except (ImportError, OSError, RuntimeError) as exc:
+    logger.info("RotorQuant HIP kernels unavailable: %s", exc)
+
+# ---------------------------------------------------------------------------
+# Cache size helpers (reference: rq_backend.py:155-188)
+# ---------------------------------------------------------------------------
+
+
+def _next_power_of_2(n: int) -> int:
+    return 1 << (n - 1).bit_length() if n > 0 else 1
+
+
+def _rq_bytes_per_component(head_dim: int, num_kv_heads: int) -> int:
+    """Nibble-packed indices (head_dim / 2 bytes) plus one fp32 norm, per head."""
+    return num_kv_heads * (head_dim // 2) + num_kv_heads * RQ_NORM_BYTES
+
+
+def _rq_bytes_per_token_kv(head_dim: int, num_kv_heads: int) -> int:
+    """K + V payload per token (1088 B for 8 heads of 128)."""
+    return 2 * _rq_bytes_per_component(head_dim, num_kv_heads)
+
+
+def _rq_padded_slot_bytes(head_dim: int) -> int:
+    """Per-head slot share, padded to a power of two (256 B for head_dim 128)."""
+    return _next_power_of_2(_rq_bytes_per_token_kv(head_dim, 1))
+
+
+def _rq_total_bytes(head_dim: int, num_kv_heads: int) -> int:
+    return num_kv_heads * _rq_padded_slot_bytes(head_dim)
+
+
+# ---------------------------------------------------------------------------
+# Rotation matrices (reference: rq_backend.py:194-264)
+# ---------------------------------------------------------------------------
+
+
+def _quat_left(w, x, y, z) -> torch.Tensor:
+    """Matrix of v -> q v (Hamilton product, [w, x, y, z] order)."""
+    return torch.tensor([[w, -x, -y, -z],
+                         [x, w, -z, y],
+                         [y, z, w, -x],
+                         [z, -y, x, w]], dtype=torch.float32)
+
+
+def _quat_right_conj(w, x, y, z) -> torch.Tensor:
+    """Matrix of v -> v conj(q)."""
+    return torch.tensor([[w, x, y, z],
+                         [-x, w, -z, y],
+                         [-y, z, w, -x],
+                         [-z, -y, x, w]], dtype=torch.float32)
+
+
+def _build_iso_R(quantizer, d: int, device, mode: str = "fast") -> torch.Tensor:
+    """Block-diagonal R with 4x4 blocks: 'fast' v -> q_L v conj(q_L), 'full' v -> q_L v conj(q_R).
+
+    The fp32 4x4 block products are formed on the CPU (init-time, 32 blocks)
+    and R is then moved to `device`.
+    """
+    qL = quantizer.q_L.detach().float().cpu()
+    qR = quantizer.q_R.detach().float().cpu() if mode == "full" else qL
+    D_pad = quantizer.d_padded
+    R = torch.eye(D_pad, dtype=torch.float32)
+    for g in range(quantizer.n_groups):
+        lw, lx, ly, lz = (float(v) for v in qL[g])
+        rw, rx, ry, rz = (float(v) for v in qR[g])
+        R[4 * g:4 * g + 4, 4 * g:4 * g + 4] = _quat_left(lw, lx, ly, lz) @ _quat_right_conj(rw, rx, ry, rz)
+    return R[:d, :d].contiguous().to(device)
+
+
+def _build_planar_R(quantizer, d: int, device) -> torch.Tensor:
+    """Block-diagonal R with 2x2 Givens blocks [[c, -s], [s, c]]."""
+    cs = quantizer.rot2.detach().float().cpu()
+    R = torch.eye(quantizer.d_padded, dtype=torch.float32)
+    for g in range(quantizer.n_groups):
+        c, s = float(cs[g, 0]), float(cs[g, 1])
+        R[2 * g:2 * g + 2, 2 * g:2 * g + 2] = torch.tensor([[c, -s], [s, c]], dtype=torch.float32)
+    return R[:d, :d].contiguous().to(device)
+
+
+def _build_rotation_matrix(quantizer, d: int, device) -> torch.Tensor:
+    if hasattr(quantizer, "q_L"):
+        return _build_iso_R(quantizer, d, device, getattr(quantizer, "mode", "fast"))
+    return _build_planar_R(quantizer, d, device)
+
+
+# ---------------------------------------------------------------------------
+# vLLM base classes (lazy; local stand-ins when vLLM is absent)
+# ---------------------------------------------------------------------------
+
+
+class _AttentionTypeStandIn(str, enum.Enum):
+    DECODER = "decoder"
+    ENCODER = "encoder"
+    ENCODER_ONLY = "encoder_only"
+    ENCODER_DECODER = "encoder_decoder"
+
+
+class _CGSupportStandIn(enum.Enum):
+    NEVER = 0
+    UNIFORM_SINGLE_TOKEN_DECODE = 1
+    UNIFORM_BATCH = 2
+    ALWAYS = 3
+
+
+class _BackendStandIn:
+    pass
+
+
+class _ImplStandIn:
+    def __init__(self, num_heads, head_size, scale, num_kv_heads=None, alibi_slopes=None, sliding_window=None,
+                 kv_cache_dtype="auto", logits_soft_cap=None, attn_type=_AttentionTypeStandIn.DECODER,
+                 *args, **kwargs):
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else num_heads
+        self.alibi_slopes = alibi_slopes
+        self.sliding_window = sliding_window
+        self.kv_cache_dtype = kv_cache_dtype
+        self.logits_soft_cap = logits_soft_cap
+        self.attn_type = attn_type
+
+
+class _BuilderStandIn:
+    pass
+
+
+@dataclass(frozen=True, kw_only=True)
+class _FullAttentionSpecStandIn:
+    block_size: int
+    num_kv_heads: int
+    head_size: int
+    dtype: torch.dtype
+
+
+def _import_vllm_bases():
+    """Best available vLLM base classes: FlashAttention* (as the reference), ROCm's, or stand-ins."""
+    try:
+        from vllm.v1.attention.backend import AttentionCGSupport, AttentionType
+    except Exception:  # noqa: BLE001  (vLLM absent or incompatible)
+        return (_BackendStandIn, _ImplStandIn, _BuilderStandIn, _FullAttentionSpecStandIn,
+                _CGSupportStandIn, _AttentionTypeStandIn, False)
+    try:
+        from vllm.v1.kv_cache_interface import FullAttentionSpec
+    except Exception:  # noqa: BLE001
+        FullAttentionSpec = _FullAttentionSpecStandIn
+    for mod, names in (("vllm.v1.attention.backends.flash_attn",
+                        ("FlashAttentionBackend", "FlashAttentionImpl", "FlashAttentionMetadataBuilder")),
+                       ("vllm.v1.attention.backends.rocm_attn",
+                        ("RocmAttentionBackend", "RocmAttentionImpl", "RocmAttentionMetadataBuilder")),
+                       ("vllm.v1.attention.backends.triton_attn",
+                        ("TritonAttentionBackend", "TritonAttentionImpl", "TritonAttentionMetadataBuilder"))):
+        try:
+            m = __import__(mod, fromlist=list(names))
+            return (getattr(m, names[0]), getattr(m, names[1]), getattr(m, names[2]), FullAttentionSpec,
+                    AttentionCGSupport, AttentionType, True)
+        except Exception:  # noqa: BLE001
+            continue
+    return (_BackendStandIn, _ImplStandIn, _BuilderStandIn, FullAttentionSpec, AttentionCGSupport, AttentionType,
+            True)
+
+
+(_BackendBase, _ImplBase, _BuilderBase, FullAttentionSpec, AttentionCGSupport, AttentionType,
+ _HAVE_VLLM) = _import_vllm_bases()
+
+# ---------------------------------------------------------------------------
+# KV cache spec (reference: rq_backend.py:272-283)
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True, kw_only=True)
+class RQFullAttentionSpec(FullAttentionSpec):
+    """Full-attention KV spec whose pages hold the packed RotorQuant slots (uint8)."""
+
+    @property
+    def real_page_size_bytes(self) -> int:  # noqa: D102
+        return self.block_size * _rq_total_bytes(self.head_size, self.num_kv_heads)
+
+
+# ---------------------------------------------------------------------------
+# Metadata builder (reference: rq_backend.py:291-313)
+# ---------------------------------------------------------------------------
+
+
+class RQMetadataBuilder(_BuilderBase):
+    """Builder of the parent backend; CUDA/HIP-graph support only with the fused kernels."""
+
+    @classmethod
+    def get_cudagraph_support(cls, vllm_config: object, kv_cache_spec: object):
+        if _fused_paged_kernel_available and _parse_rq_fused_paged_env():
+            return AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE
+        return AttentionCGSupport.NEVER
+
+
+# ---------------------------------------------------------------------------
+# Backend (reference: rq_backend.py:322-371)
+# ---------------------------------------------------------------------------
+
+
+class RQAttentionBackend(_BackendBase):
+    """RotorQuant compressed-KV attention backend, registered as CUSTOM."""
+
+    forward_includes_kv_cache_update = True
+
+    @classmethod
+    def supports_mm_prefix(cls) -> bool:
+        return True
+
+    @staticmethod
+    def get_name() -> str:
+        return "CUSTOM"
+
+    @staticmethod
+    def get_impl_cls():
+        return RQAttentionImpl
+
+    @staticmethod
+    def get_builder_cls():
+        return RQMetadataBuilder
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                           cache_dtype_str: str = "auto") -> tuple[int, ...]:
+        """(num_blocks, block_size, total_bytes) uint8."""
+        return (num_blocks, block_size, _rq_total_bytes(head_size, num_kv_heads))
+
+    @staticmethod
+    def get_kv_cache_stride_order(include_num_layers_dimension: bool = False) -> tuple[int, ...]:
+        """Raises so vLLM falls back to the identity layout."""
+        raise NotImplementedError
+
+
+# ---------------------------------------------------------------------------
+# Attention implementation (reference: rq_backend.py:379-1036)
+# ---------------------------------------------------------------------------
+
+
+class RQAttentionImpl(_ImplBase):
+    """compress -> store -> fused decode / int8 prefill (or paged decompress + attention)."""
+
+    def __init__(self, *args, **kwargs) -> None:
+        super().__init__(*args, **kwargs)
+        head_size = self.head_size
+        num_kv_heads = self.num_kv_heads
+        rq_mode = _parse_rq_mode()
+        iso_mode = _parse_iso_mode()
+        k_bits, v_bits = _parse_kv_bits()
+        self._k_bits, self._v_bits, self._rq_mode = k_bits, v_bits, rq_mode
+
+        vllm_config = None
+        if _HAVE_VLLM:
+            try:
+                from vllm.config import get_current_vllm_config_or_none
+                vllm_config = get_current_vllm_config_or_none()
+            except Exception:  # noqa: BLE001
+                vllm_config = None
+        device = vllm_config.device_config.device if vllm_config is not None else torch.device("cpu")
+
+        if rq_mode == "iso":
+            kq = IsoQuantMSE(head_size, k_bits, seed=RQ_SEED, mode=iso_mode, device=device)
+            vq = kq if v_bits == k_bits else IsoQuantMSE(head_size, v_bits, seed=RQ_SEED, mode=iso_mode,
+                                                         device=device)
+        else:
+            kq = PlanarQuantMSE(head_size, k_bits, seed=RQ_SEED, device=device)
+            vq = kq if v_bits == k_bits else PlanarQuantMSE(head_size, v_bits, seed=RQ_SEED, device=device)
+        self._k_quantizer, self._v_quantizer = kq, vq
+
+        # One R (from the K quantizer) serves K and V (reference :472-480).
+        R = _build_rotation_matrix(kq, head_size, device)
+        self._rq_rot = R
+        self._rq_rot_T = R.T.contiguous()
+        self._rq_rot_T_even = self._rq_rot_T[:, 0::2].contiguous()
+        self._rq_rot_T_odd = self._rq_rot_T[:, 1::2].contiguous()
+        self._rq_rot_block = 4 if rq_mode == "iso" else 2
+        self._half_d = head_size // 2
+
+        self._k_idx_end = num_kv_heads * self._half_d
+        self._k_norm_end = self._k_idx_end + num_kv_heads * RQ_NORM_BYTES
+        self._v_idx_end = self._k_norm_end + num_kv_heads * self._half_d
+        self._v_norm_end = self._v_idx_end + num_kv_heads * RQ_NORM_BYTES
+        self._total_bytes = _rq_total_bytes(head_size, num_kv_heads)
+
+        self._cg_buffers_ready = False
+        self._max_model_len = vllm_config.model_config.max_model_len if vllm_config is not None else 8192
+        self._max_prefill_len = (vllm_config.scheduler_config.max_num_batched_tokens
+                                 if vllm_config is not None else 2048)
+        self._fused_paged_available = _parse_rq_fused_paged_env() and _fused_paged_kernel_available
+        self._fused_prefill_available = _parse_rq_fused_paged_env() and _fused_prefill_kernel_available
+
+        fp16_total = 2 * num_kv_heads * head_size * 2
+        logger.info("RQAttentionImpl: %s mode, %d KV heads, head_size=%d, k_bits=%d, v_bits=%d, "
+                    "%d bytes/token (%.2fx compression vs FP16)", rq_mode, num_kv_heads, head_size, k_bits,
+                    v_bits, self._total_bytes, fp16_total / self._total_bytes)
+        logger.info("Fused paged RQ decode: %s; fused paged RQ int8 prefill: %s",
+                    "enabled" if self._fused_paged_available else "disabled",
+                    "enabled" if self._fused_prefill_available else "disabled")
+
+    # -- scratch -----------------------------------------------------------
+
+    def _init_cg_buffers(self, kv_cache, compute_dtype):
+        """Device-side tensors used by every launch (codebooks, rotation splits, scratch)."""
+        dev = kv_cache.device
+        self._dev_kc = self._k_quantizer.centroids.to(dev, torch.float32).contiguous()
+        self._dev_vc = self._v_quantizer.centroids.to(dev, torch.float32).contiguous()
+        self._dev_kb = self._k_quantizer.boundaries.to(dev, torch.float32).contiguous()
+        self._dev_vb = self._v_quantizer.boundaries.to(dev, torch.float32).contiguous()
+        self._dev_R = self._rq_rot.to(dev, torch.float32).contiguous()
+        self._dev_rte = self._rq_rot_T_even.to(dev).contiguous()
+        self._dev_rto = self._rq_rot_T_odd.to(dev).contiguous()
+        self._decode_ws = None
+        self._cg_buffers_ready = True
+
+    # -- compress + store ----------------------------------------------------
+
+    def _compress_and_store(self, key, value, kv_cache, slot_mapping, compress_out=None, row_out=None) -> None:
+        """Fused K+V compress written straight into the slots (rq_backend.py:585-657)."""
+        if _compress_store_fn is None:
+            raise RuntimeError("RotorQuant HIP kernels are not available")
+        n = slot_mapping.shape[0]
+        _compress_store_fn(key[:n], value[:n], kv_cache, slot_mapping, self._dev_rte, self._dev_rto,
+                           self._dev_kb, self._dev_vb, rot_block=self._rq_rot_block)
+
+    # -- non-fused path -----------------------------------------------------------
+
+    def _forward_unfused(self, query, kv_cache, md, output, num_actual_tokens):
+        """Paged decompress + fp32 attention in rotated space (replaces the FA call, :937-1036)."""
+        BS = kv_cache.shape[1]
+        H, D = self.num_kv_heads, self.head_size
+        q = query[:num_actual_tokens]
+        q_rot = (q.float() @ self._dev_R.T).to(q.dtype).float()
+        k_cache, v_cache, bt, _ = _paged_decompress_fn(kv_cache, md.block_table, md.seq_lens, H, D, self._dev_kc,
+                                                       self._dev_vc, torch.float32)
+        qsl = getattr(md, "query_start_loc", None)
+        seq_lens = md.seq_lens.tolist()
+        starts = qsl.tolist() if qsl is not None else [0, num_actual_tokens]
+        bt_host = bt.cpu()
+        G = self.num_heads // H if hasattr(self, "num_heads") else q.shape[1] // H
+        out_rot = torch.zeros(num_actual_tokens, q.shape[1], D, dtype=torch.float32, device=q.device)
+        for b, L in enumerate(seq_lens):
+            s0, s1 = starts[b], starts[b + 1]
+            if s1 <= s0 or L == 0:
+                continue
+            nblk = (L + BS - 1) // BS
+            ids = bt_host[b, :nblk].to(q.device).long()
+            K = k_cache[ids].reshape(-1, H, D)[:L]
+            V = v_cache[ids].reshape(-1, H, D)[:L]
+            K = K.repeat_interleave(G, dim=1).transpose(0, 1).contiguous()  # (HQ, L, D)
+            V = V.repeat_interleave(G, dim=1).transpose(0, 1).contiguous()
+            Q = q_rot[s0:s1].transpose(0, 1).contiguous()  # (HQ, T, D)
+            S = torch.matmul(Q, K.transpose(1, 2).contiguous()) * self.scale
+            T = s1 - s0
+            pos = L - T + torch.arange(T, device=q.device)
+            S = S.masked_fill(torch.arange(L, device=q.device)[None, None, :] > pos[None, :, None], float("-inf"))
+            P = torch.softmax(S, dim=-1)
+            out_rot[s0:s1] = torch.matmul(P, V).transpose(0, 1)
+        out_rot = out_rot.to(q.dtype).float()
+        output[:num_actual_tokens] = (out_rot @ self._dev_R).to(output.dtype)
+        return output
+
+    # -- forward -------------------------------------------------------------
+
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
+                output_block_scale=None):
+        """compress/store new K/V, then attention from the packed cache."""
+        assert output is not None, "Output tensor must be provided."
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("Fused output quantization is not supported with RotorQuant backend")
+        if attn_metadata is None or kv_cache is None:
+            return output.zero_()
+        if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
+            n = attn_metadata.num_actual_tokens
+            return self._forward_encoder_attention(query[:n], key[:n], value[:n], output[:n], attn_metadata, layer)
+
+        num_actual_tokens = attn_metadata.num_actual_tokens
+        max_query_len = getattr(attn_metadata, "max_query_len", None)
+        # A single token (reference :904), or a uniform batch of single-token decodes.
+        is_decode = num_actual_tokens == 1 or max_query_len == 1
+        if not self._cg_buffers_ready:
+            self._init_cg_buffers(kv_cache, query.dtype)
+        if key is not None and value is not None:
+            self._compress_and_store(key, value, kv_cache, attn_metadata.slot_mapping)
+
+        if is_decode and self._fused_paged_available:
+            n = num_actual_tokens
+            _fused_paged_rq_decode_fn(query[:n], kv_cache, attn_metadata.block_table, attn_metadata.seq_lens,
+                                      self._k_quantizer.centroids, self._v_quantizer.centroids, self._rq_rot,
+                                      self.num_kv_heads, self.head_size, kv_cache.shape[1], sm_scale=self.scale,
+                                      out=output[:n])
+            return output
+
+        if (not is_decode and self._fused_prefill_available
+                and not getattr(attn_metadata, "use_cascade", False)):
+            if attn_metadata.seq_lens.numel() == 1:
+                _fused_paged_rq_int8_prefill_fn(query[:num_actual_tokens], kv_cache, attn_metadata.block_table,
+                                                attn_metadata.seq_lens, self._k_quantizer.centroids,
+                                                self._v_quantizer.centroids, self._rq_rot, self.num_kv_heads,
+                                                self.head_size, kv_cache.shape[1], sm_scale=self.scale,
+                                                out=output[:num_actual_tokens])
+            else:
+                _fused_paged_rq_int8_prefill_fn(query[:num_actual_tokens], kv_cache, attn_metadata.block_table,
+                                                attn_metadata.seq_lens, self._k_quantizer.centroids,
+                                                self._v_quantizer.centroids, self._rq_rot, self.num_kv_heads,
+                                                self.head_size, kv_cache.shape[1], sm_scale=self.scale,
+                                                out=output[:num_actual_tokens],
+                                                cu_seqlens_q=attn_metadata.query_start_loc,
+                                                max_q_len=max_query_len)
+            return output
+
+        if getattr(attn_metadata, "use_cascade", False):
+            raise NotImplementedError("RQ does not yet support cascade attention")
+        return self._forward_unfused(query, kv_cache, attn_metadata, output, num_actual_tokens)
+
+
+# ---------------------------------------------------------------------------
+# Registration (reference: rq_backend.py:1043-1093)
+# ---------------------------------------------------------------------------
+
+_original_get_kv_cache_spec = None
+
+
+def register_rq_backend() -> None:
+    """Register RotorQuant as vLLM's CUSTOM attention backend and make decoder
+    attention layers report RQFullAttentionSpec (uint8 pages sized for the packed slots)."""
+    global _original_get_kv_cache_spec
+    from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_backend
+
+    register_backend(AttentionBackendEnum.CUSTOM, "rotorquant_vllm.vllm.rq_backend.RQAttentionBackend")
+
+    from vllm.v1.core.single_type_kv_cache_manager import spec_manager_map
+
+    if RQFullAttentionSpec not in spec_manager_map:
+        spec_manager_map[RQFullAttentionSpec] = spec_manager_map[FullAttentionSpec]
+
+    from vllm.model_executor.layers.attention.attention import Attention
+
+    if _original_get_kv_cache_spec is None:
+        _original_get_kv_cache_spec = Attention.get_kv_cache_spec
+    original = _original_get_kv_cache_spec
+
+    def _rq_get_kv_cache_spec(self, vllm_config):
+        spec = original(self, vllm_config)
+        if isinstance(spec, FullAttentionSpec) and not isinstance(spec, RQFullAttentionSpec):
+            kwargs = {f.name: getattr(spec, f.name) for f in dc_fields(spec)}
+            kwargs["dtype"] = torch.uint8
+            return RQFullAttentionSpec(**kwargs)
+        return spec
+
+    Attention.get_kv_cache_spec = _rq_get_kv_cache_spec
+    logger.info("RQ attention backend registered as CUSTOM (compressed cache)")
+
+
+__all__ = ["RQAttentionBackend", "RQAttentionImpl", "RQMetadataBuilder", "RQFullAttentionSpec",
+           "register_rq_backend"]

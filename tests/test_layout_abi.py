@@ -1,0 +1,108 @@
+"""Layout KATs of the reference, env parsing, and the C ABI surface (no GPU)."""
+import os
+import re
+
+import pytest
+import torch
+
+from rotorquant_vllm import _lib
+from rotorquant_vllm.vllm import rq_backend as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+class TestCacheLayout:
+    """Reference KATs: tests/test_vllm_integration.py:44-62, tests/test_benchmarks.py:144-156."""
+
+    def test_nibble_packed_size(self):
+        assert B._rq_bytes_per_token_kv(128, 8) == 1088
+        assert B._rq_padded_slot_bytes(128) == 256
+        assert 8 * B._rq_padded_slot_bytes(128) == 2048
+
+    def test_cache_shape(self):
+        assert B.RQAttentionBackend.get_kv_cache_shape(100, 16, 8, 128) == (100, 16, 2048)
+        assert B.RQAttentionBackend.get_kv_cache_shape(7, 16, 4, 128) == (7, 16, 1024)
+
+    def test_page_size(self):
+        spec = B.RQFullAttentionSpec(block_size=16, num_kv_heads=8, head_size=128, dtype=torch.uint8)
+        assert spec.real_page_size_bytes == 32768
+
+    def test_compression_ratio(self):
+        r = 8 * 128 * 2 * 2 / B._rq_bytes_per_token_kv(128, 8)
+        assert 3.5 < r < 4.0
+
+    def test_oracle_layout_agrees(self):
+        import oracle as O
+        lay = O.slot_layout(8, 128)
+        assert lay == dict(k_idx_end=512, k_norm_end=544, v_idx_end=1056, v_norm_end=1088, total_bytes=2048)
+
+
+class TestEnv:
+    def test_defaults(self, monkeypatch):
+        for k in ("RQ_MODE", "RQ_BITS", "RQ_K_BITS", "RQ_V_BITS", "RQ_ISO_MODE", "RQ_USE_FUSED_PAGED"):
+            monkeypatch.delenv(k, raising=False)
+        assert B._parse_rq_mode() == "iso" and B._parse_iso_mode() == "fast"
+        assert B._parse_kv_bits() == (3, 3) and B._parse_rq_fused_paged_env() is False
+
+    def test_overrides(self, monkeypatch):
+        monkeypatch.setenv("RQ_MODE", "PLANAR")
+        monkeypatch.setenv("RQ_BITS", "4")
+        monkeypatch.setenv("RQ_V_BITS", "3")
+        monkeypatch.setenv("RQ_K_BITS", "")
+        monkeypatch.setenv("RQ_USE_FUSED_PAGED", "Yes")
+        assert B._parse_rq_mode() == "planar" and B._parse_kv_bits() == (4, 3)
+        assert B._parse_rq_fused_paged_env() is True
+
+    @pytest.mark.parametrize("var,val,msg", [
+        ("RQ_MODE", "turbo", "RQ_MODE must be 'iso' or 'planar', got 'turbo'"),
+        ("RQ_BITS", "2", "RQ_BITS must be 3 or 4, got '2'"),
+        ("RQ_K_BITS", "5", "RQ_K_BITS must be 3 or 4, got '5'"),
+        ("RQ_V_BITS", "8", "RQ_V_BITS must be 3 or 4, got '8'"),
+        ("RQ_ISO_MODE", "slow", "RQ_ISO_MODE must be 'fast' or 'full', got 'slow'"),
+    ])
+    def test_invalid_values_raise(self, monkeypatch, var, val, msg):
+        monkeypatch.setenv(var, val)
+        fn = {"RQ_MODE": B._parse_rq_mode, "RQ_BITS": B._parse_rq_bits, "RQ_K_BITS": B._parse_kv_bits,
+              "RQ_V_BITS": B._parse_kv_bits, "RQ_ISO_MODE": B._parse_iso_mode}[var]
+        with pytest.raises(ValueError, match=re.escape(msg)):
+            fn()
+
+
+def _header_symbols():
+    txt = open(os.path.join(ROOT, "include", "rq_abi.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char \*)\s*(rq_\w+)\(", txt, re.M)))
+
+
+class TestABI:
+    def test_library_exports_every_declared_symbol(self):
+        lib = _lib.load()
+        syms = _header_symbols()
+        assert len(syms) >= 10
+        for s in syms:
+            assert hasattr(lib, s), s
+        assert set(syms) == set(_lib.EXPORTED)
+
+    def test_version(self):
+        assert _lib.load().rq_abi_version() == 1
+
+    def test_argument_validation_without_gpu(self):
+        """Bad arguments are rejected before any device work, with a message."""
+        lib = _lib.load()
+        rc = lib.rq_compress(None, 7, 1, 128, None, None, 4, None, 7, None, None, None)
+        assert rc == 1 and b"dtype" in lib.rq_last_error()
+        rc = lib.rq_compress(None, 0, 1, 100, None, None, 4, None, 7, None, None, None)
+        assert rc == 1 and b"head_dim" in lib.rq_last_error()
+        rc = lib.rq_fused_decode(None, 1, 1, 32, 0, 0, None, 1, 16, 0, 0, 8, 64, None, 1, 1, None, 16, None, 8, None,
+                                 8, None, 4, 0.1, None, 0, 0, None, 0, None)
+        assert rc == 1 and b"head_dim" in lib.rq_last_error()
+        rc = lib.rq_fused_decode(None, 1, 1, 40, 0, 0, None, 1, 16, 0, 0, 2, 128, None, 1, 1, None, 16, None, 8,
+                                 None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
+        assert rc == 1 and b"integer <= 16" in lib.rq_last_error()
+        with pytest.raises(ValueError):
+            _lib.check(1, "x")
+
+    def test_kernels_reject_cpu_tensors(self):
+        from rotorquant_vllm import kernels as K
+        with pytest.raises(RuntimeError, match="no CPU path"):
+            K.iso_decompress(torch.zeros(1, 1, 64, dtype=torch.uint8), torch.ones(1, 1, 1), torch.zeros(8),
+                             torch.float16)
