@@ -162,7 +162,10 @@ int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, int32_t blo
  * of rot_block (2 or 4).  head_dim must be 128; num_q_heads / num_kv_heads
  * must be an integer <= 16; n_k_centroids / n_v_centroids 8 or 16.
  * max_seq_len bounds every seq_lens entry (it sizes the split-KV grid).
- * workspace: rq_fused_decode_workspace_bytes(...) bytes of scratch.
+ * workspace: rq_fused_decode_workspace_bytes(...) bytes of scratch, zero-filled
+ * before its first use; each call leaves its per-sequence counters at zero
+ * again, so the same workspace serves later calls (calls sharing one
+ * workspace must not overlap).  One kernel launch per call.
  */
 int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num_q_heads,
                                         int32_t head_dim, int64_t max_seq_len);

@@ -50,12 +50,22 @@ inline int32_t next_pow2_i32(int32_t n) {
 // ---------------------------------------------------------------------------
 // Scalar conversions (round to nearest even)
 // ---------------------------------------------------------------------------
+
+// Hides a value from the optimiser (no instruction emitted).  Used where an
+// fp32 product must be rounded to fp32 before a 16-bit cast: without it the
+// backend folds multiply + cast into one v_fma_mix with a +0 addend, which
+// rounds once instead of twice and turns -0 into +0.
+__device__ __forceinline__ float opaque(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    // gfx950 converts with v_cvt_pk_bf16_f32 (round to nearest even).
+    __bf16 b = (__bf16)f;
+    uint16_t s;
+    __builtin_memcpy(&s, &b, 2);
+    return s;
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
     _Float16 h;

@@ -36,8 +36,8 @@ __device__ __forceinline__ void unpack8(uint32_t word, const float *cb, float no
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint32_t byte = (word >> (8 * i)) & 0xffu;
-        v[2 * i] = cb[byte >> 4] * norm;
-        v[2 * i + 1] = cb[byte & 15u] * norm;
+        v[2 * i] = opaque(cb[byte >> 4] * norm);
+        v[2 * i + 1] = opaque(cb[byte & 15u] * norm);
     }
 }
 

@@ -1,11 +1,494 @@
-// INT8-MFMA causal prefill over the packed cache (placeholder until the kernel lands).
+// Causal prefill attention over the packed RotorQuant cache on int8 MFMA (gfx950).
+//
+// Replaces fused_paged_rq_int8_prefill
+// (src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:247-363, kernel :43-239):
+// attention in the rotated space, q_rot = q R^T rounded to the q dtype, output
+// rounded and rotated back by R.  Differences from the reference, on purpose:
+//   * any number of sequences per launch (cu_seqlens_q), and query i of a
+//     sequence sits at position seq_len - q_len + i (chunked prefill with a
+//     cached prefix is causal-correct; the reference places it at i);
+//   * key tiles entirely above the causal diagonal are skipped;
+//   * int8 operands are rounded to nearest and carry a second int8 "low" part
+//     where one int8 is too coarse for the 2e-2 output tolerance:
+//       Q K^T = s_q s_k [q_hi.k_hi + (q_hi.k_lo + q_lo.k_hi) / 128]   (3 MFMAs)
+//       P V   = s_w s_v [w_hi.v_hi + (w_hi.v_lo + w_lo.v_hi) / 128]   (3 MFMAs)
+//     q per query row (absmax / 127); k, v from per-codebook index -> int8
+//     byte tables (centroid * 127 / max|centroid| and the residual * 128)
+//     with the per-token scale norm * max|centroid| / 127; w = p * v_norm
+//     per 64-key tile scaled by the tile's largest v norm.
+//
+// Work split: one workgroup per (query block of QB positions, kv head,
+// sequence).  Its waves are (query head of the GQA group, 16-position group);
+// each 64-key tile of K/V is decoded once into LDS (int8) and shared by all of
+// them.  MFMA v_mfma_i32_16x16x64_i8 (wave64, lane l, g = l / 16):
+//   A (16 x 64): lane holds row l % 16, k = 16g .. 16g+15 (16 bytes)
+//   B (64 x 16): lane holds col l % 16, k = 16g .. 16g+15
+//   C (16 x 16): lane holds col l % 16, rows 4g .. 4g+3 (4 int32)
+// S^T = K Q^T: rows = 16 keys of a key block, cols = 16 query positions.
+// O^T = V^T P^T: rows = 16 head dims, k = the 16 keys lane g holds scores
+// for (keys 16b + 4g + i, b = 0..3, i = 0..3), so P needs no transpose.
+#include <algorithm>
+
 #include "rq_common.h"
 
-extern "C" int rq_int8_prefill(const void *, int32_t, int64_t, int32_t, int64_t, int64_t, const int32_t *, int64_t,
-                               int64_t, const uint8_t *, int64_t, int32_t, int64_t, int64_t, int32_t, int32_t,
-                               const int32_t *, int64_t, int64_t, const int32_t *, const float *, int32_t,
-                               const float *, int32_t, const float *, int32_t, float, void *, int64_t, int64_t,
-                               void *) {
-    rq::set_error("rq_int8_prefill: not implemented yet");
-    return RQ_EINVAL;
+namespace rq {
+
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+constexpr int kPD = 128;   // head_dim
+constexpr int kKT = 64;    // keys per tile
+constexpr int kPQ = 16;    // query positions per wave
+constexpr float kLog2eP = 1.4426950408889634f;
+
+__device__ __forceinline__ i32x4 mfma_i8(u32x4 a, u32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
+                                                 0);
+}
+
+// int8 table: 16 signed bytes (index -> value) in 4 dwords; lookup of four
+// indices (selector bytes) with v_perm, merging on index bit 3 for 16 entries.
+struct Table8 {
+    uint32_t w[4];
+};
+
+template <int BITS>
+__device__ __forceinline__ uint32_t lookup_i8(const Table8 &t, uint32_t sel) {
+    if constexpr (BITS == 3) {
+        return perm(t.w[1], t.w[0], sel);
+    } else {
+        const uint32_t s7 = sel & 0x07070707u;
+        const uint32_t m = ((sel >> 3) & 0x01010101u) * 0xFFu;
+        return (perm(t.w[1], t.w[0], s7) & ~m) | (perm(t.w[3], t.w[2], s7) & m);
+    }
+}
+
+__device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
+
+struct PrefillArgs {
+    const void *q;
+    int64_t q_st, q_sh;
+    const int32_t *cu_q;
+    const uint8_t *cache;
+    int64_t stride_block, stride_token;
+    int block_size, bs_shift;
+    int64_t num_blocks;
+    int H, G, HQ;
+    const int32_t *bt;
+    int64_t bt_ss, max_blocks;
+    const int32_t *seq_lens;
+    const float *kc, *vc;
+    int nkc, nvc;
+    const float *R;
+    int rot_block;
+    float score_scale;  // sm_scale * log2(e)
+    int qb;             // query positions per workgroup (= 16 * position groups)
+    int npg;            // position groups per workgroup
+    void *out;
+    int64_t o_st, o_sh;
+};
+
+// LDS layout (bytes).  The per-wave staging buffers (q_rot before the key
+// loop, out_rot after it) alias the tile area, which is idle then.
+constexpr int kLdsKhi = 0;                          // [64 keys][128] int8, dims permuted per 8
+constexpr int kLdsKlo = kLdsKhi + kKT * kPD;        // same, low parts
+constexpr int kLdsVthi = kLdsKlo + kKT * kPD;       // [128 dims][64 keys in MFMA k order] int8
+constexpr int kLdsVtlo = kLdsVthi + kKT * kPD;      // same, low parts
+constexpr int kLdsSk = kLdsVtlo + kKT * kPD;        // [64] float: k norm * kmax/127 * score_scale
+constexpr int kLdsSw = kLdsSk + kKT * 4;            // [64] float: v norm
+constexpr int kLdsSwTile = kLdsSw + kKT * 4;        // [4] float: tile max v norm / 127 (+ pad)
+constexpr int kLdsOff = kLdsSwTile + 16;            // [64] uint64 token byte offsets
+constexpr int kLdsEnd = kLdsOff + kKT * 8;
+constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave: 16 x 128 16-bit values
+
+template <int DT, int KB, int VB>
+__global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
+    const int qblk = blockIdx.x;
+    const int h = blockIdx.y;
+    const int64_t seq = blockIdx.z;
+    const int q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
+    const int T = q1 - q0;
+    const int L = a.seq_lens[seq];
+    const int pos_base = L - T;  // position of query 0
+    const int L_eff = (int)min((int64_t)L, a.max_blocks * a.block_size);  // table capacity bounds the keys
+    if (qblk * a.qb >= T || T <= 0) return;
+
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, col = lane & 15;
+    const int gh = wave / a.npg;            // query head inside the GQA group
+    const int pg = wave - gh * a.npg;       // 16-position group
+    const int hq = h * a.G + gh;
+    const int i0 = qblk * a.qb + pg * kPQ;  // first query index of this wave
+    const bool wave_active = i0 < T;
+    const int my_i = i0 + col;              // query index of this lane's column
+    const int my_pos = pos_base + my_i;
+
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *sk = reinterpret_cast<float *>(lds + kLdsSk);
+    float *sw = reinterpret_cast<float *>(lds + kLdsSw);
+    float *sw_tile = reinterpret_cast<float *>(lds + kLdsSwTile);
+    uint64_t *toff = reinterpret_cast<uint64_t *>(lds + kLdsOff);
+    uint16_t *wbuf = reinterpret_cast<uint16_t *>(lds + wave * kWaveBytes);
+
+    // ---- tables ----------------------------------------------------------------
+    float kmax = 0.f, vmax = 0.f;
+    for (int e = 0; e < a.nkc; ++e) kmax = fmaxf(kmax, fabsf(a.kc[e]));
+    for (int e = 0; e < a.nvc; ++e) vmax = fmaxf(vmax, fabsf(a.vc[e]));
+    kmax = kmax > 0.f ? kmax : 1.f;
+    vmax = vmax > 0.f ? vmax : 1.f;
+    Table8 tkh, tkl, tvh, tvl;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t hw = 0, lw = 0, vhw = 0, vlw = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * w + i;
+            const float tk = e < a.nkc ? a.kc[e] * (127.f / kmax) : 0.f;
+            const int kh = sat_i8(tk);
+            const int kl = sat_i8((tk - (float)kh) * 128.f);
+            const float tv = e < a.nvc ? a.vc[e] * (127.f / vmax) : 0.f;
+            const int vh = sat_i8(tv);
+            const int vl = sat_i8((tv - (float)vh) * 128.f);
+            hw |= (uint32_t)(kh & 0xff) << (8 * i);
+            lw |= (uint32_t)(kl & 0xff) << (8 * i);
+            vhw |= (uint32_t)(vh & 0xff) << (8 * i);
+            vlw |= (uint32_t)(vl & 0xff) << (8 * i);
+        }
+        tkh.w[w] = hw;
+        tkl.w[w] = lw;
+        tvh.w[w] = vhw;
+        tvl.w[w] = vlw;
+    }
+    const float k_unit = kmax / 127.f * a.score_scale;  // k int8 unit, in log2-domain score units
+    const float v_unit = vmax / 127.f;
+
+    // ---- Q^T operand (cols = this wave's 16 positions): q_rot rounded to the q dtype,
+    //      quantised per position to hi/lo int8, dims in the permuted order of K ----
+    u32x4 qh[2], ql[2];
+    float sq = 0.f;
+    if (wave_active) {
+        // q_rot of the 16 positions into wbuf [16][128] (fp32 of the dtype-rounded value)
+        for (int idx = lane; idx < kPQ * kPD; idx += 64) {
+            const int r = idx / kPD, j = idx - r * kPD;
+            const int qi = i0 + r;
+            uint32_t v = 0;
+            if (qi < T) {
+                const uint16_t *qrow =
+                    reinterpret_cast<const uint16_t *>(a.q) + (int64_t)(q0 + qi) * a.q_st + (int64_t)hq * a.q_sh;
+                const int k0 = (j / a.rot_block) * a.rot_block;
+                float acc = 0.f;
+                for (int i = 0; i < a.rot_block; ++i)
+                    acc = __builtin_fmaf(Elem<DT>::to_f32(qrow[k0 + i]), a.R[j * kPD + k0 + i], acc);
+                v = Elem<DT>::from_f32(acc);
+            }
+            wbuf[idx] = (uint16_t)v;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // per-position absmax over 128 dims: lane (g, col) covers dims 32g .. 32g+31
+        float amax = 0.f;
+        for (int d = 0; d < 32; ++d) amax = fmaxf(amax, fabsf(Elem<DT>::to_f32(wbuf[col * kPD + 32 * g + d])));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        sq = amax > 0.f ? amax / 127.f : 1.f;
+        const float inv = 1.f / sq;
+        // k-step s covers dims 64s .. 64s+63; lane group g holds dims 64s + 16g .. +15,
+        // stored as two 8-dim groups in the order e0 e2 e4 e6 e1 e3 e5 e7.
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int base = 64 * s + 16 * g + 8 * half;
+                const int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+                uint32_t h2[2] = {0, 0}, l2[2] = {0, 0};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = Elem<DT>::to_f32(wbuf[col * kPD + base + order[e]]) * inv;
+                    const int xh = sat_i8(x);
+                    const int xl = sat_i8((x - (float)xh) * 128.f);
+                    h2[e >> 2] |= (uint32_t)(xh & 0xff) << (8 * (e & 3));
+                    l2[e >> 2] |= (uint32_t)(xl & 0xff) << (8 * (e & 3));
+                }
+                hw[2 * half] = h2[0];
+                hw[2 * half + 1] = h2[1];
+                lw[2 * half] = l2[0];
+                lw[2 * half + 1] = l2[1];
+            }
+            qh[s] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            ql[s] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- key range: causal bound of the whole workgroup --------------------------
+    const int last_i = min(T, (qblk + 1) * a.qb) - 1;
+    const int kv_end = min(L_eff, pos_base + last_i + 1);  // keys [0, kv_end) may be visible
+    const SlotLayout SL(a.H, kPD);
+    const int32_t *bt_row = a.bt + seq * a.bt_ss;
+
+    float acc[8][4];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[m][i] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    for (int k0 = 0; k0 < kv_end; k0 += kKT) {
+        const int nk = min(kKT, kv_end - k0);
+        __syncthreads();  // previous tile fully consumed
+        // ---- token offsets and norms of this key tile ----
+        for (int t = tid; t < kKT; t += nthr) {
+            uint64_t off = 0;
+            float skv = 0.f, nv = 0.f;
+            if (t < nk) {
+                const int pos = k0 + t;
+                int lb, o;
+                if (a.bs_shift >= 0) {
+                    lb = pos >> a.bs_shift;
+                    o = pos & (a.block_size - 1);
+                } else {
+                    lb = pos / a.block_size;
+                    o = pos - lb * a.block_size;
+                }
+                int64_t phys = bt_row[lb];
+                phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
+                off = (uint64_t)(phys * a.stride_block + (int64_t)o * a.stride_token);
+                skv = *reinterpret_cast<const float *>(a.cache + off + SL.k_norm + 4 * h) * k_unit;
+                nv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
+            }
+            toff[t] = off;
+            sk[t] = skv;
+            sw[t] = nv;
+        }
+        __syncthreads();
+        // tile scale for w = p * v_norm: largest v norm of the tile / 127
+        if (wave == 0) {
+            float mx = fmaxf(sw[lane], 0.f);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            if (lane == 0) sw_tile[0] = mx > 0.f ? mx / 127.f : 1.f;
+        }
+        // ---- decode K (row-major, permuted dims, hi and lo) ----
+        for (int w = tid; w < kKT * 16; w += nthr) {
+            const int t = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
+            uint32_t x = 0;
+            if (t < nk) x = *reinterpret_cast<const uint32_t *>(a.cache + toff[t] + SL.k_idx + h * 64 + 4 * dw);
+            const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
+            uint2 hi = make_uint2(lookup_i8<KB>(tkh, even), lookup_i8<KB>(tkh, odd));
+            uint2 lo = make_uint2(lookup_i8<KB>(tkl, even), lookup_i8<KB>(tkl, odd));
+            *reinterpret_cast<uint2 *>(lds + kLdsKhi + t * kPD + 8 * dw) = hi;
+            *reinterpret_cast<uint2 *>(lds + kLdsKlo + t * kPD + 8 * dw) = lo;
+        }
+        // ---- decode V transposed: Vt[dim][kk], kk = MFMA k index of key t:
+        //      key t = 16b + 4g + i  ->  kk = 16g + 4b + i ----
+        for (int w = tid; w < 16 * 16; w += nthr) {
+            const int tq = w >> 4, dw = w & 15;  // key quad (4 consecutive keys), dword position
+            uint32_t x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 4 * tq + i;
+                x[i] = t < nk ? *reinterpret_cast<const uint32_t *>(a.cache + toff[t] + SL.v_idx + h * 64 + 4 * dw)
+                              : 0u;
+            }
+            const uint32_t A01 = perm(x[1], x[0], 0x05010400u), B01 = perm(x[1], x[0], 0x07030602u);
+            const uint32_t A23 = perm(x[3], x[2], 0x05010400u), B23 = perm(x[3], x[2], 0x07030602u);
+            const uint32_t G4[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u),
+                                    perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
+            const int t0 = 4 * tq;                  // = 16b + 4gg
+            const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 8 * dw + 2 * j;
+                const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
+                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + d * kKT + kk) = lookup_i8<VB>(tvh, se);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + (d + 1) * kKT + kk) = lookup_i8<VB>(tvh, so);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + d * kKT + kk) = lookup_i8<VB>(tvl, se);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + (d + 1) * kKT + kk) = lookup_i8<VB>(tvl, so);
+            }
+        }
+        __syncthreads();
+        if (!wave_active) continue;
+        if (k0 > pos_base + i0 + kPQ - 1) continue;  // tile entirely above this wave's diagonal
+        const float s_w = sw_tile[0];
+
+        // ---- S^T = K Q^T for 4 key blocks of 16 ----
+        float s[16];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            i32x4 chh = i32x4{0, 0, 0, 0}, cx = chh;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const int row = 16 * b + col;  // key
+                const u32x4 kh = *reinterpret_cast<const u32x4 *>(lds + kLdsKhi + row * kPD + 64 * st + 16 * g);
+                const u32x4 kl = *reinterpret_cast<const u32x4 *>(lds + kLdsKlo + row * kPD + 64 * st + 16 * g);
+                chh = mfma_i8(kh, qh[st], chh);
+                cx = mfma_i8(kh, ql[st], cx);
+                cx = mfma_i8(kl, qh[st], cx);
+            }
+            const float4 skb = *reinterpret_cast<const float4 *>(sk + 16 * b + 4 * g);
+            const float skv[4] = {skb.x, skb.y, skb.z, skb.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = k0 + 16 * b + 4 * g + i;
+                const float v = ((float)chh[i] + (float)cx[i] * (1.f / 128.f)) * sq * skv[i];
+                s[4 * b + i] = (key < k0 + nk && key <= my_pos) ? v : -INFINITY;
+            }
+        }
+        // ---- online softmax over this lane's 16 keys + the other 3 key groups ----
+        float tmax = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        if (__any(m_new > m_run)) {
+            const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[m][i] *= alpha;
+            l_run *= alpha;
+            m_run = m_new;
+        }
+        // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i)
+        uint32_t wh[4], wl[4];
+        const float inv_sw = 1.f / s_w;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float4 nvb = *reinterpret_cast<const float4 *>(sw + 16 * b + 4 * g);
+            const float nvv[4] = {nvb.x, nvb.y, nvb.z, nvb.w};
+            uint32_t hw = 0, lw = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[4 * b + i] - m_run);
+                l_run += p;
+                const float x = p * nvv[i] * inv_sw;
+                const int xh = sat_i8(x);
+                const int xl = sat_i8((x - (float)xh) * 128.f);
+                hw |= (uint32_t)(xh & 0xff) << (8 * i);
+                lw |= (uint32_t)(xl & 0xff) << (8 * i);
+            }
+            wh[b] = hw;
+            wl[b] = lw;
+        }
+        const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
+        // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
+        const float o_unit = s_w * v_unit;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const u32x4 vah = *reinterpret_cast<const u32x4 *>(lds + kLdsVthi + (16 * m + col) * kKT + 16 * g);
+            const u32x4 val = *reinterpret_cast<const u32x4 *>(lds + kLdsVtlo + (16 * m + col) * kKT + 16 * g);
+            const i32x4 zero = i32x4{0, 0, 0, 0};
+            const i32x4 oh = mfma_i8(vah, ph, zero);
+            i32x4 ol = mfma_i8(vah, pl, zero);
+            ol = mfma_i8(val, ph, ol);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[m][i] += ((float)oh[i] + (float)ol[i] * (1.f / 128.f)) * o_unit;
+        }
+    }
+    __syncthreads();  // the staging buffers below alias the tile area
+    if (!wave_active) return;
+
+    // ---- epilogue: normalise, round to the q dtype, rotate back by R, round ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
+    // acc[m][i] = O[position col][dim 16m + 4g + i]
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            wbuf[col * kPD + 16 * m + 4 * g + i] = (uint16_t)Elem<DT>::from_f32(acc[m][i] * inv_l);
+    __builtin_amdgcn_wave_barrier();
+    for (int idx = lane; idx < kPQ * kPD; idx += 64) {
+        const int r = idx / kPD, d = idx - r * kPD;
+        if (i0 + r >= T) continue;
+        const int kb0 = (d / a.rot_block) * a.rot_block;
+        float o = 0.f;
+        for (int i = 0; i < a.rot_block; ++i)
+            o = __builtin_fmaf(Elem<DT>::to_f32(wbuf[r * kPD + kb0 + i]), a.R[(kb0 + i) * kPD + d], o);
+        uint16_t *dst = reinterpret_cast<uint16_t *>(a.out) + (int64_t)(q0 + i0 + r) * a.o_st + (int64_t)hq * a.o_sh;
+        dst[d] = (uint16_t)Elem<DT>::from_f32(o);
+    }
+}
+
+template <int DT, int KB, int VB>
+static void launch_prefill(const PrefillArgs &a, int64_t num_seqs, int64_t max_q_len, int nwaves, hipStream_t st) {
+    const size_t lds = std::max<size_t>(kLdsEnd, (size_t)nwaves * kWaveBytes);
+    dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)a.H, (unsigned)num_seqs);
+    hipLaunchKernelGGL((prefill_kernel<DT, KB, VB>), grid, dim3(64 * nwaves), lds, st, a);
+}
+
+template <int DT>
+static void launch_prefill_bits(const PrefillArgs &a, int64_t ns, int64_t mq, int nw, int kb, int vb,
+                                hipStream_t st) {
+    if (kb == 3 && vb == 3) launch_prefill<DT, 3, 3>(a, ns, mq, nw, st);
+    else if (kb == 3) launch_prefill<DT, 3, 4>(a, ns, mq, nw, st);
+    else if (vb == 3) launch_prefill<DT, 4, 3>(a, ns, mq, nw, st);
+    else launch_prefill<DT, 4, 4>(a, ns, mq, nw, st);
+}
+
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                               int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
+                               int64_t num_seqs, int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks,
+                               int32_t block_size, int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
+                               int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                               int64_t bt_stride_seq, const int32_t *seq_lens, const float *k_centroids,
+                               int32_t n_k_centroids, const float *v_centroids, int32_t n_v_centroids,
+                               const float *rotation, int32_t rot_block, float sm_scale, void *out,
+                               int64_t out_stride_tok, int64_t out_stride_head, void *stream) {
+    RQ_CHECK_ARG(dtype == RQ_DTYPE_BF16 || dtype == RQ_DTYPE_F16, "prefill dtype must be f16 or bf16");
+    RQ_CHECK_ARG(head_dim == kPD, "head_dim %d unsupported (only %d)", head_dim, kPD);
+    RQ_CHECK_ARG(num_kv_heads >= 1 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 16,
+                 "num_q_heads %d / num_kv_heads %d must be an integer <= 16", num_q_heads, num_kv_heads);
+    RQ_CHECK_ARG((n_k_centroids == 8 || n_k_centroids == 16) && (n_v_centroids == 8 || n_v_centroids == 16),
+                 "centroid counts must be 8 or 16");
+    RQ_CHECK_ARG(rot_block == 2 || rot_block == 4, "rot_block %d must be 2 or 4", rot_block);
+    RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0,
+                 "bad sizes");
+    RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
+                 "cache slots must be 4-byte aligned");
+    if (num_seqs == 0 || max_q_len == 0 || num_blocks == 0) return RQ_OK;
+    PrefillArgs a{};
+    a.q = q;
+    a.q_st = q_stride_tok;
+    a.q_sh = q_stride_head;
+    a.cu_q = cu_seqlens_q;
+    a.cache = kv_cache;
+    a.stride_block = stride_block;
+    a.stride_token = stride_token;
+    a.block_size = block_size;
+    a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+    a.num_blocks = num_blocks;
+    a.H = num_kv_heads;
+    a.G = num_q_heads / num_kv_heads;
+    a.HQ = num_q_heads;
+    a.bt = block_table;
+    a.bt_ss = bt_stride_seq;
+    a.max_blocks = max_blocks;
+    a.seq_lens = seq_lens;
+    a.kc = k_centroids;
+    a.vc = v_centroids;
+    a.nkc = n_k_centroids;
+    a.nvc = n_v_centroids;
+    a.R = rotation;
+    a.rot_block = rot_block;
+    a.score_scale = sm_scale * kLog2eP;
+    a.npg = std::max(1, 8 / a.G);
+    a.qb = kPQ * a.npg;
+    a.out = out;
+    a.o_st = out_stride_tok;
+    a.o_sh = out_stride_head;
+    const int nwaves = a.G * a.npg;
+    const int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == RQ_DTYPE_BF16) launch_prefill_bits<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, kb, vb, st);
+    else launch_prefill_bits<RQ_DTYPE_F16>(a, num_seqs, max_q_len, nwaves, kb, vb, st);
+    return check_launch("prefill_kernel");
 }

@@ -250,9 +250,11 @@ _ws_cache: dict = {}
 
 
 def _workspace(dev, nbytes: int) -> torch.Tensor:
+    """Zero-filled decode scratch (its per-sequence counters must start at zero;
+    every call leaves them zero again), grown on demand and reused."""
     buf = _ws_cache.get(dev)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
         _ws_cache[dev] = buf
     return buf
 
@@ -267,7 +269,8 @@ def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: 
     Reference: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312 (same
     arguments; `max_seq_len` optionally bounds seq_lens and sizes the split-KV
     grid, default block_table.shape[1] * block_size; `workspace` optionally
-    supplies the split-KV scratch, a uint8 device tensor).
+    supplies the split-KV scratch, a uint8 device tensor that must be zero
+    before its first use -- the call leaves it reusable).
     """
     num_seqs, H_Q, D = q.shape
     assert D == head_dim, f"D={D} != head_dim={head_dim}"
