@@ -375,8 +375,6 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
         }
         __builtin_amdgcn_wave_barrier();
     }
-    const int nch = (L + a.chunk - 1) / a.chunk;
-
 }
 
 // Merge the chunk partials of (seq, query head): log-sum-exp over chunks, round
