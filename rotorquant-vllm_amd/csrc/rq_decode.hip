@@ -39,7 +39,7 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 
 constexpr int kD = 128;          // head_dim handled by this kernel
 constexpr int kTile = 32;        // tokens per inner iteration
-constexpr int kMaxWaves = 8;     // waves per workgroup (kv heads beyond 8 loop)
+constexpr int kMaxWaves = 8;     // kv heads (= waves) per workgroup
 constexpr int kMaxKvHeads = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -53,17 +53,21 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                       0, 0, 0);
 }
 
-// Centroids (fp32) -> 16-bit table split in low / high bytes.
+// Centroids (fp32, 16-byte aligned, n = 8 or 16) -> 16-bit table split in low /
+// high bytes.  The loads are uniform vector loads issued together.
 template <int DT>
 __device__ __forceinline__ Table16 make_table(const float *c, int n) {
+    const float4 *c4 = reinterpret_cast<const float4 *>(c);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v4[4] = {c4[0], c4[1], n > 8 ? c4[2] : z, n > 8 ? c4[3] : z};
     Table16 t;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
+        const float e[4] = {v4[w].x, v4[w].y, v4[w].z, v4[w].w};
         uint32_t lo = 0, hi = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int e = 4 * w + i;
-            uint32_t bits = e < n ? Elem<DT>::from_f32(c[e]) : 0u;
+            const uint32_t bits = Elem<DT>::from_f32(e[i]);
             lo |= (bits & 0xffu) << (8 * i);
             hi |= (bits >> 8) << (8 * i);
         }
@@ -90,6 +94,7 @@ struct DecodeArgs {
     int64_t stride_block, stride_token;
     int block_size;
     int bs_shift;       // log2(block_size), or -1 when block_size is not a power of two
+    float inv_block_size;
     int H, G, HQ;
     const int32_t *bt;
     int64_t bt_ss;
@@ -104,7 +109,9 @@ struct DecodeArgs {
     int max_chunks;
     int max_len;        // min(max_blocks * block_size, max_chunks * chunk): lengths are clamped to it
     int64_t num_blocks; // physical blocks; table entries outside [0, num_blocks) read block 0
-    int wave_lds;       // per-wave LDS bytes: 512 + G * 256
+    int hpw;            // kv heads per workgroup = waves per workgroup (divides H, <= 8)
+    int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
+    int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
     float *part_acc;    // [seq][chunk][HQ][D]
     float *part_ml;     // [seq][chunk][HQ][2]
     void *out;
@@ -124,256 +131,387 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     }
 }
 
-// Registers of one 32-token tile for one kv head (loaded one tile ahead).
-struct TileRegs {
-    uint4 kw[2];      // K indices: token 16j + (lane & 15), bytes 16g .. 16g+15 of the head
-    uint32_t vw[8];   // V indices: dword (lane & 15) of tokens 4g+i (i < 4) and 16+4g+(i-4)
-    float nrm;        // lane < 32: K norm * score_scale of token lane; else V norm of token lane-32
-                      // (zero for tokens past the end)
-};
+// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows) with the
+// gfx950 row-swap permutes: swapping a register with itself leaves lane l
+// holding {x[l], x[l^32]} (resp. {x[l], x[l^16]}) in the two results.
+__device__ __forceinline__ float rows_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
 
-template <int DT, int KB, int VB>
-__global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(size_t)(lds_u8 *)p; }
+
+// Direct global -> LDS copies, issued as inline assembly so that the compiler
+// neither waits for them before unrelated LDS accesses nor counts them: the
+// kernel waits for them itself with s_waitcnt vmcnt.  Lane l writes its bytes
+// at LDS address m0 + l * size (m0 = wave-uniform destination).
+//   copy16: 16 bytes from the uniform base `src` + per-lane 32-bit offset.
+//   copy4:  4 bytes from a per-lane address.
+__device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "s"(dst)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void copy4(const uint8_t *src, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_copies() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup = (chunk, sequence, kv-head group of hpw heads); wave w owns kv
+// head h0 + w.  32-token tiles are staged in LDS by direct global->LDS copies
+// into two stages, two tiles ahead of the compute:
+//   stage layout: token t at t * tok_stride: [K idx of the hpw heads | V idx]
+//                 then norm rows (2*hpw x 32 fp32): K norms of each head, V norms.
+// One copy instruction moves a whole token's K+V index run (8*hpw x 16 B), so
+// every request covers whole cache lines.  Iteration i: wait for tile i (tile
+// i+1 stays in flight), barrier, read this wave's operands into registers,
+// barrier, refill the stage with tile i+2, compute tile i from registers.
+// Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
+constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
+
+template <int DT, int KB, int VB, int HPW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
     const int chunk_id = blockIdx.x;
     const int64_t seq = blockIdx.y;
     const int L = min(a.seq_lens[seq], a.max_len);
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;    // k-group / row-group
-    const int col = lane & 15;  // MFMA column (query head inside the GQA group) / row
-
     const int t_begin = chunk_id * a.chunk;
     if (t_begin >= L) return;
     const int n_tok = min(L - t_begin, a.chunk);
+    const int n_tiles = (n_tok + kTile - 1) / kTile;
+
+    // HPW > 0: heads per workgroup fixed at compile time (LDS offsets become immediates)
+    const int hpw = HPW > 0 ? HPW : a.hpw;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;    // k-group / row-group
+    const int col = lane & 15;  // MFMA column (query head inside the GQA group) / row
+    const int h0 = blockIdx.z * hpw;
+    const int h = h0 + wave;
     const SlotLayout SL(a.H, kD);
+    const int TS = HPW > 0 ? 128 * HPW + 16 : a.tok_stride;
+    const int norm_off = kTile * TS;
+    const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
 
     extern __shared__ __align__(16) uint8_t lds[];
-    // per wave: 32 token byte offsets | 64 norms | G x 128 q_rot (16-bit)
-    uint8_t *wbase = lds + wave * a.wave_lds;
-    uint64_t *woff = reinterpret_cast<uint64_t *>(wbase);
-    float *wnorm = reinterpret_cast<float *>(wbase + 256);
-    uint16_t *wq = reinterpret_cast<uint16_t *>(wbase + 512);
-    const int32_t *bt_row = a.bt + seq * a.bt_ss;
+    uint8_t *const stage0 = lds;
+    uint8_t *const stage1 = lds + stage_bytes;
+    int32_t *const bt_lds = reinterpret_cast<int32_t *>(lds + 2 * stage_bytes);
+    const int tl = lane & 31;  // token of this lane in a tile (slot base, norm copy)
 
-    const int nwaves = blockDim.x >> 6;
-    for (int h = wave; h < a.H; h += nwaves) {
-        // ---- rotated queries of this wave's GQA group: q_rot = q R^T, rounded to the q dtype ----
-        for (int idx = lane; idx < a.G * kD; idx += 64) {
-            int qh = idx / kD, j = idx - qh * kD;
-            const uint16_t *qrow = reinterpret_cast<const uint16_t *>(a.q) + seq * a.q_ss + (int64_t)(h * a.G + qh) * a.q_sh;
-            int k0 = (j / a.rot_block) * a.rot_block;
-            float acc = 0.f;
-            for (int i = 0; i < a.rot_block; ++i)
-                acc = __builtin_fmaf(Elem<DT>::to_f32(qrow[k0 + i]), a.R[j * kD + k0 + i], acc);
-            wq[qh * kD + j] = (uint16_t)Elem<DT>::from_f32(acc);
+    // Block index and in-block offset of token t0 + tl (the tile start t_begin + t0
+    // is split once; the lane's small remainder is divided with a float
+    // reciprocal and one correction each way when block_size is not a power of two).
+    auto locate = [&](int t0, int &lb, int &off) {
+        const int pos = t_begin + t0;
+        if (a.bs_shift >= 0) {
+            lb = (pos + tl) >> a.bs_shift;
+            off = (pos + tl) & (a.block_size - 1);
+        } else {
+            const int lb0 = pos / a.block_size;
+            const int x = pos - lb0 * a.block_size + tl;
+            int dq = (int)((float)x * a.inv_block_size);
+            dq += (dq + 1) * a.block_size <= x ? 1 : 0;
+            dq -= dq * a.block_size > x ? 1 : 0;
+            lb = lb0 + dq;
+            off = x - dq * a.block_size;
         }
-        __builtin_amdgcn_wave_barrier();
+    };
+    // This chunk's block-table entries, staged once (out-of-range physical
+    // blocks read block 0).
+    int lb_first;
+    {
+        const int pos = t_begin;
+        lb_first = a.bs_shift >= 0 ? pos >> a.bs_shift : pos / a.block_size;
+        const int last = t_begin + n_tok - 1;
+        const int lb_end = (a.bs_shift >= 0 ? last >> a.bs_shift : last / a.block_size) + 1;
+        const int32_t *bt_row = a.bt + seq * a.bt_ss;
+        for (int k = threadIdx.x; k < lb_end - lb_first; k += blockDim.x) {
+            const int p = bt_row[lb_first + k];
+            bt_lds[k] = (p < 0 || p >= a.num_blocks) ? 0 : p;
+        }
+    }
+    __syncthreads();
+    // Byte offset of the slot of token t0 + tl (token past the end: offset 0).
+    auto tok_base = [&](int t0) -> uint64_t {
+        if (t0 + tl >= n_tok) return 0;
+        int lb, off;
+        locate(t0, lb, off);
+        const int64_t p = bt_lds[lb - lb_first];
+        return (uint64_t)(p * a.stride_block + (int64_t)off * a.stride_token);
+    };
+    // Copies of the tile starting at t0 into stage sb.  Per wave and full tile:
+    // kTile / hpw token copies and one norm copy.
+    auto issue = [&](int t0, const uint8_t *sb) {
+        const uint64_t base = tok_base(t0);
+        const int valid = min(kTile, n_tok - t0);
+        const uint32_t dst = lds_addr(sb);
+        const uint32_t kv_src = lane < 4 * hpw ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * lane)
+                                               : (uint32_t)(SL.v_idx + 64 * h0 + 16 * (lane - 4 * hpw));
+        for (int tt = wave; tt < valid; tt += hpw) {
+            const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
+            if (lane < 8 * hpw) copy16(tok, kv_src, dst + tt * TS);
+        }
+        // norm rows 2*wave, 2*wave+1 (row j < hpw: K norm of head h0+j, else V norm of head h0+j-hpw)
+        const int nrow = 2 * wave + (lane >> 5);
+        const uint32_t norm_src = nrow < hpw ? (uint32_t)(SL.k_norm + 4 * (h0 + nrow))
+                                             : (uint32_t)(SL.v_norm + 4 * (h0 + nrow - hpw));
+        if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
+    };
 
-        // Q^T operand: lane (g, col) for dim chunk c holds dims 32g + 8c + {0,2,4,6,1,3,5,7}.
-        // The MFMA runs in fp16 for any query dtype: the dtype-rounded q_rot is
-        // scaled by 2^qexp (exact) so its largest element sits in [2^14, 2^15).
-        float qv[4][8];
-        float qmax = 0.f;
+    issue(0, stage0);
+
+    // ---- rotated queries of head h: q_rot = q R^T rounded to the q dtype -------------
+    // Staged through this wave's slice of stage 1 (tile 1 is copied there afterwards).
+    uint16_t *wq = reinterpret_cast<uint16_t *>(stage1) + wave * (16 * kD);
+    {
+        // Lane: dims j, j+1 (one rotation block; rb is 2 or 4).  The q loads of four
+        // query heads are issued together.
+        const int rb = a.rot_block;
+        const int j = 2 * lane;
+        const int k0 = (j / rb) * rb;
+        float r0[4], r1[4];
+        if (rb == 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(a.R + j * kD + k0);
+            const float4 y = *reinterpret_cast<const float4 *>(a.R + (j + 1) * kD + k0);
+            r0[0] = x.x, r0[1] = x.y, r0[2] = x.z, r0[3] = x.w;
+            r1[0] = y.x, r1[1] = y.y, r1[2] = y.z, r1[3] = y.w;
+        } else {
+            const float2 x = *reinterpret_cast<const float2 *>(a.R + j * kD + k0);
+            const float2 y = *reinterpret_cast<const float2 *>(a.R + (j + 1) * kD + k0);
+            r0[0] = x.x, r0[1] = x.y, r0[2] = 0.f, r0[3] = 0.f;
+            r1[0] = y.x, r1[1] = y.y, r1[2] = 0.f, r1[3] = 0.f;
+        }
+        const uint16_t *qbase = reinterpret_cast<const uint16_t *>(a.q) + seq * a.q_ss + (int64_t)(h * a.G) * a.q_sh + k0;
+        for (int qh0 = 0; qh0 < a.G; qh0 += 4) {
+            uint2 raw[4];
     #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 w = col < a.G ? *reinterpret_cast<const uint4 *>(wq + col * kD + 32 * g + 8 * c)
-                                      : make_uint4(0, 0, 0, 0);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            for (int u = 0; u < 4; ++u) {
+                const uint16_t *qp = qbase + (int64_t)min(qh0 + u, a.G - 1) * a.q_sh;
+                raw[u] = rb == 4 ? *reinterpret_cast<const uint2 *>(qp) : make_uint2(*reinterpret_cast<const uint32_t *>(qp), 0u);
+            }
     #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qv[c][2 * i] = Elem<DT>::to_f32(ws[i] & 0xffffu);
-                qv[c][2 * i + 1] = Elem<DT>::to_f32(ws[i] >> 16);
-                qmax = fmaxf(qmax, fmaxf(fabsf(qv[c][2 * i]), fabsf(qv[c][2 * i + 1])));
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t w4[2] = {raw[u].x, raw[u].y};
+                float acc0 = 0.f, acc1 = 0.f;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (i < rb) {
+                        const float x = Elem<DT>::to_f32((w4[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+                        acc0 = __builtin_fmaf(x, r0[i], acc0);
+                        acc1 = __builtin_fmaf(x, r1[i], acc1);
+                    }
+                }
+                if (qh0 + u < a.G)
+                    reinterpret_cast<uint32_t *>(wq + (qh0 + u) * kD)[lane] =
+                        Elem<DT>::from_f32(acc0) | (Elem<DT>::from_f32(acc1) << 16);
             }
         }
-        qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
-        qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
-        const int qexp = qmax > 0.f ? 141 - (int)((__float_as_uint(qmax) >> 23) & 0xffu) : 0;  // 14 - floor(log2 qmax)
-        const float qinv = ldexpf(1.f, -qexp);
-        u32x4 qop[4];
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // Q^T operand: lane (g, col) for dim chunk c holds dims 32g + 8c + {0,2,4,6,1,3,5,7}.
+    // The MFMA runs in fp16 for any query dtype: the dtype-rounded q_rot is
+    // scaled by 2^qexp (exact) so its largest element sits in [2^14, 2^15).
+    float qv[4][8];
+    float qmax = 0.f;
     #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            float e[8];
+    for (int c = 0; c < 4; ++c) {
+        const uint4 w = col < a.G ? *reinterpret_cast<const uint4 *>(wq + col * kD + 32 * g + 8 * c)
+                                  : make_uint4(0, 0, 0, 0);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     #pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = ldexpf(qv[c][i], qexp);
-            qop[c].x = pack2<RQ_DTYPE_F16>(e[0], e[2]);
-            qop[c].y = pack2<RQ_DTYPE_F16>(e[4], e[6]);
-            qop[c].z = pack2<RQ_DTYPE_F16>(e[1], e[3]);
-            qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
+        for (int i = 0; i < 4; ++i) {
+            qv[c][2 * i] = Elem<DT>::to_f32(ws[i] & 0xffffu);
+            qv[c][2 * i + 1] = Elem<DT>::to_f32(ws[i] >> 16);
+            qmax = fmaxf(qmax, fmaxf(fabsf(qv[c][2 * i]), fabsf(qv[c][2 * i + 1])));
         }
-
-        const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
-        const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
-
-        f32x4 acc[8];
+    }
+    qmax = rows_max(qmax);
+    const int qexp = qmax > 0.f ? 141 - (int)((__float_as_uint(qmax) >> 23) & 0xffu) : 0;  // 14 - floor(log2 qmax)
+    const float sc = a.score_scale * ldexpf(1.f, -qexp);  // undoes the query's power-of-two scale
+    u32x4 qop[4];
     #pragma unroll
-        for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        float m_run = -INFINITY;  // running max (log2 domain) for query head `col`
-        float l_run = 0.f;        // this lane's partial sum of p
-        int e_run = -126;         // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
+    for (int c = 0; c < 4; ++c) {
+        float e[8];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = ldexpf(qv[c][i], qexp);
+        qop[c].x = pack2<RQ_DTYPE_F16>(e[0], e[2]);
+        qop[c].y = pack2<RQ_DTYPE_F16>(e[4], e[6]);
+        qop[c].z = pack2<RQ_DTYPE_F16>(e[1], e[3]);
+        qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
+    }
+    // Compiler-visible global loads go before the next copy: the compiler does not
+    // count the copies, so a wait it inserts for its own load waits for them too.
+    const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
+    const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
+    __syncthreads();  // every wave is done with its q slice before tile 1 lands in stage 1
+    if (n_tiles > 1) issue(kTile, stage1);
 
-        const uint8_t *cache = a.cache;
-        const int k_idx = SL.k_idx + h * 64;
-        const int v_idx = SL.v_idx + h * 64;
-        const int k_norm = SL.k_norm + 4 * h;
-        const int v_norm = SL.v_norm + 4 * h;
-        const int my_tt = lane & 31;
+    f32x4 acc[8];
+    #pragma unroll
+    for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;  // running max (log2 domain) for query head `col`
+    float l_run = 0.f;        // this lane's partial sum of p
+    int e_run = -126;         // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
 
-        // Issue the loads of the tile starting at t0.  Tokens past the end read
-        // slot 0 of block 0 (always mapped) and get a zero norm.
-        auto load_tile = [&](int t0) {
-            TileRegs r;
-            const int valid = n_tok - t0;
-            uint64_t my_off = 0;
-            const bool ok = my_tt < valid;
-            if (ok) {
-                int pos = t_begin + t0 + my_tt;
-                int lb, off;
-                if (a.bs_shift >= 0) {
-                    lb = pos >> a.bs_shift;
-                    off = pos & (a.block_size - 1);
-                } else {
-                    lb = pos / a.block_size;
-                    off = pos - lb * a.block_size;
-                }
-                int64_t phys = bt_row[lb];
-                phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
-                my_off = (uint64_t)(phys * a.stride_block + (int64_t)off * a.stride_token);
-            }
-            if (lane < 32) woff[lane] = my_off;
-            __builtin_amdgcn_wave_barrier();
-            const uint64_t ok0 = woff[col], ok1 = woff[16 + col];
-            r.kw[0] = *reinterpret_cast<const uint4 *>(cache + ok0 + k_idx + 16 * g);
-            r.kw[1] = *reinterpret_cast<const uint4 *>(cache + ok1 + k_idx + 16 * g);
-            const ulonglong2 va = *reinterpret_cast<const ulonglong2 *>(woff + 4 * g);
-            const ulonglong2 vb = *reinterpret_cast<const ulonglong2 *>(woff + 4 * g + 2);
-            const ulonglong2 vc = *reinterpret_cast<const ulonglong2 *>(woff + 16 + 4 * g);
-            const ulonglong2 vd = *reinterpret_cast<const ulonglong2 *>(woff + 16 + 4 * g + 2);
-            const uint64_t vo[8] = {va.x, va.y, vb.x, vb.y, vc.x, vc.y, vd.x, vd.y};
-    #pragma unroll
-            for (int i = 0; i < 8; ++i) r.vw[i] = *reinterpret_cast<const uint32_t *>(cache + vo[i] + v_idx + 4 * col);
-            float nv = *reinterpret_cast<const float *>(cache + my_off + (lane < 32 ? k_norm : v_norm));
-            nv = lane < 32 ? nv * a.score_scale : nv;
-            r.nrm = ok ? nv : 0.f;
-            __builtin_amdgcn_wave_barrier();
-            return r;
-        };
+    for (int it = 0; it < n_tiles; ++it) {
+        const int t0 = it * kTile;
+        const uint8_t *const sb = (it & 1) ? stage1 : stage0;
+        // Tile it landed?  Tile it+1 (issued later) may stay in flight when it is full.
+        if (HPW > 0 && t0 + 2 * kTile <= n_tok) wait_copies<kTile / (HPW > 0 ? HPW : 1) + 1>();
+        else wait_copies<0>();
+        __syncthreads();
 
-        TileRegs cur = load_tile(0);
-        for (int t0 = 0; t0 < n_tok; t0 += kTile) {
-            const int valid = n_tok - t0;
-            TileRegs nxt;
-            if (t0 + kTile < n_tok) nxt = load_tile(t0 + kTile);
+        // ---- this wave's operands of the tile ------------------------------------
+        const uint8_t *kb = sb + col * TS + 64 * wave + 16 * g;                 // token col, K bytes 16g..
+        const uint8_t *vb = sb + 4 * g * TS + 64 * hpw + 64 * wave + 4 * col;  // token 4g, V dword col
+        const uint8_t *nb = sb + norm_off + 128 * wave + 16 * g;               // K norms of tokens 4g..4g+3
+        const uint4 kw0 = *reinterpret_cast<const uint4 *>(kb);
+        const uint4 kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
+        uint32_t vw[8];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
+        const float4 nk0 = *reinterpret_cast<const float4 *>(nb);
+        const float4 nk1 = *reinterpret_cast<const float4 *>(nb + 64);
+        const float4 nv0 = *reinterpret_cast<const float4 *>(nb + 128 * hpw);
+        const float4 nv1 = *reinterpret_cast<const float4 *>(nb + 128 * hpw + 64);
+        __syncthreads();  // the stage is free once every wave holds its operands
 
-            // largest V norm of the tile (lanes 32..63) -> power-of-two scale of P
-            float nvm = lane >= 32 ? cur.nrm : 0.f;
-    #pragma unroll
-            for (int o = 1; o < 32; o <<= 1) nvm = fmaxf(nvm, __shfl_xor(nvm, o));
-            const int e_tile = (int)((__float_as_uint(__shfl(nvm, 32)) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
-            if (e_tile > e_run) {
-                const float f = ldexpf(1.f, e_run - e_tile);
-    #pragma unroll
-                for (int m = 0; m < 8; ++m) acc[m] *= f;
-                e_run = e_tile;
-            }
-            wnorm[lane] = lane < 32 ? cur.nrm : ldexpf(cur.nrm, -e_run);
-            __builtin_amdgcn_wave_barrier();
+        // ---- tile it+2 into the same stage -------------------------------------------
+        if (t0 + 2 * kTile < n_tok) issue(t0 + 2 * kTile, sb);
 
-            // ---- S^T = K Q^T ----------------------------------------------------
-            f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
-            {
-                const uint32_t k0w[4] = {cur.kw[0].x, cur.kw[0].y, cur.kw[0].z, cur.kw[0].w};
-                const uint32_t k1w[4] = {cur.kw[1].x, cur.kw[1].y, cur.kw[1].z, cur.kw[1].w};
-    #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    s0 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k0w[c]), qop[c], s0);
-                    s1 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k1w[c]), qop[c], s1);
-                }
-            }
-            // ---- scale by K norm, mask, online softmax ---------------------------
-            const float4 nk0 = *reinterpret_cast<const float4 *>(wnorm + 4 * g);
-            const float4 nk1 = *reinterpret_cast<const float4 *>(wnorm + 16 + 4 * g);
-            const float4 nv0 = *reinterpret_cast<const float4 *>(wnorm + 32 + 4 * g);
-            const float4 nv1 = *reinterpret_cast<const float4 *>(wnorm + 48 + 4 * g);
-            // undo the query's power-of-two scale (per query head = per lane column)
-            float s[8] = {s0.x * nk0.x * qinv, s0.y * nk0.y * qinv, s0.z * nk0.z * qinv, s0.w * nk0.w * qinv,
-                          s1.x * nk1.x * qinv, s1.y * nk1.y * qinv, s1.z * nk1.z * qinv, s1.w * nk1.w * qinv};
-            if (valid < kTile) {
-    #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    int tt = (i < 4) ? 4 * g + i : 16 + 4 * g + (i - 4);
-                    s[i] = tt < valid ? s[i] : -INFINITY;
-                }
-            }
-            float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            if (__any(tmax > m_run)) {
-                const float m_new = fmaxf(m_run, tmax);
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
-    #pragma unroll
-                for (int m = 0; m < 8; ++m) acc[m] *= alpha;
-                l_run *= alpha;
-                m_run = m_new;
-            }
-            float p[8];
+        // ---- tokens past the end were not copied: their stage bytes are stale.  Zero
+        // their norms and V indices (a stale nibble >= 8 would look up a NaN in an
+        // 8-entry table, and NaN * 0 would reach the accumulator); their scores are
+        // masked below.
+        const int valid = min(kTile, n_tok - t0);
+        float nk[8] = {nk0.x, nk0.y, nk0.z, nk0.w, nk1.x, nk1.y, nk1.z, nk1.w};
+        float nv[8] = {nv0.x, nv0.y, nv0.z, nv0.w, nv1.x, nv1.y, nv1.z, nv1.w};
+        if (valid < kTile) {
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
-                l_run += p[i];
-            }
-            u32x4 pop;
-            pop.x = pack2<RQ_DTYPE_F16>(p[0] * nv0.x, p[1] * nv0.y);
-            pop.y = pack2<RQ_DTYPE_F16>(p[2] * nv0.z, p[3] * nv0.w);
-            pop.z = pack2<RQ_DTYPE_F16>(p[4] * nv1.x, p[5] * nv1.y);
-            pop.w = pack2<RQ_DTYPE_F16>(p[6] * nv1.z, p[7] * nv1.w);
-
-            // ---- O^T += V^T P^T ---------------------------------------------------
-            // Byte-transpose the 8 tokens' dwords: Ga[j] = byte j of tokens 0..3,
-            // Gb[j] = byte j of tokens 4..7; then split nibbles per head dim.
-            const uint32_t *vw = cur.vw;
-            uint32_t A01 = perm(vw[1], vw[0], 0x05010400u), B01 = perm(vw[1], vw[0], 0x07030602u);
-            uint32_t A23 = perm(vw[3], vw[2], 0x05010400u), B23 = perm(vw[3], vw[2], 0x07030602u);
-            uint32_t A45 = perm(vw[5], vw[4], 0x05010400u), B45 = perm(vw[5], vw[4], 0x07030602u);
-            uint32_t A67 = perm(vw[7], vw[6], 0x05010400u), B67 = perm(vw[7], vw[6], 0x07030602u);
-            uint32_t Ga[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u), perm(B23, B01, 0x05040100u),
-                              perm(B23, B01, 0x07060302u)};
-            uint32_t Gb[4] = {perm(A67, A45, 0x05040100u), perm(A67, A45, 0x07060302u), perm(B67, B45, 0x05040100u),
-                              perm(B67, B45, 0x07060302u)};
-    #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint2 ha = lookup4<VB>(tv, (Ga[j] >> 4) & 0x0f0f0f0fu), hb = lookup4<VB>(tv, (Gb[j] >> 4) & 0x0f0f0f0fu);
-                uint2 la = lookup4<VB>(tv, Ga[j] & 0x0f0f0f0fu), lb = lookup4<VB>(tv, Gb[j] & 0x0f0f0f0fu);
-                acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // dim 8r + 2j
-                acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // dim 8r + 2j + 1
-            }
-            __builtin_amdgcn_wave_barrier();
-            cur = nxt;
-        }
-
-        // ---- partials ------------------------------------------------------------
-        l_run += __shfl_xor(l_run, 16);
-        l_run += __shfl_xor(l_run, 32);
-        if (col < a.G) {
-            const int hq = h * a.G + col;
-            const int64_t pidx = (seq * a.max_chunks + chunk_id) * a.HQ + hq;
-            float *pa = a.part_acc + pidx * kD;
-            // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
-            const float es = ldexpf(1.f, e_run);
-    #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
-                float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
-                float4 *dst = reinterpret_cast<float4 *>(pa + 8 * (4 * g + i));
-                dst[0] = lo;
-                dst[1] = hi;
-            }
-            if (g == 0) {
-                a.part_ml[pidx * 2] = m_run;
-                a.part_ml[pidx * 2 + 1] = l_run;
+                const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
+                nk[i] = tt < valid ? nk[i] : 0.f;
+                nv[i] = tt < valid ? nv[i] : 0.f;
+                vw[i] = tt < valid ? vw[i] : 0u;
             }
         }
-        __builtin_amdgcn_wave_barrier();
+        // largest V norm of the tile -> power-of-two scale of P
+        float nvm = fmaxf(fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3])), fmaxf(fmaxf(nv[4], nv[5]), fmaxf(nv[6], nv[7])));
+        nvm = rows_max(nvm);
+        const int e_tile = (int)((__float_as_uint(nvm) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
+        if (e_tile > e_run) {
+            const float f = ldexpf(1.f, e_run - e_tile);
+    #pragma unroll
+            for (int m = 0; m < 8; ++m) acc[m] *= f;
+            e_run = e_tile;
+        }
+
+        // ---- S^T = K Q^T ----------------------------------------------------
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+        {
+            const uint32_t k0w[4] = {kw0.x, kw0.y, kw0.z, kw0.w};
+            const uint32_t k1w[4] = {kw1.x, kw1.y, kw1.z, kw1.w};
+    #pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s0 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k0w[c]), qop[c], s0);
+                s1 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k1w[c]), qop[c], s1);
+            }
+        }
+        // ---- scale by K norm, mask, online softmax ---------------------------
+        float s[8] = {s0.x * nk[0], s0.y * nk[1], s0.z * nk[2], s0.w * nk[3],
+                      s1.x * nk[4], s1.y * nk[5], s1.z * nk[6], s1.w * nk[7]};
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] *= sc;
+        if (valid < kTile) {
+    #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
+                s[i] = tt < valid ? s[i] : -INFINITY;
+            }
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        tmax = rows_max(tmax);
+        if (__any(tmax > m_run)) {
+            const float m_new = fmaxf(m_run, tmax);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
+    #pragma unroll
+            for (int m = 0; m < 8; ++m) acc[m] *= alpha;
+            l_run *= alpha;
+            m_run = m_new;
+        }
+        const float pf = ldexpf(1.f, -e_run);
+        float p[8];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
+            l_run += p[i];
+            nv[i] *= pf;
+        }
+        u32x4 pop;
+        pop.x = pack2<RQ_DTYPE_F16>(p[0] * nv[0], p[1] * nv[1]);
+        pop.y = pack2<RQ_DTYPE_F16>(p[2] * nv[2], p[3] * nv[3]);
+        pop.z = pack2<RQ_DTYPE_F16>(p[4] * nv[4], p[5] * nv[5]);
+        pop.w = pack2<RQ_DTYPE_F16>(p[6] * nv[6], p[7] * nv[7]);
+
+        // ---- O^T += V^T P^T ---------------------------------------------------
+        // Byte-transpose the 8 tokens' dwords: Ga[j] = byte j of tokens 0..3,
+        // Gb[j] = byte j of tokens 4..7; then split nibbles per head dim.
+        uint32_t A01 = perm(vw[1], vw[0], 0x05010400u), B01 = perm(vw[1], vw[0], 0x07030602u);
+        uint32_t A23 = perm(vw[3], vw[2], 0x05010400u), B23 = perm(vw[3], vw[2], 0x07030602u);
+        uint32_t A45 = perm(vw[5], vw[4], 0x05010400u), B45 = perm(vw[5], vw[4], 0x07030602u);
+        uint32_t A67 = perm(vw[7], vw[6], 0x05010400u), B67 = perm(vw[7], vw[6], 0x07030602u);
+        uint32_t Ga[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u), perm(B23, B01, 0x05040100u),
+                          perm(B23, B01, 0x07060302u)};
+        uint32_t Gb[4] = {perm(A67, A45, 0x05040100u), perm(A67, A45, 0x07060302u), perm(B67, B45, 0x05040100u),
+                          perm(B67, B45, 0x07060302u)};
+    #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint2 ha = lookup4<VB>(tv, (Ga[j] >> 4) & 0x0f0f0f0fu), hb = lookup4<VB>(tv, (Gb[j] >> 4) & 0x0f0f0f0fu);
+            uint2 la = lookup4<VB>(tv, Ga[j] & 0x0f0f0f0fu), lb = lookup4<VB>(tv, Gb[j] & 0x0f0f0f0fu);
+            acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // dim 8r + 2j
+            acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // dim 8r + 2j + 1
+        }
+    }
+
+    // ---- partials ------------------------------------------------------------
+    l_run = rows_sum(l_run);
+    if (col < a.G) {
+        const int hq = h * a.G + col;
+        const int64_t pidx = (seq * a.max_chunks + chunk_id) * a.HQ + hq;
+        float *pa = a.part_acc + pidx * kD;
+        // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
+        const float es = ldexpf(1.f, e_run);
+    #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
+            float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
+            float4 *dst = reinterpret_cast<float4 *>(pa + 8 * (4 * g + i));
+            dst[0] = lo;
+            dst[1] = hi;
+        }
+        if (g == 0) {
+            a.part_ml[pidx * 2] = m_run;
+            a.part_ml[pidx * 2 + 1] = l_run;
+        }
     }
 }
 
@@ -445,10 +583,17 @@ static int pick_chunk(int64_t num_seqs, int64_t max_seq_len) {
     return (int)c;
 }
 
+template <int DT, int KB, int VB, int HPW>
+static void launch_decode_h(const DecodeArgs &a, int64_t num_seqs, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3(a.max_chunks, (unsigned)num_seqs, a.H / a.hpw),
+                       dim3(64 * a.hpw), lds, st, a);
+}
+
 template <int DT, int KB, int VB>
 static void launch_decode(const DecodeArgs &a, int64_t num_seqs, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((decode_kernel<DT, KB, VB>), dim3(a.max_chunks, (unsigned)num_seqs),
-                       dim3(64 * std::min(a.H, kMaxWaves)), lds, st, a);
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, num_seqs, lds, st);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, num_seqs, lds, st);
+    else launch_decode_h<DT, KB, VB, 0>(a, num_seqs, lds, st);
 }
 
 template <int DT>
@@ -496,6 +641,8 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
                  "cache slots must be 16-byte aligned");
     RQ_CHECK_ARG(((uintptr_t)q % 16) == 0 && (q_stride_head * 2) % 16 == 0 && (q_stride_seq * 2) % 16 == 0,
                  "q rows must be 16-byte aligned");
+    RQ_CHECK_ARG(((uintptr_t)k_centroids % 16) == 0 && ((uintptr_t)v_centroids % 16) == 0 && ((uintptr_t)rotation % 16) == 0,
+                 "centroids and rotation must be 16-byte aligned");
     if (num_seqs == 0) return RQ_OK;
     RQ_CHECK_ARG(workspace_bytes >= rq_fused_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_seq_len),
                  "workspace too small");
@@ -529,13 +676,22 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.part_ml = a.part_acc + num_seqs * (int64_t)a.max_chunks * num_q_heads * kD;
     a.num_blocks = num_blocks;
     a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-    a.wave_lds = 512 + a.G * kD * 2;
+    a.inv_block_size = 1.f / (float)block_size;
+    a.hpw = 1;
+    for (int d = std::min(a.H, kMaxWaves); d >= 1; --d)
+        if (a.H % d == 0) {
+            a.hpw = d;
+            break;
+        }
+    a.tok_stride = 128 * a.hpw + 16;
+    a.stage_bytes = kTile * a.tok_stride + 2 * a.hpw * kTile * 4;
     a.max_len = num_blocks > 0 ? (int)std::min<int64_t>(max_blocks * block_size, (int64_t)a.max_chunks * a.chunk) : 0;
     a.out = out;
     a.o_ss = out_stride_seq;
     a.o_sh = out_stride_head;
-    const int nwaves = std::min(a.H, kMaxWaves);
-    size_t lds = (size_t)nwaves * a.wave_lds;
+    const int64_t bt_entries = a.chunk / block_size + 2;  // block-table entries one chunk can span
+    RQ_CHECK_ARG(bt_entries <= 8192, "block_size %d too small for %d-token chunks", block_size, a.chunk);
+    const size_t lds = 2 * (size_t)a.stage_bytes + 4 * (size_t)bt_entries;
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, num_seqs, lds, kb, vb, st);
