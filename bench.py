@@ -88,36 +88,80 @@ def decode_bytes(lens, H, HQ, D, BS):
     return (sum(lens) * 136 * H * D // 128 + sum((L + BS - 1) // BS for L in lens) * 4 + B * HQ * D * 2 * 2 + 4 * B)
 
 
-def time_decode(inp, steps, warmup):
+def time_decode(inp, steps, warmup, graphs=False):
+    """Time `steps` decode steps (step i reads cache copy i % copies).
+
+    Each step is one rq_fused_decode call (prep, split-KV decode and merge
+    kernels) issued through a pre-validated launcher, so the host issues a step
+    in a few microseconds and the GPU does not wait for Python.  With
+    graphs=True the calls are instead captured in HIP graphs and replayed (the
+    replays' outputs are checked bit for bit against eager calls).  Events
+    bracket every step on the launch stream."""
     import torch
 
+    from rotorquant_vllm import _lib
     from rotorquant_vllm import kernels as K
 
     p = inp["p"]
     dev = inp["q"].device
     kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
-    out = torch.empty_like(inp["q"])
     max_len = max(inp["lens_host"])
     caches = inp["caches"]
+    n = len(caches)
+    need = _lib.load().rq_fused_decode_workspace_bytes(len(inp["lens_host"]), inp["HQ"], inp["D"], max_len)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    outs = [torch.empty_like(inp["q"]) for _ in range(n)]
 
-    def step(i):
-        K.fused_paged_rq_decode(inp["q"], caches[i % len(caches)], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
-                                inp["D"], inp["BS"], out=out, max_seq_len=max_len)
+    launchers = [K.fused_paged_rq_decode_launcher(inp["q"], caches[i], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
+                                                  inp["D"], inp["BS"], out=outs[i], max_seq_len=max_len, workspace=ws)
+                 for i in range(n)]
+
+    def call(i):
+        launchers[i % n]()
+
+    for i in range(n):
+        call(i)
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    g_list = []
+    if graphs:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(n):
+                call(i)
+        torch.cuda.current_stream().wait_stream(side)
+        for i in range(n):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                call(i)
+            g_list.append(g)
+
+    def run(i):
+        if g_list:
+            g_list[i % n].replay()
+        else:
+            call(i)
 
     for i in range(warmup):
-        step(i)
+        run(i)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
+    ev[0].record()
     for i in range(steps):
-        starts[i].record()
-        step(i)
-        ends[i].record()
+        run(i)
+        ev[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return dict(wall_s=wall, avg_ms=sum(per) / len(per), median_ms=per[len(per) // 2], min_ms=per[0]), out
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    total_ms = ev[0].elapsed_time(ev[steps])
+    for i in range(n):  # replays must reproduce the eager results exactly
+        run(i)
+    torch.cuda.synchronize()
+    exact = all(torch.equal(o, e) for o, e in zip(outs, eager))
+    return dict(wall_s=wall, avg_ms=total_ms / steps, median_ms=per[len(per) // 2], min_ms=per[0],
+                graphs=bool(g_list), replay_matches_eager=exact), outs[0]
 
 
 def time_compress(n_tokens=32768, H=8, D=128, steps=20):
@@ -194,6 +238,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
+    ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -205,7 +250,10 @@ def main():
     lens = config1_lens()
     inp = build_decode_inputs(lens)
     torch.cuda.synchronize()
-    t, _ = time_decode(inp, args.steps, args.warmup)
+    t, _ = time_decode(inp, args.steps, args.warmup, graphs=args.graphs)
+    if t["graphs"] and not t["replay_matches_eager"]:
+        print("bench.py: graph replay differs from eager results; timing eager launches", file=sys.stderr)
+        t, _ = time_decode(inp, args.steps, args.warmup, graphs=False)
     nbytes = decode_bytes(lens, 8, 32, 128, 16)
     step_s = t["avg_ms"] * 1e-3
     gbs = nbytes / step_s / 1e9
@@ -228,7 +276,7 @@ def main():
                    "cache_copies_rotated": len(inp["caches"])},
         "decode_tok_per_s": round(64 / step_s, 1),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "step_ms": {k: round(v, 5) for k, v in t.items() if k != "wall_s"},
+        "step_ms": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in t.items() if k != "wall_s"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "rq_fused_decode (decode_kernel + decode_merge_kernel), HIP events per launch"},

@@ -112,6 +112,10 @@ struct DecodeArgs {
     int hpw;            // kv heads per workgroup = waves per workgroup (divides H, <= 8)
     int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
     int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
+    const int4 *items;  // work list (decode_prep_kernel)
+    int4 *items_out;
+    uint32_t *qops;     // [seq][H][64 lanes][16] fp16 query operands
+    float *qscale;      // [seq][H][16] score scales
     float *part_acc;    // [seq][chunk][HQ][D]
     float *part_ml;     // [seq][chunk][HQ][2]
     void *out;
@@ -175,6 +179,139 @@ __device__ __forceinline__ void wait_copies() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// q_rot = q R^T of the G query heads of (seq, kv head h), rounded to the query
+// dtype, as the fp16 Q^T MFMA operand: lane (g, col) holds for dim chunk c the
+// dims 32g + 8c + {0,2,4,6,1,3,5,7} of query head col (zero for col >= G).  The
+// rounded q_rot is scaled by 2^qexp (exact) so its largest element sits in
+// [2^14, 2^15); sc = score_scale * 2^-qexp undoes it on the scores.
+// wq: this wave's LDS scratch of G * 128 16-bit values.
+template <int DT>
+__device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, int h, uint16_t *wq, u32x4 (&qop)[4],
+                                              float &sc) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, col = lane & 15;
+    {
+        // Lane: dims j, j+1 (one rotation block; rb is 2 or 4).  The q loads of four
+        // query heads are issued together.
+        const int rb = a.rot_block;
+        const int j = 2 * lane;
+        const int k0 = (j / rb) * rb;
+        float r0[4], r1[4];
+        if (rb == 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(a.R + j * kD + k0);
+            const float4 y = *reinterpret_cast<const float4 *>(a.R + (j + 1) * kD + k0);
+            r0[0] = x.x, r0[1] = x.y, r0[2] = x.z, r0[3] = x.w;
+            r1[0] = y.x, r1[1] = y.y, r1[2] = y.z, r1[3] = y.w;
+        } else {
+            const float2 x = *reinterpret_cast<const float2 *>(a.R + j * kD + k0);
+            const float2 y = *reinterpret_cast<const float2 *>(a.R + (j + 1) * kD + k0);
+            r0[0] = x.x, r0[1] = x.y, r0[2] = 0.f, r0[3] = 0.f;
+            r1[0] = y.x, r1[1] = y.y, r1[2] = 0.f, r1[3] = 0.f;
+        }
+        const uint16_t *qbase = reinterpret_cast<const uint16_t *>(a.q) + seq * a.q_ss + (int64_t)(h * a.G) * a.q_sh + k0;
+        for (int qh0 = 0; qh0 < a.G; qh0 += 4) {
+            uint2 raw[4];
+    #pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint16_t *qp = qbase + (int64_t)min(qh0 + u, a.G - 1) * a.q_sh;
+                raw[u] = rb == 4 ? *reinterpret_cast<const uint2 *>(qp) : make_uint2(*reinterpret_cast<const uint32_t *>(qp), 0u);
+            }
+    #pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t w4[2] = {raw[u].x, raw[u].y};
+                float acc0 = 0.f, acc1 = 0.f;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (i < rb) {
+                        const float x = Elem<DT>::to_f32((w4[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+                        acc0 = __builtin_fmaf(x, r0[i], acc0);
+                        acc1 = __builtin_fmaf(x, r1[i], acc1);
+                    }
+                }
+                if (qh0 + u < a.G)
+                    reinterpret_cast<uint32_t *>(wq + (qh0 + u) * kD)[lane] =
+                        Elem<DT>::from_f32(acc0) | (Elem<DT>::from_f32(acc1) << 16);
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float qv[4][8];
+    float qmax = 0.f;
+    #pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 w = col < a.G ? *reinterpret_cast<const uint4 *>(wq + col * kD + 32 * g + 8 * c)
+                                  : make_uint4(0, 0, 0, 0);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qv[c][2 * i] = Elem<DT>::to_f32(ws[i] & 0xffffu);
+            qv[c][2 * i + 1] = Elem<DT>::to_f32(ws[i] >> 16);
+            qmax = fmaxf(qmax, fmaxf(fabsf(qv[c][2 * i]), fabsf(qv[c][2 * i + 1])));
+        }
+    }
+    qmax = rows_max(qmax);
+    const int qexp = qmax > 0.f ? 141 - (int)((__float_as_uint(qmax) >> 23) & 0xffu) : 0;  // 14 - floor(log2 qmax)
+    sc = a.score_scale * ldexpf(1.f, -qexp);
+    #pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float e[8];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = ldexpf(qv[c][i], qexp);
+        qop[c].x = pack2<RQ_DTYPE_F16>(e[0], e[2]);
+        qop[c].y = pack2<RQ_DTYPE_F16>(e[4], e[6]);
+        qop[c].z = pack2<RQ_DTYPE_F16>(e[1], e[3]);
+        qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Per-call preparation, one workgroup per sequence:
+//   * the fp16 query operands (and score scales) of every kv head, stored in
+//     lane order so each decode lane loads its 64 bytes contiguously;
+//   * the work list: items[prefix(seq) + c] = {seq, c, tokens of chunk c}, where
+//     prefix(seq) counts the chunks of the sequences before it.  Entries from
+//     the total up to num_seqs * max_chunks get seq = -1.  Decode workgroup i
+//     takes item i, so the non-empty chunks occupy the first workgroup ids and
+//     spread evenly over the XCDs.
+template <int DT>
+__global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
+    const int64_t seq = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
+    __shared__ __align__(16) uint16_t wq_all[kMaxWaves][16 * kD];
+    __shared__ int part[kMaxWaves];
+    for (int h = wave; h < a.H; h += nw) {
+        u32x4 qop[4];
+        float sc;
+        query_operand<DT>(a, seq, h, wq_all[wave], qop, sc);
+        uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
+    #pragma unroll
+        for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
+        if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
+    }
+    // chunks of the sequences before this one
+    auto nch = [&](int64_t b) {
+        const int L = min(a.seq_lens[b], a.max_len);
+        return L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
+    };
+    int cnt = 0;
+    for (int64_t b = threadIdx.x; b < seq; b += blockDim.x) cnt += nch(b);
+    for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o);
+    if (lane == 0) part[wave] = cnt;
+    __syncthreads();
+    int prefix = 0;
+    for (int w = 0; w < nw; ++w) prefix += part[w];
+    const int mine = nch(seq);
+    const int L = min(a.seq_lens[seq], a.max_len);
+    for (int c = threadIdx.x; c < mine; c += blockDim.x)
+        a.items_out[prefix + c] = make_int4((int)seq, c, min(L - c * a.chunk, a.chunk), 0);
+    if (seq == gridDim.x - 1) {
+        const int64_t cap = (int64_t)gridDim.x * a.max_chunks;
+        for (int64_t i = prefix + mine + threadIdx.x; i < cap; i += blockDim.x) a.items_out[i] = make_int4(-1, 0, 0, 0);
+    }
+}
+
 // Workgroup = (chunk, sequence, kv-head group of hpw heads); wave w owns kv
 // head h0 + w.  32-token tiles are staged in LDS by direct global->LDS copies
 // into two stages, two tiles ahead of the compute:
@@ -189,12 +326,12 @@ constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 
 
 template <int DT, int KB, int VB, int HPW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
-    const int chunk_id = blockIdx.x;
-    const int64_t seq = blockIdx.y;
-    const int L = min(a.seq_lens[seq], a.max_len);
+    const int4 item = a.items[blockIdx.x];
+    if (item.x < 0) return;
+    const int64_t seq = item.x;
+    const int chunk_id = item.y;
     const int t_begin = chunk_id * a.chunk;
-    if (t_begin >= L) return;
-    const int n_tok = min(L - t_begin, a.chunk);
+    const int n_tok = item.z;
     const int n_tiles = (n_tok + kTile - 1) / kTile;
 
     // HPW > 0: heads per workgroup fixed at compile time (LDS offsets become immediates)
@@ -276,93 +413,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
     };
 
-    issue(0, stage0);
-
-    // ---- rotated queries of head h: q_rot = q R^T rounded to the q dtype -------------
-    // Staged through this wave's slice of stage 1 (tile 1 is copied there afterwards).
-    uint16_t *wq = reinterpret_cast<uint16_t *>(stage1) + wave * (16 * kD);
-    {
-        // Lane: dims j, j+1 (one rotation block; rb is 2 or 4).  The q loads of four
-        // query heads are issued together.
-        const int rb = a.rot_block;
-        const int j = 2 * lane;
-        const int k0 = (j / rb) * rb;
-        float r0[4], r1[4];
-        if (rb == 4) {
-            const float4 x = *reinterpret_cast<const float4 *>(a.R + j * kD + k0);
-            const float4 y = *reinterpret_cast<const float4 *>(a.R + (j + 1) * kD + k0);
-            r0[0] = x.x, r0[1] = x.y, r0[2] = x.z, r0[3] = x.w;
-            r1[0] = y.x, r1[1] = y.y, r1[2] = y.z, r1[3] = y.w;
-        } else {
-            const float2 x = *reinterpret_cast<const float2 *>(a.R + j * kD + k0);
-            const float2 y = *reinterpret_cast<const float2 *>(a.R + (j + 1) * kD + k0);
-            r0[0] = x.x, r0[1] = x.y, r0[2] = 0.f, r0[3] = 0.f;
-            r1[0] = y.x, r1[1] = y.y, r1[2] = 0.f, r1[3] = 0.f;
-        }
-        const uint16_t *qbase = reinterpret_cast<const uint16_t *>(a.q) + seq * a.q_ss + (int64_t)(h * a.G) * a.q_sh + k0;
-        for (int qh0 = 0; qh0 < a.G; qh0 += 4) {
-            uint2 raw[4];
-    #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint16_t *qp = qbase + (int64_t)min(qh0 + u, a.G - 1) * a.q_sh;
-                raw[u] = rb == 4 ? *reinterpret_cast<const uint2 *>(qp) : make_uint2(*reinterpret_cast<const uint32_t *>(qp), 0u);
-            }
-    #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t w4[2] = {raw[u].x, raw[u].y};
-                float acc0 = 0.f, acc1 = 0.f;
-    #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (i < rb) {
-                        const float x = Elem<DT>::to_f32((w4[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-                        acc0 = __builtin_fmaf(x, r0[i], acc0);
-                        acc1 = __builtin_fmaf(x, r1[i], acc1);
-                    }
-                }
-                if (qh0 + u < a.G)
-                    reinterpret_cast<uint32_t *>(wq + (qh0 + u) * kD)[lane] =
-                        Elem<DT>::from_f32(acc0) | (Elem<DT>::from_f32(acc1) << 16);
-            }
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-
-    // Q^T operand: lane (g, col) for dim chunk c holds dims 32g + 8c + {0,2,4,6,1,3,5,7}.
-    // The MFMA runs in fp16 for any query dtype: the dtype-rounded q_rot is
-    // scaled by 2^qexp (exact) so its largest element sits in [2^14, 2^15).
-    float qv[4][8];
-    float qmax = 0.f;
-    #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint4 w = col < a.G ? *reinterpret_cast<const uint4 *>(wq + col * kD + 32 * g + 8 * c)
-                                  : make_uint4(0, 0, 0, 0);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            qv[c][2 * i] = Elem<DT>::to_f32(ws[i] & 0xffffu);
-            qv[c][2 * i + 1] = Elem<DT>::to_f32(ws[i] >> 16);
-            qmax = fmaxf(qmax, fmaxf(fabsf(qv[c][2 * i]), fabsf(qv[c][2 * i + 1])));
-        }
-    }
-    qmax = rows_max(qmax);
-    const int qexp = qmax > 0.f ? 141 - (int)((__float_as_uint(qmax) >> 23) & 0xffu) : 0;  // 14 - floor(log2 qmax)
-    const float sc = a.score_scale * ldexpf(1.f, -qexp);  // undoes the query's power-of-two scale
+    // Query operand, score scale and codebook tables: compiler-visible loads, issued
+    // before the first copy (the compiler does not count the copies, so a wait it
+    // inserts for its own load would wait for them too).
     u32x4 qop[4];
+    {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
     #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        float e[8];
-    #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = ldexpf(qv[c][i], qexp);
-        qop[c].x = pack2<RQ_DTYPE_F16>(e[0], e[2]);
-        qop[c].y = pack2<RQ_DTYPE_F16>(e[4], e[6]);
-        qop[c].z = pack2<RQ_DTYPE_F16>(e[1], e[3]);
-        qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
+        for (int c = 0; c < 4; ++c) {
+            const uint4 w = src[c];
+            qop[c] = u32x4{w.x, w.y, w.z, w.w};
+        }
     }
-    // Compiler-visible global loads go before the next copy: the compiler does not
-    // count the copies, so a wait it inserts for its own load waits for them too.
+    const float sc = a.qscale[(seq * a.H + h) * 16 + col];
     const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
     const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
-    __syncthreads();  // every wave is done with its q slice before tile 1 lands in stage 1
+
+    issue(0, stage0);
+
     if (n_tiles > 1) issue(kTile, stage1);
 
     f32x4 acc[8];
@@ -517,8 +585,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
 
 // Merge the chunk partials of (seq, query head): log-sum-exp over chunks, round
 // to the query dtype (the reference's out_rot, fused_paged_rq_decode.py:201-206),
-// rotate back by R in fp32 and round again (:308).  One wave per query head,
-// two head dims per lane; the chunk loop issues its loads four at a time.
+// rotate back by R in fp32 and round again (:308).  One wave per query head:
+// lane c first loads chunk c's (m, l) (64 chunks per pass), the weights are
+// formed with wave reductions, then the accumulators (two head dims per lane)
+// are summed with eight chunks' loads in flight.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.y;
@@ -532,33 +602,42 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const float *ml = a.part_ml + (seq * a.max_chunks) * (int64_t)a.HQ * 2 + hq * 2;
     const float *pa = a.part_acc + (seq * a.max_chunks) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, ml[c * cs_ml]);
-    float lsum = 0.f, o0 = 0.f, o1 = 0.f;
-    int c = 0;
-    for (; c + 4 <= nch; c += 4) {
-        float w[4], l[4];
-        float2 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            w[u] = ml[(c + u) * cs_ml];
-            l[u] = ml[(c + u) * cs_ml + 1];
-            v[u] = reinterpret_cast<const float2 *>(pa + (c + u) * cs_acc)[lane];
+    float lsum = 0.f, o0 = 0.f, o1 = 0.f, M = -INFINITY;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        const float2 v = c < nch ? *reinterpret_cast<const float2 *>(ml + c * cs_ml) : make_float2(-INFINITY, 0.f);
+        float pm = v.x;
+        for (int o = 32; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
+        const float Mn = fmaxf(M, pm);
+        const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // -inf - finite -> 0 on the first pass
+        o0 *= alpha;
+        o1 *= alpha;
+        lsum *= alpha;
+        M = Mn;
+        const float w = c < nch ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
+        float wl = w * v.y;
+        for (int o = 32; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
+        lsum += wl;
+        const int n = min(64, nch - c0);
+        const float *pc = pa + c0 * cs_acc;
+        int i = 0;
+        for (; i + 8 <= n; i += 8) {
+            float2 x[8];
+    #pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = reinterpret_cast<const float2 *>(pc + (i + u) * cs_acc)[lane];
+    #pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i + u));
+                o0 += wu * x[u].x;
+                o1 += wu * x[u].y;
+            }
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float e = exp2f(w[u] - M);
-            lsum += e * l[u];
-            o0 += e * v[u].x;
-            o1 += e * v[u].y;
+        for (; i < n; ++i) {
+            const float2 x = reinterpret_cast<const float2 *>(pc + i * cs_acc)[lane];
+            const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+            o0 += wu * x.x;
+            o1 += wu * x.y;
         }
-    }
-    for (; c < nch; ++c) {
-        const float e = exp2f(ml[c * cs_ml] - M);
-        lsum += e * ml[c * cs_ml + 1];
-        const float2 v = reinterpret_cast<const float2 *>(pa + c * cs_acc)[lane];
-        o0 += e * v.x;
-        o1 += e * v.y;
     }
     const float inv = nch > 0 ? 1.f / lsum : 0.f;  // empty context -> zeros (reference: acc 0, l 1)
     orot[2 * lane] = Elem<DT>::to_f32(Elem<DT>::from_f32(o0 * inv));
@@ -585,7 +664,7 @@ static int pick_chunk(int64_t num_seqs, int64_t max_seq_len) {
 
 template <int DT, int KB, int VB, int HPW>
 static void launch_decode_h(const DecodeArgs &a, int64_t num_seqs, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3(a.max_chunks, (unsigned)num_seqs, a.H / a.hpw),
+    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)(num_seqs * a.max_chunks), 1, a.H / a.hpw),
                        dim3(64 * a.hpw), lds, st, a);
 }
 
@@ -613,8 +692,10 @@ extern "C" int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num
     int chunk = pick_chunk(num_seqs, max_seq_len);
     int64_t max_chunks = (max_seq_len + chunk - 1) / chunk;
     if (max_chunks < 1) max_chunks = 1;
-    int64_t n = num_seqs * max_chunks * num_q_heads;
-    return n * ((int64_t)head_dim + 2) * (int64_t)sizeof(float) + 256;
+    // partials (acc + m/l) | query operands (<= num_q_heads kv heads) | score scales | work list
+    const int64_t n = num_seqs * max_chunks * num_q_heads;
+    return n * ((int64_t)head_dim + 2) * 4 + num_seqs * num_q_heads * (64 * 16 * 4 + 16 * 4) +
+           num_seqs * max_chunks * 16 + 256;
 }
 
 extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
@@ -674,6 +755,10 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.max_chunks = (int)(max_chunks < 1 ? 1 : max_chunks);
     a.part_acc = reinterpret_cast<float *>(workspace);
     a.part_ml = a.part_acc + num_seqs * (int64_t)a.max_chunks * num_q_heads * kD;
+    a.qops = reinterpret_cast<uint32_t *>(a.part_ml + num_seqs * (int64_t)a.max_chunks * num_q_heads * 2);
+    a.qscale = reinterpret_cast<float *>(a.qops + num_seqs * (int64_t)num_kv_heads * 64 * 16);
+    a.items_out = reinterpret_cast<int4 *>(a.qscale + num_seqs * (int64_t)num_kv_heads * 16);
+    a.items = a.items_out;
     a.num_blocks = num_blocks;
     a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
     a.inv_block_size = 1.f / (float)block_size;
@@ -694,9 +779,14 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     const size_t lds = 2 * (size_t)a.stage_bytes + 4 * (size_t)bt_entries;
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
+        const dim3 pgrid((unsigned)num_seqs), pblock(64 * std::min(a.H, kMaxWaves));
+        if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, 0, st, a);
+        else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, 0, st, a);
+        int rc = check_launch("decode_prep_kernel");
+        if (rc) return rc;
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, num_seqs, lds, kb, vb, st);
         else launch_decode_bits<RQ_DTYPE_F16>(a, num_seqs, lds, kb, vb, st);
-        int rc = check_launch("decode_kernel");
+        rc = check_launch("decode_kernel");
         if (rc) return rc;
     }
     dim3 mgrid((num_q_heads + 3) / 4, (unsigned)num_seqs);

@@ -250,28 +250,18 @@ _ws_cache: dict = {}
 
 
 def _workspace(dev, nbytes: int) -> torch.Tensor:
-    """Zero-filled decode scratch (its per-sequence counters must start at zero;
-    every call leaves them zero again), grown on demand and reused."""
+    """Decode scratch (split-KV partials, query operands, work list), grown on
+    demand and reused; every call rewrites what it reads."""
     buf = _ws_cache.get(dev)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         _ws_cache[dev] = buf
     return buf
 
 
-def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
-                          seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
-                          rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
-                          sm_scale: float | None = None, out: torch.Tensor | None = None,
-                          max_seq_len: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Fused paged decode attention; q (num_seqs, H_Q, D) in original space -> output in original space.
-
-    Reference: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312 (same
-    arguments; `max_seq_len` optionally bounds seq_lens and sizes the split-KV
-    grid, default block_table.shape[1] * block_size; `workspace` optionally
-    supplies the split-KV scratch, a uint8 device tensor that must be zero
-    before its first use -- the call leaves it reusable).
-    """
+def _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads,
+                       head_dim, block_size, sm_scale, out, max_seq_len, workspace):
+    """Validated argument tuple of one rq_fused_decode call (tensors it creates are returned to keep them alive)."""
     num_seqs, H_Q, D = q.shape
     assert D == head_dim, f"D={D} != head_dim={head_dim}"
     assert H_Q % num_kv_heads == 0
@@ -297,14 +287,54 @@ def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: 
     R = _f32(rotation, dev)
     kc, vc = _f32(centroids_k, dev), _f32(centroids_v, dev)
     sl = seq_lens.contiguous()
-    rc = L.rq_fused_decode(
-        q.data_ptr(), _lib.dtype_code(q.dtype), num_seqs, H_Q, q.stride(0), q.stride(1), kv_cache.data_ptr(),
-        kv_cache.shape[0], block_size, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
-        block_table.data_ptr(), MB, block_table.stride(0), sl.data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(),
-        vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0),
-        out.stride(1), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
-    _lib.check(rc, "rq_fused_decode")
+    args = (q.data_ptr(), _lib.dtype_code(q.dtype), num_seqs, H_Q, q.stride(0), q.stride(1), kv_cache.data_ptr(),
+            kv_cache.shape[0], block_size, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
+            block_table.data_ptr(), MB, block_table.stride(0), sl.data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(),
+            vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0),
+            out.stride(1), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+    return L, args, out, (q, block_table, R, kc, vc, sl, ws)
+
+
+def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                          seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
+                          rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
+                          sm_scale: float | None = None, out: torch.Tensor | None = None,
+                          max_seq_len: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused paged decode attention; q (num_seqs, H_Q, D) in original space -> output in original space.
+
+    Reference: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312 (same
+    arguments; `max_seq_len` optionally bounds seq_lens and sizes the split-KV
+    grid, default block_table.shape[1] * block_size; `workspace` optionally
+    supplies the scratch, a uint8 device tensor of at least
+    rq_fused_decode_workspace_bytes(...) bytes, reusable across calls).
+    """
+    L, args, out, _keep = _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation,
+                                             num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace)
+    _lib.check(L.rq_fused_decode(*args), "rq_fused_decode")
     return out
+
+
+def fused_paged_rq_decode_launcher(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                                   seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
+                                   rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
+                                   sm_scale: float | None = None, out: torch.Tensor | None = None,
+                                   max_seq_len: int | None = None, workspace: torch.Tensor | None = None):
+    """Validate once and return a zero-argument callable that re-issues the same
+    rq_fused_decode call (same buffers, the stream current now) without
+    per-call Python work -- for loops over static buffers such as a benchmark.
+    The callable returns `out`; the tensors must outlive it."""
+    L, args, out, keep = _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation,
+                                            num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace)
+    fn = L.rq_fused_decode
+
+    def launch():
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc, "rq_fused_decode")
+        return out
+
+    launch.keep = keep
+    return launch
 
 
 # ---------------------------------------------------------------------------

@@ -116,3 +116,45 @@ def test_decode_split_invariance():
     one["q"] = case["q"][1:2]
     got_one = run_decode(one)
     assert np.array_equal(got_all[1], got_one[0])
+
+
+def test_decode_graph_replay_matches_eager():
+    """rq_fused_decode captured in a HIP graph: each of several replays, with eager
+    calls on other inputs in between, reproduces the eager result bit for bit."""
+    from rotorquant_vllm import _lib
+    from rotorquant_vllm import kernels as K
+    lens = [700, 4000, 33, 2500]
+    case = decode_case(9, 4, 8, 32, lens)
+    other = decode_case(10, 2, 8, 32, [300, 5000])
+    p = case["p"]
+    dev = torch.device("cuda")
+    args = dict(num_kv_heads=8, head_dim=128, block_size=16, sm_scale=case["sm_scale"])
+    cache, bt, sl = (torch.from_numpy(case[k]).to(dev) for k in ("cache", "bt", "lens"))
+    ocache, obt, osl = (torch.from_numpy(other[k]).to(dev) for k in ("cache", "bt", "lens"))
+    q, oq = case["q"].to(dev), other["q"].to(dev)
+    kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
+    need = _lib.load().rq_fused_decode_workspace_bytes(4, 32, 128, max(lens))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+
+    def call():
+        K.fused_paged_rq_decode(q, cache, bt, sl, kc, vc, R, out=out, max_seq_len=max(lens), workspace=ws, **args)
+
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for _ in range(3):
+        out.zero_()
+        K.fused_paged_rq_decode(oq, ocache, obt, osl, kc, vc, R, max_seq_len=5000, **args)  # eager work between
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
