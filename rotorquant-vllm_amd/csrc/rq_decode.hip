@@ -87,6 +87,8 @@ __device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
     return u32x4{e.x, e.y, o.x, o.y};
 }
 
+struct TileDesc;
+
 struct DecodeArgs {
     const void *q;
     int64_t q_ss, q_sh;
@@ -94,7 +96,6 @@ struct DecodeArgs {
     int64_t stride_block, stride_token;
     int block_size;
     int bs_shift;       // log2(block_size), or -1 when block_size is not a power of two
-    float inv_block_size;
     int H, G, HQ;
     const int32_t *bt;
     int64_t bt_ss;
@@ -105,19 +106,19 @@ struct DecodeArgs {
     const float *R;
     int rot_block;
     float score_scale;  // sm_scale * log2(e)
-    int chunk;          // tokens per workgroup (multiple of kTile)
-    int max_chunks;
-    int max_len;        // min(max_blocks * block_size, max_chunks * chunk): lengths are clamped to it
+    int max_len;        // min(max_blocks * block_size, max_seq_len): lengths are clamped to it
     int64_t num_blocks; // physical blocks; table entries outside [0, num_blocks) read block 0
     int hpw;            // kv heads per workgroup = waves per workgroup (divides H, <= 8)
     int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
     int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
-    const int4 *items;  // work list (decode_prep_kernel)
-    int4 *items_out;
+    int grid_w;         // decode workgroups per kv-head group (the tile ranges)
+    TileDesc *descs;    // [total tiles] (prep kernel)
+    int *tile_prefix;   // [seq] tiles before the sequence
+    int *n_tiles_total;
     uint32_t *qops;     // [seq][H][64 lanes][16] fp16 query operands
     float *qscale;      // [seq][H][16] score scales
-    float *part_acc;    // [seq][chunk][HQ][D]
-    float *part_ml;     // [seq][chunk][HQ][2]
+    float *part_acc;    // [slot][HQ][D], slot = workgroup + seq
+    float *part_ml;     // [slot][HQ][2]
     void *out;
     int64_t o_ss, o_sh;
 };
@@ -165,11 +166,15 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_
 // neither waits for them before unrelated LDS accesses nor counts them: the
 // kernel waits for them itself with s_waitcnt vmcnt.  Lane l writes its bytes
 // at LDS address m0 + l * size (m0 = wave-uniform destination).
-//   copy16: 16 bytes from the uniform base `src` + per-lane 32-bit offset.
-//   copy4:  4 bytes from a per-lane address.
+//   copy16:  16 bytes from the uniform base `src` + per-lane 32-bit offset.
+//   copy16v: 16 bytes from a per-lane address.
+//   copy4:   4 bytes from a per-lane address.
 __device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32_t dst) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "s"(dst)
                  : "memory", "m0");
+}
+__device__ __forceinline__ void copy16v(const uint8_t *src, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
 }
 __device__ __forceinline__ void copy4(const uint8_t *src, uint32_t dst) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
@@ -265,74 +270,118 @@ __device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, 
     __builtin_amdgcn_wave_barrier();
 }
 
-// Per-call preparation, one workgroup per sequence:
-//   * the fp16 query operands (and score scales) of every kv head, stored in
-//     lane order so each decode lane loads its 64 bytes contiguously;
-//   * the work list: items[prefix(seq) + c] = {seq, c, tokens of chunk c}, where
-//     prefix(seq) counts the chunks of the sequences before it.  Entries from
-//     the total up to num_seqs * max_chunks get seq = -1.  Decode workgroup i
-//     takes item i, so the non-empty chunks occupy the first workgroup ids and
-//     spread evenly over the XCDs.
+// Tile descriptor: one 32-token tile of one sequence, written by the prep kernel
+// and read by the decode workgroup that owns the tile.
+struct TileDesc {
+    int32_t seq, tile, valid, pad;  // sequence, tile index inside it, tokens in the tile (1..32)
+    uint64_t off[kTile];            // byte offset of each token's slot (0 past `valid`)
+};
+static_assert(sizeof(TileDesc) == 16 + 8 * kTile, "TileDesc layout");
+constexpr int kDescPieces = (int)sizeof(TileDesc) / 16;  // 16-byte copy pieces per descriptor
+constexpr int kRing = 4;                                   // descriptors staged ahead in LDS
+
+__device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
+    const int L = min(a.seq_lens[b], a.max_len);
+    return L > 0 ? (L + kTile - 1) / kTile : 0;
+}
+
+// Per-call preparation; workgroup (seq, y):
+//   * y == 0: the fp16 query operands (and score scales) of every kv head of the
+//     sequence, stored in lane order so each decode lane loads its 64 bytes;
+//   * all: the tile descriptors of the sequence's tiles y, y + gridDim.y, ...,
+//     placed after the tiles of the sequences before it (the tiles of all
+//     sequences, in order, form the work the decode kernel splits evenly);
+//   * tile_prefix[seq] = tiles before the sequence; the last sequence also
+//     stores the total.
 template <int DT>
 __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.x;
+    const int y = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
     __shared__ __align__(16) uint16_t wq_all[kMaxWaves][16 * kD];
     __shared__ int part[kMaxWaves];
-    for (int h = wave; h < a.H; h += nw) {
-        u32x4 qop[4];
-        float sc;
-        query_operand<DT>(a, seq, h, wq_all[wave], qop, sc);
-        uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
+    if (y == 0) {
+        for (int h = wave; h < a.H; h += nw) {
+            u32x4 qop[4];
+            float sc;
+            query_operand<DT>(a, seq, h, wq_all[wave], qop, sc);
+            uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
     #pragma unroll
-        for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
-        if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
+            for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
+            if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
+        }
     }
-    // chunks of the sequences before this one
-    auto nch = [&](int64_t b) {
-        const int L = min(a.seq_lens[b], a.max_len);
-        return L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
-    };
     int cnt = 0;
-    for (int64_t b = threadIdx.x; b < seq; b += blockDim.x) cnt += nch(b);
+    for (int64_t b = threadIdx.x; b < seq; b += blockDim.x) cnt += seq_tiles(a, b);
     for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o);
     if (lane == 0) part[wave] = cnt;
     __syncthreads();
     int prefix = 0;
     for (int w = 0; w < nw; ++w) prefix += part[w];
-    const int mine = nch(seq);
+    const int n = seq_tiles(a, seq);
     const int L = min(a.seq_lens[seq], a.max_len);
-    for (int c = threadIdx.x; c < mine; c += blockDim.x)
-        a.items_out[prefix + c] = make_int4((int)seq, c, min(L - c * a.chunk, a.chunk), 0);
-    if (seq == gridDim.x - 1) {
-        const int64_t cap = (int64_t)gridDim.x * a.max_chunks;
-        for (int64_t i = prefix + mine + threadIdx.x; i < cap; i += blockDim.x) a.items_out[i] = make_int4(-1, 0, 0, 0);
+    if (y == 0 && threadIdx.x == 0) {
+        a.tile_prefix[seq] = prefix;
+        if (seq == gridDim.x - 1) *a.n_tiles_total = prefix + n;
+    }
+    const int32_t *bt_row = a.bt + seq * a.bt_ss;
+    // four consecutive tokens per thread and step (block-table loads issued together)
+    for (int j0 = 4 * (y * (int)blockDim.x + (int)threadIdx.x); j0 < n * kTile; j0 += 4 * gridDim.y * blockDim.x) {
+        int phys[4];
+    #pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int pos = j0 + u;
+            const int lb = a.bs_shift >= 0 ? pos >> a.bs_shift : pos / a.block_size;
+            phys[u] = pos < L ? bt_row[lb] : 0;
+        }
+        TileDesc *d = a.descs + prefix + j0 / kTile;
+        uint64_t off[4];
+    #pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int pos = j0 + u;
+            const int in_blk = a.bs_shift >= 0 ? (pos & (a.block_size - 1)) : pos % a.block_size;
+            const int64_t p = (phys[u] < 0 || phys[u] >= a.num_blocks) ? 0 : phys[u];
+            off[u] = pos < L ? (uint64_t)(p * a.stride_block + (int64_t)in_blk * a.stride_token) : 0;
+        }
+        uint4 *o4 = reinterpret_cast<uint4 *>(&d->off[j0 % kTile]);
+        o4[0] = make_uint4((uint32_t)off[0], (uint32_t)(off[0] >> 32), (uint32_t)off[1], (uint32_t)(off[1] >> 32));
+        o4[1] = make_uint4((uint32_t)off[2], (uint32_t)(off[2] >> 32), (uint32_t)off[3], (uint32_t)(off[3] >> 32));
+        if (j0 % kTile == 0) {
+            d->seq = (int32_t)seq;
+            d->tile = j0 / kTile;
+            d->valid = min(kTile, L - j0);
+            d->pad = 0;
+        }
     }
 }
 
-// Workgroup = (chunk, sequence, kv-head group of hpw heads); wave w owns kv
-// head h0 + w.  32-token tiles are staged in LDS by direct global->LDS copies
-// into two stages, two tiles ahead of the compute:
+// Decode.  The tiles of all sequences, in order, are split into gridDim.x equal
+// contiguous ranges; workgroup w (with blockIdx.z selecting a group of hpw kv
+// heads, one wave per head) takes range w, so every workgroup gets the same work
+// whatever the sequence lengths.  A range covers one or more sequence segments;
+// each segment ends in a partial (m, l, acc) at slot w + seq, which is unique
+// because ranges are contiguous and ordered.
+//
+// Data movement: tile descriptors are copied into an LDS ring four tiles ahead
+// and each tile's K/V index runs and norms two tiles ahead, into two stages:
 //   stage layout: token t at t * tok_stride: [K idx of the hpw heads | V idx]
 //                 then norm rows (2*hpw x 32 fp32): K norms of each head, V norms.
 // One copy instruction moves a whole token's K+V index run (8*hpw x 16 B), so
-// every request covers whole cache lines.  Iteration i: wait for tile i (tile
-// i+1 stays in flight), barrier, read this wave's operands into registers,
-// barrier, refill the stage with tile i+2, compute tile i from registers.
+// every request covers whole cache lines.  Iteration t: wait for tile t (tile
+// t+1 stays in flight), barrier, read this wave's operands into registers,
+// barrier, copy descriptor t+4 and tile t+2, compute tile t from registers.
 // Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
 constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
 
 template <int DT, int KB, int VB, int HPW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
-    const int4 item = a.items[blockIdx.x];
-    if (item.x < 0) return;
-    const int64_t seq = item.x;
-    const int chunk_id = item.y;
-    const int t_begin = chunk_id * a.chunk;
-    const int n_tok = item.z;
-    const int n_tiles = (n_tok + kTile - 1) / kTile;
+    const int w = blockIdx.x;
+    const int NT = *a.n_tiles_total;
+    const int k0 = (int)((int64_t)w * NT / gridDim.x);
+    const int nt = (int)((int64_t)(w + 1) * NT / gridDim.x) - k0;
+    if (nt <= 0) return;
 
     // HPW > 0: heads per workgroup fixed at compile time (LDS offsets become immediates)
     const int hpw = HPW > 0 ? HPW : a.hpw;
@@ -346,59 +395,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int TS = HPW > 0 ? 128 * HPW + 16 : a.tok_stride;
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
+    const int tl = lane & 31;  // token of this lane in a tile (slot base, norm copy)
 
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *const stage0 = lds;
     uint8_t *const stage1 = lds + stage_bytes;
-    int32_t *const bt_lds = reinterpret_cast<int32_t *>(lds + 2 * stage_bytes);
-    const int tl = lane & 31;  // token of this lane in a tile (slot base, norm copy)
+    const TileDesc *const ring = reinterpret_cast<const TileDesc *>(lds + 2 * stage_bytes);
 
-    // Block index and in-block offset of token t0 + tl (the tile start t_begin + t0
-    // is split once; the lane's small remainder is divided with a float
-    // reciprocal and one correction each way when block_size is not a power of two).
-    auto locate = [&](int t0, int &lb, int &off) {
-        const int pos = t_begin + t0;
-        if (a.bs_shift >= 0) {
-            lb = (pos + tl) >> a.bs_shift;
-            off = (pos + tl) & (a.block_size - 1);
-        } else {
-            const int lb0 = pos / a.block_size;
-            const int x = pos - lb0 * a.block_size + tl;
-            int dq = (int)((float)x * a.inv_block_size);
-            dq += (dq + 1) * a.block_size <= x ? 1 : 0;
-            dq -= dq * a.block_size > x ? 1 : 0;
-            lb = lb0 + dq;
-            off = x - dq * a.block_size;
-        }
+    // Descriptor of local tile i -> ring slot i % kRing (wave 0, one copy).
+    auto issue_desc = [&](int i) {
+        if (wave == 0 && lane < kDescPieces)
+            copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * lane, lds_addr(reinterpret_cast<const uint8_t *>(ring + i % kRing)));
     };
-    // This chunk's block-table entries, staged once (out-of-range physical
-    // blocks read block 0).
-    int lb_first;
-    {
-        const int pos = t_begin;
-        lb_first = a.bs_shift >= 0 ? pos >> a.bs_shift : pos / a.block_size;
-        const int last = t_begin + n_tok - 1;
-        const int lb_end = (a.bs_shift >= 0 ? last >> a.bs_shift : last / a.block_size) + 1;
-        const int32_t *bt_row = a.bt + seq * a.bt_ss;
-        for (int k = threadIdx.x; k < lb_end - lb_first; k += blockDim.x) {
-            const int p = bt_row[lb_first + k];
-            bt_lds[k] = (p < 0 || p >= a.num_blocks) ? 0 : p;
-        }
-    }
-    __syncthreads();
-    // Byte offset of the slot of token t0 + tl (token past the end: offset 0).
-    auto tok_base = [&](int t0) -> uint64_t {
-        if (t0 + tl >= n_tok) return 0;
-        int lb, off;
-        locate(t0, lb, off);
-        const int64_t p = bt_lds[lb - lb_first];
-        return (uint64_t)(p * a.stride_block + (int64_t)off * a.stride_token);
-    };
-    // Copies of the tile starting at t0 into stage sb.  Per wave and full tile:
-    // kTile / hpw token copies and one norm copy.
-    auto issue = [&](int t0, const uint8_t *sb) {
-        const uint64_t base = tok_base(t0);
-        const int valid = min(kTile, n_tok - t0);
+    // Copies of local tile i into stage sb.  Per wave and full tile: kTile / hpw
+    // token copies and one norm copy.
+    auto issue = [&](int i, const uint8_t *sb) {
+        const TileDesc &d = ring[i % kRing];
+        const int valid = __builtin_amdgcn_readfirstlane(d.valid);
+        const uint64_t base = d.off[tl];
         const uint32_t dst = lds_addr(sb);
         const uint32_t kv_src = lane < 4 * hpw ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * lane)
                                                : (uint32_t)(SL.v_idx + 64 * h0 + 16 * (lane - 4 * hpw));
@@ -406,48 +420,113 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
             if (lane < 8 * hpw) copy16(tok, kv_src, dst + tt * TS);
         }
-        // norm rows 2*wave, 2*wave+1 (row j < hpw: K norm of head h0+j, else V norm of head h0+j-hpw)
-        const int nrow = 2 * wave + (lane >> 5);
-        const uint32_t norm_src = nrow < hpw ? (uint32_t)(SL.k_norm + 4 * (h0 + nrow))
-                                             : (uint32_t)(SL.v_norm + 4 * (h0 + nrow - hpw));
-        if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
+        if constexpr (HPW > 0) {
+            // Norms in 16-byte pieces: a token's K norms and V norms of the hpw heads
+            // are NP pieces; one copy covers TPI tokens (waves 0 .. kTile/TPI - 1).
+            // Lane l takes token slot q' = l / NP, piece l % NP, where slot q' holds
+            // token 4 (q' % (TPI/4)) + q' / (TPI/4) of the copy's token range: the
+            // norms of tokens 4g + i (fixed i) then land 16 NP g bytes apart (distinct
+            // banks) and tokens i, i+1, ... 256 bytes apart.
+            constexpr int NP = HPW / 2, TPI = 64 / NP;
+            if (wave < kTile / TPI) {
+                const int qs = lane / NP, p = lane % NP;
+                const int tt = wave * TPI + 4 * (qs % (TPI / 4)) + qs / (TPI / 4);
+                const uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
+                                                : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
+                if (tt < valid) copy16v(a.cache + d.off[tt] + src, dst + norm_off + 1024 * wave);
+            }
+        } else {
+            // norm rows 2*wave, 2*wave+1 (row j < hpw: K norm of head h0+j, else V norm of head h0+j-hpw)
+            const int nrow = 2 * wave + (lane >> 5);
+            const uint32_t norm_src = nrow < hpw ? (uint32_t)(SL.k_norm + 4 * (h0 + nrow))
+                                                 : (uint32_t)(SL.v_norm + 4 * (h0 + nrow - hpw));
+            if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
+        }
     };
 
-    // Query operand, score scale and codebook tables: compiler-visible loads, issued
-    // before the first copy (the compiler does not count the copies, so a wait it
-    // inserts for its own load would wait for them too).
-    u32x4 qop[4];
-    {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
-    #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 w = src[c];
-            qop[c] = u32x4{w.x, w.y, w.z, w.w};
-        }
-    }
-    const float sc = a.qscale[(seq * a.H + h) * 16 + col];
+    for (int i = 0; i < min(nt, kRing); ++i) issue_desc(i);
+    wait_copies<0>();
+    __syncthreads();
+
     const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
     const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
 
-    issue(0, stage0);
-
-    if (n_tiles > 1) issue(kTile, stage1);
-
+    // Per-segment state.  The query operand and score scale are compiler-visible
+    // loads, issued at a segment start before further copies (the compiler does
+    // not count the copies, so its wait for these loads also waits for them).
+    int seq = __builtin_amdgcn_readfirstlane(ring[0].seq);
+    u32x4 qop[4];
+    float sc;
     f32x4 acc[8];
+    float m_run, l_run;
+    int e_run;
+    auto begin_segment = [&]() {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.qops + (((int64_t)seq * a.H + h) * 64 + lane) * 16);
     #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;  // running max (log2 domain) for query head `col`
-    float l_run = 0.f;        // this lane's partial sum of p
-    int e_run = -126;         // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = src[c];
+            qop[c] = u32x4{v.x, v.y, v.z, v.w};
+        }
+        sc = a.qscale[((int64_t)seq * a.H + h) * 16 + col];
+    #pragma unroll
+        for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m_run = -INFINITY;  // running max (log2 domain) for query head `col`
+        l_run = 0.f;        // this lane's partial sum of p
+        e_run = -126;       // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
+    };
+    // Partial of the current segment -> slot w + seq.
+    auto end_segment = [&]() {
+        const float lsum = rows_sum(l_run);
+        if (col < a.G) {
+            const int hq = h * a.G + col;
+            const int64_t pidx = (int64_t)(w + seq) * a.HQ + hq;
+            float *pa = a.part_acc + pidx * kD;
+            // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
+            const float es = ldexpf(1.f, e_run);
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
+                float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
+                float4 *dst = reinterpret_cast<float4 *>(pa + 8 * (4 * g + i));
+                dst[0] = lo;
+                dst[1] = hi;
+            }
+            if (g == 0) {
+                a.part_ml[pidx * 2] = m_run;
+                a.part_ml[pidx * 2 + 1] = lsum;
+            }
+        }
+    };
+    begin_segment();
 
-    for (int it = 0; it < n_tiles; ++it) {
-        const int t0 = it * kTile;
-        const uint8_t *const sb = (it & 1) ? stage1 : stage0;
-        // Tile it landed?  Tile it+1 (issued later) may stay in flight when it is full.
-        if (HPW > 0 && t0 + 2 * kTile <= n_tok) wait_copies<kTile / (HPW > 0 ? HPW : 1) + 1>();
-        else wait_copies<0>();
+    issue(0, stage0);
+    if (nt > 1) issue(1, stage1);
+
+    for (int t = 0; t < nt; ++t) {
+        const uint8_t *const sb = (t & 1) ? stage1 : stage0;
+        // Tile t landed?  Issued after its copies: descriptor t+3 (wave 0, from
+        // iteration t-1; the prologue issues descriptors 0..3 before tile 0) and tile
+        // t+1, which may stay in flight when it is full.
+        if (HPW > 0 && t + 1 < nt && __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid) == kTile) {
+            // per wave and full tile: kTile / HPW token copies, plus one norm copy on
+            // the first kTile / (128 / HPW) waves
+            constexpr int NC = kTile / (HPW > 0 ? HPW : 1);
+            const int extra = (wave < kTile * (HPW > 0 ? HPW : 1) / 128 ? 1 : 0) + (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
+            if (extra == 2) wait_copies<NC + 2>();
+            else if (extra == 1) wait_copies<NC + 1>();
+            else wait_copies<NC>();
+        } else {
+            wait_copies<0>();
+        }
         __syncthreads();
 
+        const int tseq = __builtin_amdgcn_readfirstlane(ring[t % kRing].seq);
+        const int valid = __builtin_amdgcn_readfirstlane(ring[t % kRing].valid);
+        if (tseq != seq) {  // a new sequence starts at this tile
+            end_segment();
+            seq = tseq;
+            begin_segment();
+        }
         // ---- this wave's operands of the tile ------------------------------------
         const uint8_t *kb = sb + col * TS + 64 * wave + 16 * g;                 // token col, K bytes 16g..
         const uint8_t *vb = sb + 4 * g * TS + 64 * hpw + 64 * wave + 4 * col;  // token 4g, V dword col
@@ -457,20 +536,38 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         uint32_t vw[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
-        const float4 nk0 = *reinterpret_cast<const float4 *>(nb);
-        const float4 nk1 = *reinterpret_cast<const float4 *>(nb + 64);
-        const float4 nv0 = *reinterpret_cast<const float4 *>(nb + 128 * hpw);
-        const float4 nv1 = *reinterpret_cast<const float4 *>(nb + 128 * hpw + 64);
-        __syncthreads();  // the stage is free once every wave holds its operands
+        float4 nk0, nk1, nv0, nv1;
+        if constexpr (HPW > 0) {
+            // token 4g + i at 256 i + 16 NP q (+1024 for tokens 16.. when TPI = 16),
+            // q = g (tokens < 16) or 4 + g (tokens >= 16 when TPI = 32)
+            constexpr int NP = HPW / 2, TPI = 64 / NP;
+            const float *n0 = reinterpret_cast<const float *>(sb + norm_off + 16 * NP * g + 16 * (wave / 4) + 4 * (wave % 4));
+            const int hi = TPI == 16 ? 1024 : 16 * NP * 4;  // tokens 16..31
+            const int vo = 16 * (NP / 2);                     // V norms after the K pieces
+            auto ld4 = [&](int o) {
+                const float *p = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(n0) + o);
+                return make_float4(p[0], p[64], p[128], p[192]);
+            };
+            nk0 = ld4(0);
+            nk1 = ld4(hi);
+            nv0 = ld4(vo);
+            nv1 = ld4(vo + hi);
+        } else {
+            nk0 = *reinterpret_cast<const float4 *>(nb);
+            nk1 = *reinterpret_cast<const float4 *>(nb + 64);
+            nv0 = *reinterpret_cast<const float4 *>(nb + 128 * hpw);
+            nv1 = *reinterpret_cast<const float4 *>(nb + 128 * hpw + 64);
+        }
+        __syncthreads();  // the stage and descriptor slot t are free once every wave holds its operands
 
-        // ---- tile it+2 into the same stage -------------------------------------------
-        if (t0 + 2 * kTile < n_tok) issue(t0 + 2 * kTile, sb);
+        // ---- descriptor t+4 and tile t+2 ---------------------------------------------
+        if (t + kRing < nt) issue_desc(t + kRing);
+        if (t + 2 < nt) issue(t + 2, sb);
 
         // ---- tokens past the end were not copied: their stage bytes are stale.  Zero
         // their norms and V indices (a stale nibble >= 8 would look up a NaN in an
         // 8-entry table, and NaN * 0 would reach the accumulator); their scores are
         // masked below.
-        const int valid = min(kTile, n_tok - t0);
         float nk[8] = {nk0.x, nk0.y, nk0.z, nk0.w, nk1.x, nk1.y, nk1.z, nk1.w};
         float nv[8] = {nv0.x, nv0.y, nv0.z, nv0.w, nv1.x, nv1.y, nv1.z, nv1.w};
         if (valid < kTile) {
@@ -560,35 +657,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         }
     }
 
-    // ---- partials ------------------------------------------------------------
-    l_run = rows_sum(l_run);
-    if (col < a.G) {
-        const int hq = h * a.G + col;
-        const int64_t pidx = (seq * a.max_chunks + chunk_id) * a.HQ + hq;
-        float *pa = a.part_acc + pidx * kD;
-        // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
-        const float es = ldexpf(1.f, e_run);
-    #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
-            float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
-            float4 *dst = reinterpret_cast<float4 *>(pa + 8 * (4 * g + i));
-            dst[0] = lo;
-            dst[1] = hi;
-        }
-        if (g == 0) {
-            a.part_ml[pidx * 2] = m_run;
-            a.part_ml[pidx * 2 + 1] = l_run;
-        }
-    }
+    end_segment();
 }
 
-// Merge the chunk partials of (seq, query head): log-sum-exp over chunks, round
+// Merge the partials of (seq, query head): log-sum-exp over the segments, round
 // to the query dtype (the reference's out_rot, fused_paged_rq_decode.py:201-206),
 // rotate back by R in fp32 and round again (:308).  One wave per query head:
-// lane c first loads chunk c's (m, l) (64 chunks per pass), the weights are
+// lane c first loads segment c's (m, l) (64 segments per pass), the weights are
 // formed with wave reductions, then the accumulators (two head dims per lane)
-// are summed with eight chunks' loads in flight.
+// are summed with eight segments' loads in flight.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.y;
@@ -597,15 +674,30 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     __shared__ float orot_all[4][kD];
     float *orot = orot_all[wave];
     if (hq >= a.HQ) return;
-    const int L = min(a.seq_lens[seq], a.max_len);
-    const int nch = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
-    const float *ml = a.part_ml + (seq * a.max_chunks) * (int64_t)a.HQ * 2 + hq * 2;
-    const float *pa = a.part_acc + (seq * a.max_chunks) * (int64_t)a.HQ * kD + hq * kD;
+    // Workgroups whose tile ranges cover the sequence: workgroup w owns tiles
+    // [w NT / G, (w+1) NT / G), so tile t belongs to w(t) = ((t + 1) G - 1) / NT.
+    // Partials sit at slots w + seq for w in [w(first tile), w(last tile)];
+    // workgroups with an empty range (more workgroups than tiles) wrote nothing.
+    const int n = seq_tiles(a, seq);
+    int nch = 0, w_lo = 0;
+    int64_t NT = 1, G = 1;
+    if (n > 0) {
+        NT = *a.n_tiles_total;
+        G = a.grid_w;
+        const int64_t P = a.tile_prefix[seq];
+        w_lo = (int)(((P + 1) * G - 1) / NT);
+        nch = (int)(((P + n) * G - 1) / NT) - w_lo + 1;
+    }
+    auto has_tiles = [&](int64_t w) { return (w + 1) * NT / G > w * NT / G; };
+    const float *ml = a.part_ml + (w_lo + seq) * (int64_t)a.HQ * 2 + hq * 2;
+    const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
     float lsum = 0.f, o0 = 0.f, o1 = 0.f, M = -INFINITY;
     for (int c0 = 0; c0 < nch; c0 += 64) {
         const int c = c0 + lane;
-        const float2 v = c < nch ? *reinterpret_cast<const float2 *>(ml + c * cs_ml) : make_float2(-INFINITY, 0.f);
+        const bool ok = c < nch && has_tiles(w_lo + c);
+        const uint64_t okm = __ballot(ok);
+        const float2 v = ok ? *reinterpret_cast<const float2 *>(ml + c * cs_ml) : make_float2(-INFINITY, 0.f);
         float pm = v.x;
         for (int o = 32; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
         const float Mn = fmaxf(M, pm);
@@ -614,7 +706,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         o1 *= alpha;
         lsum *= alpha;
         M = Mn;
-        const float w = c < nch ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
+        const float w = ok ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
         float wl = w * v.y;
         for (int o = 32; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
         lsum += wl;
@@ -624,7 +716,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         for (; i + 8 <= n; i += 8) {
             float2 x[8];
     #pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = reinterpret_cast<const float2 *>(pc + (i + u) * cs_acc)[lane];
+            for (int u = 0; u < 8; ++u)
+                x[u] = (okm >> (i + u)) & 1 ? reinterpret_cast<const float2 *>(pc + (i + u) * cs_acc)[lane] : make_float2(0.f, 0.f);
     #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i + u));
@@ -633,6 +726,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
             }
         }
         for (; i < n; ++i) {
+            if (!((okm >> i) & 1)) continue;
             const float2 x = reinterpret_cast<const float2 *>(pc + i * cs_acc)[lane];
             const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
             o0 += wu * x.x;
@@ -656,32 +750,77 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     reinterpret_cast<uint32_t *>(dst)[lane] = packed;
 }
 
-static int pick_chunk(int64_t num_seqs, int64_t max_seq_len) {
-    int64_t c = 256;
-    while (c < 16384 && num_seqs * ((max_seq_len + c - 1) / c) > 4096) c *= 2;
-    return (int)c;
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
+
+// Decode workgroups per kv-head group: as many as are resident at once.
+template <int DT, int KB, int VB, int HPW>
+static int decode_grid(const DecodeArgs &a, size_t lds) {
+    static int per_cu[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    dev = dev < 0 || dev >= 64 ? 0 : dev;
+    if (per_cu[dev] == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW>),
+                                                          64 * a.hpw, lds) != hipSuccess || nb <= 0)
+            nb = 1;
+        per_cu[dev] = std::min(nb, kMaxWgPerCu);
+    }
+    const int groups = a.H / a.hpw;
+    return std::max(1, per_cu[dev] * device_cus() / groups);
 }
 
 template <int DT, int KB, int VB, int HPW>
-static void launch_decode_h(const DecodeArgs &a, int64_t num_seqs, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)(num_seqs * a.max_chunks), 1, a.H / a.hpw),
-                       dim3(64 * a.hpw), lds, st, a);
+static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st) {
+    a.grid_w = decode_grid<DT, KB, VB, HPW>(a, lds);
+    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw), lds,
+                       st, a);
 }
 
 template <int DT, int KB, int VB>
-static void launch_decode(const DecodeArgs &a, int64_t num_seqs, size_t lds, hipStream_t st) {
-    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, num_seqs, lds, st);
-    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, num_seqs, lds, st);
-    else launch_decode_h<DT, KB, VB, 0>(a, num_seqs, lds, st);
+static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st) {
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, lds, st);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, lds, st);
+    else launch_decode_h<DT, KB, VB, 0>(a, lds, st);
 }
 
 template <int DT>
-static void launch_decode_bits(const DecodeArgs &a, int64_t num_seqs, size_t lds, int kb, int vb, hipStream_t st) {
-    if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, num_seqs, lds, st);
-    else if (kb == 3) launch_decode<DT, 3, 4>(a, num_seqs, lds, st);
-    else if (vb == 3) launch_decode<DT, 4, 3>(a, num_seqs, lds, st);
-    else launch_decode<DT, 4, 4>(a, num_seqs, lds, st);
+static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, hipStream_t st) {
+    if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st);
+    else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st);
+    else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st);
+    else launch_decode<DT, 4, 4>(a, lds, st);
 }
+
+// Workspace layout (256-byte aligned regions).
+struct DecodeWorkspace {
+    int64_t part_acc, part_ml, qops, qscale, descs, tile_prefix, n_tiles, total;
+    DecodeWorkspace(int64_t num_seqs, int64_t num_q_heads, int64_t max_seq_len) {
+        auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+        const int64_t slots = (int64_t)kMaxWgPerCu * device_cus() + num_seqs;
+        const int64_t max_tiles = num_seqs * ((max_seq_len + kTile - 1) / kTile);
+        part_acc = 0;
+        part_ml = al(part_acc + slots * num_q_heads * kD * 4);
+        qops = al(part_ml + slots * num_q_heads * 2 * 4);
+        qscale = al(qops + num_seqs * num_q_heads * 64 * 16 * 4);  // kv heads <= query heads
+        descs = al(qscale + num_seqs * num_q_heads * 16 * 4);
+        tile_prefix = al(descs + max_tiles * (int64_t)sizeof(TileDesc));
+        n_tiles = al(tile_prefix + num_seqs * 4);
+        total = al(n_tiles + 4);
+    }
+};
 
 }  // namespace rq
 
@@ -689,13 +828,8 @@ using namespace rq;
 
 extern "C" int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num_q_heads, int32_t head_dim,
                                                    int64_t max_seq_len) {
-    int chunk = pick_chunk(num_seqs, max_seq_len);
-    int64_t max_chunks = (max_seq_len + chunk - 1) / chunk;
-    if (max_chunks < 1) max_chunks = 1;
-    // partials (acc + m/l) | query operands (<= num_q_heads kv heads) | score scales | work list
-    const int64_t n = num_seqs * max_chunks * num_q_heads;
-    return n * ((int64_t)head_dim + 2) * 4 + num_seqs * num_q_heads * (64 * 16 * 4 + 16 * 4) +
-           num_seqs * max_chunks * 16 + 256;
+    (void)head_dim;
+    return DecodeWorkspace(num_seqs, num_q_heads, std::max<int64_t>(max_seq_len, 1)).total;
 }
 
 extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
@@ -750,18 +884,19 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.R = rotation;
     a.rot_block = rot_block;
     a.score_scale = sm_scale * kLog2e;
-    a.chunk = pick_chunk(num_seqs, max_seq_len);
-    int64_t max_chunks = (max_seq_len + a.chunk - 1) / a.chunk;
-    a.max_chunks = (int)(max_chunks < 1 ? 1 : max_chunks);
-    a.part_acc = reinterpret_cast<float *>(workspace);
-    a.part_ml = a.part_acc + num_seqs * (int64_t)a.max_chunks * num_q_heads * kD;
-    a.qops = reinterpret_cast<uint32_t *>(a.part_ml + num_seqs * (int64_t)a.max_chunks * num_q_heads * 2);
-    a.qscale = reinterpret_cast<float *>(a.qops + num_seqs * (int64_t)num_kv_heads * 64 * 16);
-    a.items_out = reinterpret_cast<int4 *>(a.qscale + num_seqs * (int64_t)num_kv_heads * 16);
-    a.items = a.items_out;
+    {
+        const DecodeWorkspace W(num_seqs, num_q_heads, std::max<int64_t>(max_seq_len, 1));
+        uint8_t *base = reinterpret_cast<uint8_t *>(workspace);
+        a.part_acc = reinterpret_cast<float *>(base + W.part_acc);
+        a.part_ml = reinterpret_cast<float *>(base + W.part_ml);
+        a.qops = reinterpret_cast<uint32_t *>(base + W.qops);
+        a.qscale = reinterpret_cast<float *>(base + W.qscale);
+        a.descs = reinterpret_cast<TileDesc *>(base + W.descs);
+        a.tile_prefix = reinterpret_cast<int *>(base + W.tile_prefix);
+        a.n_tiles_total = reinterpret_cast<int *>(base + W.n_tiles);
+    }
     a.num_blocks = num_blocks;
     a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-    a.inv_block_size = 1.f / (float)block_size;
     a.hpw = 1;
     for (int d = std::min(a.H, kMaxWaves); d >= 1; --d)
         if (a.H % d == 0) {
@@ -770,22 +905,21 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
         }
     a.tok_stride = 128 * a.hpw + 16;
     a.stage_bytes = kTile * a.tok_stride + 2 * a.hpw * kTile * 4;
-    a.max_len = num_blocks > 0 ? (int)std::min<int64_t>(max_blocks * block_size, (int64_t)a.max_chunks * a.chunk) : 0;
+    a.max_len = num_blocks > 0 ? (int)std::min<int64_t>(max_blocks * block_size, max_seq_len) : 0;
     a.out = out;
     a.o_ss = out_stride_seq;
     a.o_sh = out_stride_head;
-    const int64_t bt_entries = a.chunk / block_size + 2;  // block-table entries one chunk can span
-    RQ_CHECK_ARG(bt_entries <= 8192, "block_size %d too small for %d-token chunks", block_size, a.chunk);
-    const size_t lds = 2 * (size_t)a.stage_bytes + 4 * (size_t)bt_entries;
+    a.grid_w = 1;
+    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc);
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
-        const dim3 pgrid((unsigned)num_seqs), pblock(64 * std::min(a.H, kMaxWaves));
+        const dim3 pgrid((unsigned)num_seqs, 4), pblock(64 * std::min(a.H, kMaxWaves));
         if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, 0, st, a);
         else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, 0, st, a);
         int rc = check_launch("decode_prep_kernel");
         if (rc) return rc;
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, num_seqs, lds, kb, vb, st);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, num_seqs, lds, kb, vb, st);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st);
         rc = check_launch("decode_kernel");
         if (rc) return rc;
     }
