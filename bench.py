@@ -231,6 +231,16 @@ def cpu_baseline(inp, budget_s=15.0):
                        f"decompress + torch fp32 attention, {el:.1f} s", cpu=cpu_model(), os_cpu_count=os.cpu_count())
 
 
+def measured_traffic():
+    """HBM bytes per decode call measured with rocprofv3 counters (see the JSON for the commands)."""
+    p = os.path.join(ROOT, "profiles", "decode_cfg1_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f)["bytes_per_call"]["total"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,6 +249,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run one 256 MiB device-to-device copy (a kernel of known traffic for counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -247,6 +259,12 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    if args.calib_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     lens = config1_lens()
     inp = build_decode_inputs(lens)
     torch.cuda.synchronize()
@@ -278,8 +296,10 @@ def main():
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "step_ms": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in t.items() if k != "wall_s"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rq_fused_decode (decode_kernel + decode_merge_kernel), HIP events per launch"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "one rq_fused_decode call (decode_prep_kernel + decode_kernel + decode_merge_kernel), "
+                               "HIP events around each call on its stream; traffic = HBM bytes per call from "
+                               "profiles/decode_cfg1_traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated)"},
     }
     if not args.no_compress:
         result["compress"] = time_compress()

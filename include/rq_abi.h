@@ -160,12 +160,14 @@ int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, int32_t blo
  * out: same shape and dtype, strides out_stride_seq / out_stride_head.
  * rotation: R, head_dim x head_dim fp32 row major, block diagonal with blocks
  * of rot_block (2 or 4).  head_dim must be 128; num_q_heads / num_kv_heads
- * must be an integer <= 16; n_k_centroids / n_v_centroids 8 or 16.
- * max_seq_len bounds every seq_lens entry (it sizes the split-KV grid).
- * workspace: rq_fused_decode_workspace_bytes(...) bytes of scratch, zero-filled
- * before its first use; each call leaves its per-sequence counters at zero
- * again, so the same workspace serves later calls (calls sharing one
- * workspace must not overlap).  One kernel launch per call.
+ * must be an integer <= 16; n_k_centroids / n_v_centroids 8 or 16; centroids
+ * and rotation 16-byte aligned.
+ * max_seq_len bounds every seq_lens entry (it sizes the work and workspace).
+ * workspace: at least rq_fused_decode_workspace_bytes(...) bytes of device
+ * scratch (split partials, query operands, tile descriptors); no
+ * initialisation is needed and every call rewrites what it reads, so one
+ * workspace serves any number of calls (calls sharing one workspace must not
+ * overlap).  Three kernel launches per call (prep, decode, merge).
  */
 int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num_q_heads,
                                         int32_t head_dim, int64_t max_seq_len);

@@ -3,18 +3,22 @@
 // Replaces fused_paged_rq_decode (src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312,
 // kernel :32-206).  Same mathematics -- attention in the rotated space, with
 // q_rot = bf16(q R^T), K/V = centroid[idx] * norm, exp2 online softmax, and
-// out = bf16(bf16(out_rot) R) -- organised for CDNA4:
+// out = bf16(bf16(out_rot) R) -- organised for CDNA4 in three launches:
 //
-//   * grid (chunk, seq); a workgroup owns one chunk of a sequence's context
-//     for ALL kv heads (one wave per kv head), so each token's contiguous
-//     payload is read once and all GQA query heads of a kv head share it;
-//   * Q K^T and P V run on v_mfma_f32_16x16x32_{bf16,f16}: the GQA group
-//     (<= 16 query heads) is the 16-wide N side, tokens / head dims the M side;
-//   * nibble -> 16-bit centroid lookups are register v_perm_b32 table lookups;
-//     the K/V norms are factored out of the MFMA operands (applied to the
-//     scores and to P), so the operands are raw centroids;
-//   * split-KV: each chunk writes (m, l, acc) partials; a merge kernel
-//     combines them (log-sum-exp), rounds, and rotates back by R.
+//   * decode_prep_kernel: per sequence, the fp16 Q^T MFMA operand of every kv
+//     head and one descriptor per 32-token tile (slot offsets from the block
+//     table);
+//   * decode_kernel: persistent; the tiles of the whole batch are split into
+//     equal contiguous ranges, one per resident workgroup.  A workgroup holds
+//     one wave per kv head, so each token's K/V bytes are read once and shared
+//     by all GQA query heads.  Tiles are copied global -> LDS two ahead;
+//     Q K^T and P V run on v_mfma_f32_16x16x32_f16 with the GQA group
+//     (<= 16 query heads) as the 16-wide N side; nibble -> fp16 centroid
+//     lookups are register v_perm_b32 table lookups and the K/V norms are
+//     applied to the scores and to P.  Each sequence segment of a range ends
+//     in an (m, l, acc) partial;
+//   * decode_merge_kernel: log-sum-exp over a sequence's partials, rounding
+//     and the rotation back by R.
 //
 // MFMA operand layout used below (16x16x32, wave64, lane l, g = l / 16):
 //   A (16 x 32): lane holds row l % 16, k = 8g .. 8g+7   (4 dwords of 2 x 16-bit)
