@@ -666,10 +666,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
 
 // Merge the partials of (seq, query head): log-sum-exp over the segments, round
 // to the query dtype (the reference's out_rot, fused_paged_rq_decode.py:201-206),
-// rotate back by R in fp32 and round again (:308).  One wave per query head:
-// lane c first loads segment c's (m, l) (64 segments per pass), the weights are
-// formed with wave reductions, then the accumulators (two head dims per lane)
-// are summed with eight segments' loads in flight.
+// rotate back by R in fp32 and round again (:308).  One wave per query head,
+// two head dims per lane; per pass of 16 segments, the (m, l) of each segment
+// and the lane's accumulator entries of all of them are loaded together.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.y;
@@ -678,6 +677,15 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     __shared__ float orot_all[4][kD];
     float *orot = orot_all[wave];
     if (hq >= a.HQ) return;
+    // R entries for this lane's two output dims (issued first; independent of the partials)
+    float rr[2][4];
+    #pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int d = 2 * lane + e;
+        const int k0 = (d / a.rot_block) * a.rot_block;
+    #pragma unroll
+        for (int i = 0; i < 4; ++i) rr[e][i] = i < a.rot_block ? a.R[(k0 + i) * kD + d] : 0.f;
+    }
     // Workgroups whose tile ranges cover the sequence: workgroup w owns tiles
     // [w NT / G, (w+1) NT / G), so tile t belongs to w(t) = ((t + 1) G - 1) / NT.
     // Partials sit at slots w + seq for w in [w(first tile), w(last tile)];
@@ -697,44 +705,35 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
     float lsum = 0.f, o0 = 0.f, o1 = 0.f, M = -INFINITY;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-        const int c = c0 + lane;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        // lane c (< 16) loads segment c0 + c's (m, l); every lane loads its two dims of
+        // up to 16 segments' accumulators -- all issued before any is used
+        const int c = c0 + (lane & 15);
         const bool ok = c < nch && has_tiles(w_lo + c);
-        const uint64_t okm = __ballot(ok);
+        const uint64_t okm = __ballot(ok && lane < 16);
         const float2 v = ok ? *reinterpret_cast<const float2 *>(ml + c * cs_ml) : make_float2(-INFINITY, 0.f);
-        float pm = v.x;
-        for (int o = 32; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
+        float2 x[16];
+    #pragma unroll
+        for (int u = 0; u < 16; ++u)
+            x[u] = (okm >> u) & 1 ? reinterpret_cast<const float2 *>(pa + (c0 + u) * cs_acc)[lane] : make_float2(0.f, 0.f);
+        float pm = lane < 16 ? v.x : -INFINITY;
+        for (int o = 8; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
+        pm = __shfl(pm, 0);
         const float Mn = fmaxf(M, pm);
         const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // -inf - finite -> 0 on the first pass
         o0 *= alpha;
         o1 *= alpha;
         lsum *= alpha;
         M = Mn;
-        const float w = ok ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
+        const float w = ok && lane < 16 ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
         float wl = w * v.y;
-        for (int o = 32; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
-        lsum += wl;
-        const int n = min(64, nch - c0);
-        const float *pc = pa + c0 * cs_acc;
-        int i = 0;
-        for (; i + 8 <= n; i += 8) {
-            float2 x[8];
+        for (int o = 8; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
+        lsum += __shfl(wl, 0);
     #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                x[u] = (okm >> (i + u)) & 1 ? reinterpret_cast<const float2 *>(pc + (i + u) * cs_acc)[lane] : make_float2(0.f, 0.f);
-    #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i + u));
-                o0 += wu * x[u].x;
-                o1 += wu * x[u].y;
-            }
-        }
-        for (; i < n; ++i) {
-            if (!((okm >> i) & 1)) continue;
-            const float2 x = reinterpret_cast<const float2 *>(pc + i * cs_acc)[lane];
-            const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
-            o0 += wu * x.x;
-            o1 += wu * x.y;
+        for (int u = 0; u < 16; ++u) {
+            const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+            o0 += wu * x[u].x;
+            o1 += wu * x[u].y;
         }
     }
     const float inv = nch > 0 ? 1.f / lsum : 0.f;  // empty context -> zeros (reference: acc 0, l 1)
@@ -748,7 +747,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         const int d = 2 * lane + e;
         const int k0 = (d / a.rot_block) * a.rot_block;
         float r = 0.f;
-        for (int i = 0; i < a.rot_block; ++i) r = __builtin_fmaf(orot[k0 + i], a.R[(k0 + i) * kD + d], r);
+        for (int i = 0; i < a.rot_block; ++i) r = __builtin_fmaf(orot[k0 + i], rr[e][i], r);
         packed |= Elem<DT>::from_f32(r) << (16 * e);
     }
     reinterpret_cast<uint32_t *>(dst)[lane] = packed;
