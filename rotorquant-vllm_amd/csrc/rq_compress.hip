@@ -16,17 +16,34 @@
 //   index : number of boundaries b with b < r_j (torch.bucketize right=False,
 //           :184); pack byte j = (idx[2j] << 4) | idx[2j+1] (:187-188).
 //
-// Work split: one 64-lane wave owns 64 rows (one row = one (token, head) of K
-// or V).  The rows are staged through LDS with coalesced 16-byte loads; each
-// lane then reduces one row's norm in the fixed order above, and finally 16
-// lanes per row each produce 8 indices (one packed dword).
+// How the kernel meets that contract cheaply:
+//   * divide: y = 1/d is computed once per row (correctly rounded); each element
+//     then takes q0 = x*y and two remainder corrections r = fma(-q, d, x),
+//     q = fma(r, y, q).  With y = RN(1/d) and the first correction bringing q
+//     within one ulp of x/d, the second gives RN(x/d) (Markstein's theorem),
+//     provided nothing underflows; rows or elements outside the guarded range
+//     (d > 2^40, or 0 < |x| < 2^-60) use the plain division instead.
+//   * index : a 64-cell table over a monotone map cell(v) = clamp(fma(v, s, c))
+//     replaces the 15 comparisons.  Because cell() is monotone, every boundary
+//     in a lower cell than v is < v and every boundary in a higher cell is > v;
+//     when each cell holds at most one boundary (checked per workgroup), the
+//     count is table[cell].n + (table[cell].b < v).  Boundary sets that fail the
+//     check (NaNs, unsorted, too close together) take the 15-comparison count.
+//
+// Work split: a workgroup of four waves owns 64 rows (one row = one (token,
+// head) of K or V).  Per-row source and destination addresses are resolved
+// once; the rows are staged through LDS with coalesced 16-byte loads; four
+// lanes per row reduce the norm's partial sums; D/8 lanes per row then produce
+// 8 indices each (one packed dword).
 #include "rq_common.h"
 
 namespace rq {
 
-constexpr int kRowsPerWave = 64;
+constexpr int kRows = 64;        // rows per workgroup
+constexpr int kThreads = 256;    // four waves
 constexpr int kMaxBounds = 15;
 constexpr int kMaxD = 256;
+constexpr int kCells = 64;       // bucketize lookup cells per boundary set
 
 // Where the rows come from and where their bytes go.
 struct RowMap {
@@ -46,16 +63,64 @@ struct RowMap {
     int64_t stride_block, stride_token;
     int32_t total_bytes;
     int32_t H;
+    int32_t pad_vec;    // slot padding can be cleared with 16-byte stores
 };
 
-// Byte address of the slot of row r's token (nullptr when the slot is < 0).
-__device__ __forceinline__ uint8_t *slot_base(const RowMap &m, int64_t t) {
-    int64_t s = m.slot_mapping[t];
+// Per-row addresses, resolved once per workgroup.
+struct RowRef {
+    const uint8_t *src;  // first element (nullptr: row past the end)
+    uint8_t *idx_dst;    // packed indices (nullptr: row past the end or slot skipped)
+    float *norm_dst;
+    int32_t is_v, pad;
+};
+
+// LDS map of one workgroup (bytes).
+constexpr int kOffRefs = 0;                                  // RowRef[kRows]
+constexpr int kOffTbl = kOffRefs + kRows * 32;               // float2[2][kCells]: {boundary, count}
+constexpr int kOffBnd = kOffTbl + 2 * kCells * 8;            // float[2][16]
+constexpr int kOffCell = kOffBnd + 2 * 16 * 4;               // int[2][16]
+constexpr int kOffPad = kOffCell + 2 * 16 * 4;               // uint8_t *[kRows / 2]
+constexpr int kOffMisc = kOffPad + (kRows / 2) * 8;          // int: pad count, table flag
+constexpr int kOffNorm = kOffMisc + 16;                      // float[kRows]
+constexpr int kOffRows = (kOffNorm + kRows * 4 + 15) / 16 * 16;
+static_assert(sizeof(RowRef) == 32, "RowRef layout");
+
+// Byte address of a token's slot given its slot id (nullptr when the slot is < 0
+// or past the cache).
+__device__ __forceinline__ uint8_t *slot_base(const RowMap &m, int64_t s) {
     if (s < 0 || s >= m.num_slots) return nullptr;
-    int64_t blk = s / m.block_size;
-    int64_t off = s - blk * m.block_size;
+    int64_t blk, off;
+    if (m.num_slots <= 0x7fffffff) {
+        uint32_t b = (uint32_t)s / (uint32_t)m.block_size;
+        blk = b;
+        off = (int64_t)((uint32_t)s - b * (uint32_t)m.block_size);
+    } else {
+        blk = s / m.block_size;
+        off = s - blk * m.block_size;
+    }
     return m.cache + blk * m.stride_block + off * m.stride_token;
 }
+
+// Monotone (non-decreasing) map of a value to a lookup cell; NaN maps to 0.
+__device__ __forceinline__ int cell_of(float v, float s, float c) {
+    float t = __builtin_fmaf(v, s, c);
+    t = fminf(fmaxf(t, 0.f), (float)(kCells - 1));
+    return (int)t;
+}
+
+// Correctly rounded x / d given y = RN(1 / d) (valid in the guarded range).
+__device__ __forceinline__ float div_corrected(float x, float d, float y) {
+    float q = x * y;
+    float r = __builtin_fmaf(-q, d, x);
+    q = __builtin_fmaf(r, y, q);
+    r = __builtin_fmaf(-q, d, x);
+    return __builtin_fmaf(r, y, q);
+}
+
+template <int DT> struct Src;
+template <> struct Src<RQ_DTYPE_F16> : Elem<RQ_DTYPE_F16> { static constexpr int bytes = 2; };
+template <> struct Src<RQ_DTYPE_BF16> : Elem<RQ_DTYPE_BF16> { static constexpr int bytes = 2; };
+template <> struct Src<RQ_DTYPE_F32> { static constexpr int bytes = 4; };
 
 template <typename T>
 __device__ __forceinline__ void load8(const uint8_t *lds, float (&x)[8]) {
@@ -75,115 +140,220 @@ __device__ __forceinline__ void load8(const uint8_t *lds, float (&x)[8]) {
     }
 }
 
-template <int DT> struct Src;
-template <> struct Src<RQ_DTYPE_F16> : Elem<RQ_DTYPE_F16> { static constexpr int bytes = 2; };
-template <> struct Src<RQ_DTYPE_BF16> : Elem<RQ_DTYPE_BF16> { static constexpr int bytes = 2; };
-template <> struct Src<RQ_DTYPE_F32> { static constexpr int bytes = 4; };
+template <typename T>
+__device__ __forceinline__ void load2(const uint8_t *lds, float &a, float &b) {
+    if constexpr (T::bytes == 2) {
+        uint32_t w = *reinterpret_cast<const uint32_t *>(lds);
+        a = T::to_f32(w & 0xffffu);
+        b = T::to_f32(w >> 16);
+    } else {
+        float2 v = *reinterpret_cast<const float2 *>(lds);
+        a = v.x;
+        b = v.y;
+    }
+}
+
+// Scale and offset of the cell map for one boundary set: cell(b_0) = 0 and
+// cell(b_last) = kCells - 1 up to rounding; s = 0 when the span is empty or not finite.
+__device__ __forceinline__ void cell_params(const float *__restrict__ bnd, int nb, float &s, float &c) {
+    const float lo = bnd[0], span = bnd[nb - 1] - lo;
+    s = (span > 0.f && span < 3.0e38f) ? (float)(kCells - 1) / span : 0.f;
+    if (!(s < 1.0e30f)) s = 0.f;
+    c = -lo * s;
+    if (!(fabsf(c) < 1.0e30f)) { s = 0.f; c = 0.f; }
+}
 
 template <int DT, int BLK>
-__global__ __launch_bounds__(64) void compress_kernel(RowMap m, int64_t n_rows, int D,
-                                                      const float *__restrict__ rt_even,
-                                                      const float *__restrict__ rt_odd,
-                                                      const float *__restrict__ kbnd, int nkb,
-                                                      const float *__restrict__ vbnd, int nvb) {
+__global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_rows, int D,
+                                                            const float *__restrict__ rt_even,
+                                                            const float *__restrict__ rt_odd,
+                                                            const float *__restrict__ kbnd, int nkb,
+                                                            const float *__restrict__ vbnd, int nvb) {
     using S = Src<DT>;
     constexpr int EB = S::bytes;
-    const int lane = threadIdx.x;
-    const int64_t row0 = (int64_t)blockIdx.x * kRowsPerWave;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t row0 = (int64_t)blockIdx.x * kRows;
     const int row_bytes = D * EB;
-    const int row_pitch = row_bytes + 16;  // +16 B keeps the per-row reads bank-conflict free
-    const int chunks = row_bytes / 16;     // 16-byte pieces per row
+    const int pitch = row_bytes + 16;  // +16 B keeps the per-row reads bank-conflict free
+    const int half = D / 2;
 
     extern __shared__ __align__(16) uint8_t lds[];
-    float *lds_norm = reinterpret_cast<float *>(lds + kRowsPerWave * row_pitch);
+    RowRef *refs = reinterpret_cast<RowRef *>(lds + kOffRefs);
+    float2 *tbl = reinterpret_cast<float2 *>(lds + kOffTbl);
+    float *bnd = reinterpret_cast<float *>(lds + kOffBnd);
+    int *cells = reinterpret_cast<int *>(lds + kOffCell);
+    uint8_t **pads = reinterpret_cast<uint8_t **>(lds + kOffPad);
+    int *misc = reinterpret_cast<int *>(lds + kOffMisc);
+    float *lds_norm = reinterpret_cast<float *>(lds + kOffNorm);
+    uint8_t *rows = lds + kOffRows;
 
-    // Boundaries: uniform loads, kept in registers.
-    float kb[kMaxBounds], vb[kMaxBounds];
-#pragma unroll
-    for (int b = 0; b < kMaxBounds; ++b) {
-        kb[b] = b < nkb ? kbnd[b] : 0.f;
-        vb[b] = b < nvb ? vbnd[b] : 0.f;
-    }
+    float sk, ck, sv, cv;
+    cell_params(kbnd, nkb, sk, ck);
+    cell_params(vbnd, nvb, sv, cv);
 
-    // ---- phase 1: stage 64 rows in LDS with coalesced 16-byte loads -------
-    const int total_chunks = kRowsPerWave * chunks;
-    for (int c = lane; c < total_chunks; c += 64) {
-        int rr = c / chunks, part = c - rr * chunks;
-        int64_t r = row0 + rr;
-        uint4 v = make_uint4(0, 0, 0, 0);
+    // ---- step 0: per-row addresses (wave 0), boundary cells (wave 1) -------
+    if (wave == 0) {
+        const int rr = lane;
+        const int64_t r = row0 + rr;
+        RowRef ref{nullptr, nullptr, nullptr, 0, 0};
+        bool first = false;
+        int pad_j = 0;
+        uint8_t *base = nullptr;
         if (r < n_rows) {
-            const uint8_t *src;
             if (!m.store) {
-                src = reinterpret_cast<const uint8_t *>(m.x) + r * (int64_t)row_bytes;
+                ref.src = reinterpret_cast<const uint8_t *>(m.x) + r * (int64_t)row_bytes;
+                ref.idx_dst = m.packed + r * (int64_t)half;
+                ref.norm_dst = m.norms + r;
             } else {
-                int64_t t = r / (2 * m.H);
-                int rem = (int)(r - t * 2 * m.H);
-                bool is_v = rem >= m.H;
-                int h = is_v ? rem - m.H : rem;
-                int64_t off = is_v ? t * m.v_st + (int64_t)h * m.v_sh : t * m.k_st + (int64_t)h * m.k_sh;
-                src = reinterpret_cast<const uint8_t *>(is_v ? m.value : m.key) + off * EB;
+                const int two_h = 2 * m.H;
+                const int64_t tok0 = row0 / two_h;
+                const int rem0 = (int)(row0 - tok0 * two_h);
+                const int local = rem0 + rr;
+                const int j = local / two_h;
+                const int rem = local - j * two_h;
+                const int is_v = rem >= m.H;
+                const int h = rem - is_v * m.H;
+                const int64_t t = tok0 + j;
+                const int64_t off = is_v ? t * m.v_st + (int64_t)h * m.v_sh : t * m.k_st + (int64_t)h * m.k_sh;
+                ref.src = reinterpret_cast<const uint8_t *>(is_v ? m.value : m.key) + off * EB;
+                base = slot_base(m, m.slot_mapping[t]);
+                if (base != nullptr) {
+                    const SlotLayout L(m.H, D);
+                    ref.idx_dst = base + (is_v ? L.v_idx : L.k_idx) + h * half;
+                    ref.norm_dst = reinterpret_cast<float *>(base + (is_v ? L.v_norm : L.k_norm) + 4 * h);
+                }
+                ref.is_v = is_v;
+                first = rem == 0;
+                pad_j = j - (rem0 != 0);
             }
-            v = *reinterpret_cast<const uint4 *>(src + part * 16);
         }
-        *reinterpret_cast<uint4 *>(lds + rr * row_pitch + part * 16) = v;
-    }
-    // Zero padding of every slot whose first row this wave owns.
-    if (m.store) {
-        int pay = SlotLayout(m.H, D).payload;
-        int pad_words = (m.total_bytes - pay) / 4;
-        for (int rr = 0; rr < kRowsPerWave; ++rr) {
-            int64_t r = row0 + rr;
-            if (r >= n_rows) break;
-            if (r % (2 * m.H) != 0) continue;
-            uint8_t *base = slot_base(m, r / (2 * m.H));
-            if (base == nullptr) continue;
-            for (int w = lane; w < pad_words; w += 64)
-                reinterpret_cast<uint32_t *>(base + pay)[w] = 0u;
+        refs[rr] = ref;
+        if (m.store) {
+            if (first) pads[pad_j] = base;
+            const int npad = __popcll(__ballot(first));
+            if (lane == 0) misc[0] = npad;
         }
+    } else if (wave == 1) {
+        // lanes 0-15: K boundaries, lanes 32-47: V boundaries
+        const int kind = lane >> 5, i = lane & 31;
+        const int nb = kind ? nvb : nkb;
+        const float *src = kind ? vbnd : kbnd;
+        const float s = kind ? sv : sk, c = kind ? cv : ck;
+        float b = __builtin_inff();
+        int cl = kCells;
+        if (i < nb) {
+            b = src[i];
+            cl = cell_of(b, s, c);
+        }
+        if (i < 16) {
+            bnd[kind * 16 + i] = b;
+            cells[kind * 16 + i] = cl;
+        }
+        // cells strictly increasing and no NaN boundary -> at most one boundary per cell
+        const int next = __shfl_down(cl, 1);
+        const bool bad = i < nb && (b != b || (i + 1 < nb && !(cl < next)));
+        const bool all_ok = __ballot(bad) == 0ull;  // whole-wave vote, taken before lane 0 stores it
+        if (lane == 0) misc[1] = all_ok;
     }
     __syncthreads();
 
-    // ---- phase 2: one lane per row computes the norm in torch's order -----
+    // ---- step 1: stage the rows in LDS; clear slot padding; build tables ---
     {
-        float s[8];
+        const int C = row_bytes / 16;  // 16-byte pieces per row
+        const int rpi = kThreads / C;  // rows per iteration
+        const int my_part = tid % C, my_row = tid / C;
+        const int n_it = (kRows + rpi - 1) / rpi;
+        for (int u0 = 0; u0 < n_it; u0 += 4) {
+            uint4 v[4];
 #pragma unroll
-        for (int v = 0; v < 8; ++v) s[v] = 0.f;
-        const uint8_t *rowp = lds + lane * row_pitch;
-        for (int k = 0; k < D / 8; ++k) {
-            float x[8];
-            load8<S>(rowp + k * 8 * EB, x);
+            for (int u = 0; u < 4; ++u) {
+                const int rr = my_row + (u0 + u) * rpi;
+                v[u] = make_uint4(0, 0, 0, 0);
+                if (my_row < rpi && u0 + u < n_it && rr < kRows) {
+                    const uint8_t *src = refs[rr].src;
+                    if (src != nullptr) v[u] = *reinterpret_cast<const uint4 *>(src + my_part * 16);
+                }
+            }
+            if (u0 == 0) {
+                // table entry {boundary, count} of cell c for both sets
+                if (tid < 2 * kCells) {
+                    const int kind = tid / kCells, c = tid % kCells;
+                    const int nb = kind ? nvb : nkb;
+                    int n = 0;
+                    for (int i = 0; i < nb; ++i) n += cells[kind * 16 + i] < c;
+                    tbl[tid] = make_float2(bnd[kind * 16 + n], __int_as_float(n));
+                }
+                if (m.store) {
+                    const int pay = SlotLayout(m.H, D).payload;
+                    const int npad = misc[0];
+                    if (m.pad_vec) {
+                        const int units = (m.total_bytes - pay) / 16;
+                        for (int i = tid; i < npad * units; i += kThreads) {
+                            const int j = i / units;
+                            uint8_t *base = pads[j];
+                            if (base != nullptr)
+                                reinterpret_cast<uint4 *>(base + pay)[i - j * units] = make_uint4(0, 0, 0, 0);
+                        }
+                    } else {
+                        const int units = (m.total_bytes - pay) / 4;
+                        for (int i = tid; i < npad * units; i += kThreads) {
+                            const int j = i / units;
+                            uint8_t *base = pads[j];
+                            if (base != nullptr) reinterpret_cast<uint32_t *>(base + pay)[i - j * units] = 0u;
+                        }
+                    }
+                }
+            }
 #pragma unroll
-            for (int v = 0; v < 8; ++v) s[v] = __builtin_fmaf(x[v], x[v], s[v]);
-        }
-        float sum = s[0];
-#pragma unroll
-        for (int v = 1; v < 8; ++v) sum = sum + s[v];
-        float n = __builtin_sqrtf(sum);
-        lds_norm[lane] = n;
-        int64_t r = row0 + lane;
-        if (r < n_rows) {
-            if (!m.store) {
-                m.norms[r] = n;
-            } else {
-                int64_t t = r / (2 * m.H);
-                int rem = (int)(r - t * 2 * m.H);
-                bool is_v = rem >= m.H;
-                int h = is_v ? rem - m.H : rem;
-                uint8_t *base = slot_base(m, t);
-                SlotLayout L(m.H, D);
-                if (base != nullptr)
-                    *reinterpret_cast<float *>(base + (is_v ? L.v_norm : L.k_norm) + 4 * h) = n;
+            for (int u = 0; u < 4; ++u) {
+                const int rr = my_row + (u0 + u) * rpi;
+                if (my_row < rpi && u0 + u < n_it && rr < kRows)
+                    *reinterpret_cast<uint4 *>(rows + rr * pitch + my_part * 16) = v[u];
             }
         }
     }
     __syncthreads();
 
-    // ---- phase 3: D/8 lanes per row, 8 coordinates per lane ---------------
-    const int lanes_per_row = D / 8;
-    const int rows_per_pass = 64 / lanes_per_row;
-    const int part = lane % lanes_per_row;
-    const int sub = lane / lanes_per_row;
-    const int half = D / 2;
+    // ---- step 2: norms, four lanes per row --------------------------------
+    // lane q of a row accumulates s_{2q} and s_{2q+1}; lane 0 adds s_0..s_7 in order.
+    {
+        const int rr = tid >> 2, q = tid & 3;
+        const uint8_t *rowp = rows + rr * pitch + 2 * q * EB;
+        float s0 = 0.f, s1 = 0.f;
+        for (int k = 0; k < D / 8; ++k) {
+            float a, b;
+            load2<S>(rowp + k * 8 * EB, a, b);
+            s0 = __builtin_fmaf(a, a, s0);
+            s1 = __builtin_fmaf(b, b, s1);
+        }
+        const float s2 = __shfl_down(s0, 1), s3 = __shfl_down(s1, 1);
+        const float s4 = __shfl_down(s0, 2), s5 = __shfl_down(s1, 2);
+        const float s6 = __shfl_down(s0, 3), s7 = __shfl_down(s1, 3);
+        if (q == 0) {
+            float sum = s0 + s1;
+            sum = sum + s2;
+            sum = sum + s3;
+            sum = sum + s4;
+            sum = sum + s5;
+            sum = sum + s6;
+            sum = sum + s7;
+            const float n = __builtin_sqrtf(sum);
+            lds_norm[rr] = n;
+            float *dst = refs[rr].norm_dst;
+            if (dst != nullptr) *dst = n;
+        }
+    }
+    __syncthreads();
+
+    // ---- step 3: D/8 lanes per row, 8 coordinates per lane ----------------
+    const int lpr = D / 8;
+    const int rpp = kThreads / lpr;  // rows per pass
+    const int part = tid % lpr;
+    const int sub = tid / lpr;
+    if (sub >= rpp) return;
+    const bool use_tbl = misc[1] != 0;
     // R^T entries for this lane's 8 outputs: RT[k][j] for k in j's block.
     float rt[8][BLK];
 #pragma unroll
@@ -194,50 +364,51 @@ __global__ __launch_bounds__(64) void compress_kernel(RowMap m, int64_t n_rows, 
 #pragma unroll
         for (int i = 0; i < BLK; ++i) rt[e][i] = col[(int64_t)(k0 + i) * half + (j >> 1)];
     }
-    for (int p0 = 0; p0 < kRowsPerWave; p0 += rows_per_pass) {
-        int rr = p0 + sub;
-        int64_t r = row0 + rr;
-        bool is_v = false;
-        if (m.store) {
-            int64_t t = r / (2 * m.H);
-            is_v = (int)(r - t * 2 * m.H) >= m.H;
-        }
+    for (int rr = sub; rr < kRows; rr += rpp) {
+        uint32_t *dst = reinterpret_cast<uint32_t *>(refs[rr].idx_dst);
+        if (dst == nullptr) continue;
+        const int is_v = refs[rr].is_v;
         float x[8];
-        load8<S>(lds + rr * row_pitch + part * 8 * EB, x);
-        float den = lds_norm[rr] + 1e-10f;
+        load8<S>(rows + rr * pitch + part * 8 * EB, x);
+        const float den = lds_norm[rr] + 1e-10f;
         float xn[8];
+        bool fast = den <= 0x1p40f;
+        if constexpr (DT != RQ_DTYPE_F16) {
+            // fp16 inputs are never below 2^-24 in magnitude; the others are checked
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xn[e] = x[e] / den;
-        int nb = is_v ? nvb : nkb;
+            for (int e = 0; e < 8; ++e) fast = fast && (x[e] == 0.f || fabsf(x[e]) >= 0x1p-60f);
+        }
+        if (fast) {
+            const float y = 1.0f / den;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xn[e] = div_corrected(x[e], den, y);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xn[e] = x[e] / den;
+        }
+        const float s = is_v ? sv : sk, c = is_v ? cv : ck;
+        const float2 *t = tbl + is_v * kCells;
+        const float *bb = bnd + is_v * 16;
+        const int nb = is_v ? nvb : nkb;
         uint32_t word = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            int kb0 = (e / BLK) * BLK;  // block start inside this lane's 8 elements
+            const int kb0 = (e / BLK) * BLK;  // block start inside this lane's 8 elements
             float acc = xn[kb0] * rt[e][0];
 #pragma unroll
             for (int i = 1; i < BLK; ++i) acc = __builtin_fmaf(xn[kb0 + i], rt[e][i], acc);
-            uint32_t idx = 0;
-#pragma unroll
-            for (int b = 0; b < kMaxBounds; ++b) {
-                float bb = is_v ? vb[b] : kb[b];
-                idx += (b < nb && bb < acc) ? 1u : 0u;
+            uint32_t idx;
+            if (use_tbl) {
+                const float2 ent = t[cell_of(acc, s, c)];
+                idx = (uint32_t)__float_as_int(ent.y) + (ent.x < acc ? 1u : 0u);
+            } else {
+                idx = 0;
+                for (int b = 0; b < nb; ++b) idx += bb[b] < acc ? 1u : 0u;
             }
             // byte e/2: even coordinate in the high nibble, odd in the low one
             word |= idx << (8 * (e >> 1) + ((e & 1) ? 0 : 4));
         }
-        if (r < n_rows) {
-            if (!m.store) {
-                reinterpret_cast<uint32_t *>(m.packed + r * (int64_t)half)[part] = word;
-            } else {
-                int64_t t = r / (2 * m.H);
-                int rem = (int)(r - t * 2 * m.H);
-                int h = is_v ? rem - m.H : rem;
-                uint8_t *base = slot_base(m, t);
-                SlotLayout L(m.H, D);
-                if (base != nullptr)
-                    reinterpret_cast<uint32_t *>(base + (is_v ? L.v_idx : L.k_idx) + h * half)[part] = word;
-            }
-        }
+        dst[part] = word;
     }
 }
 
@@ -245,10 +416,10 @@ template <int DT, int BLK>
 static int launch_compress_blk(const RowMap &m, int64_t n_rows, int D, const float *rte, const float *rto,
                                const float *kb, int nkb, const float *vb, int nvb, hipStream_t st) {
     int eb = DT == RQ_DTYPE_F32 ? 4 : 2;
-    size_t lds = (size_t)kRowsPerWave * (D * eb + 16) + kRowsPerWave * sizeof(float);
-    int64_t grid = (n_rows + kRowsPerWave - 1) / kRowsPerWave;
-    hipLaunchKernelGGL((compress_kernel<DT, BLK>), dim3((unsigned)grid), dim3(64), lds, st, m, n_rows, D, rte, rto,
-                       kb, nkb, vb, nvb);
+    size_t lds = (size_t)kOffRows + (size_t)kRows * (D * eb + 16);
+    int64_t grid = (n_rows + kRows - 1) / kRows;
+    hipLaunchKernelGGL((compress_kernel<DT, BLK>), dim3((unsigned)grid), dim3(kThreads), lds, st, m, n_rows, D, rte,
+                       rto, kb, nkb, vb, nvb);
     return check_launch("compress_kernel");
 }
 
@@ -349,6 +520,8 @@ extern "C" int rq_compress_store(const void *key, const void *value, int32_t dty
     m.stride_token = stride_token;
     m.total_bytes = total_bytes;
     m.H = num_kv_heads;
+    m.pad_vec = L.payload % 16 == 0 && total_bytes % 16 == 0 && stride_token % 16 == 0 && stride_block % 16 == 0 &&
+                ((uintptr_t)kv_cache % 16) == 0;
     int64_t n_rows = n_tokens * 2 * num_kv_heads;
     return dispatch_compress(dtype, m, n_rows, head_dim, rot_t_even, rot_t_odd, rot_block, k_boundaries,
                              n_k_boundaries, v_boundaries, n_v_boundaries, (hipStream_t)stream);

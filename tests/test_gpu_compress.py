@@ -145,3 +145,82 @@ def test_cpu_tensors_rejected():
     p = Params()
     with pytest.raises(RuntimeError, match="no CPU path"):
         K.iso_compress(torch.zeros(1, 1, 128, dtype=torch.float16), p.rte, p.rto, p.kb)
+
+
+def _op_check(x, p, bnd):
+    """Op-level compress of x (N, H, D) on the GPU vs the oracle, bit-exact."""
+    K = _kernels()
+    packed, norms = K.iso_compress(_dev(x), _dev(p.rte), _dev(p.rto), _dev(bnd))
+    xb, dt = O.to_bits(x)
+    pn = p.np()
+    op, on = O.compress(xb, dt, pn["rte"], pn["rto"], bnd.numpy(), p.blk)
+    gp = packed.cpu().numpy()
+    assert np.array_equal(gp, op), f"{int((gp != op).sum())} packed bytes differ"
+    assert np.array_equal(norms.cpu().numpy().view(np.uint32), on.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_compress_extreme_magnitudes(dt):
+    """Rows that leave the corrected-division range (norm > 2^40, elements below 2^-60,
+    subnormals, all-zero rows) take the plain division and still match bit-exactly."""
+    p = Params("iso", 4, 4)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(40, 4, 128, generator=g)
+    x[0] = 0.0                                   # all-zero rows
+    x[1] *= 1e-30                                # tiny rows (subnormal in bf16/fp32 after scaling)
+    x[2] *= 1e-39
+    x[3, :, :64] *= 1e-35                        # mixed magnitudes inside a row
+    x[4] *= 1e14                                 # norm above 2^40 (fp32/bf16)
+    x[5, :, 0] = 3e4                             # one dominant element
+    x[6, :, 1::2] = 0.0
+    x[7] *= 1e-7                                 # fp16 subnormals
+    if dt == torch.float16:
+        x[4] = x[8] * 1000                       # keep fp16 finite
+    _op_check(x.to(dt), p, p.kb)
+
+
+@pytest.mark.parametrize("kind", ["duplicate", "close_pair", "uniform", "skewed"])
+def test_compress_boundary_sets(kind):
+    """Boundary sets that defeat the cell lookup (duplicates, a pair closer than a cell)
+    fall back to counting; well-separated but non-Lloyd-Max sets use the lookup."""
+    p = Params("iso", 4, 4)
+    b = p.kb.clone()
+    if kind == "duplicate":
+        b[7] = b[6]
+    elif kind == "close_pair":
+        b[3] = torch.nextafter(b[2], torch.tensor(1.0))
+    elif kind == "uniform":
+        b = torch.linspace(-0.2, 0.2, 15)
+    else:
+        b = torch.tensor([-0.3, -0.1, -0.02, 0.0, 0.01, 0.05, 0.2])
+    x = torch.randn(96, 8, 128, generator=torch.Generator().manual_seed(3)).to(torch.float16)
+    _op_check(x, p, b.float().contiguous())
+
+
+@pytest.mark.parametrize("D", [64, 80, 256])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_compress_head_dims(D, dt):
+    p = Params("planar" if D == 80 else "iso", 3, 3, head_dim=D)
+    x = torch.randn(33, 3, D, generator=torch.Generator().manual_seed(D)).to(dt)
+    _op_check(x, p, p.kb)
+
+
+@pytest.mark.parametrize("H", [3, 5])
+def test_compress_store_heads_not_dividing_workgroup(H):
+    """2H rows per token that do not divide a workgroup's 64 rows: tokens straddle
+    workgroups, so slot padding and payload come from different workgroups."""
+    K = _kernels()
+    p = Params("iso", 3, 4)
+    BS, NB, N = 16, 20, 200
+    k, v = kv_config0(N, H, 128, cfg=4)
+    slots = torch.randperm(NB * BS, generator=torch.Generator().manual_seed(H))[:N].to(torch.int64)
+    slots[9] = -1
+    cache = torch.full((NB, BS, 256 * H), 0xAB, dtype=torch.uint8, device="cuda")
+    K.compress_store(_dev(k), _dev(v), cache, _dev(slots), _dev(p.rte), _dev(p.rto), _dev(p.kb), _dev(p.vb))
+    ref = np.full((NB, BS, 256 * H), 0xAB, np.uint8)
+    pn = p.np()
+    kp, kn = O.compress(O.to_bits(k)[0], "float16", pn["rte"], pn["rto"], pn["kb"], p.blk)
+    vp, vn = O.compress(O.to_bits(v)[0], "float16", pn["rte"], pn["rto"], pn["vb"], p.blk)
+    O.compress_store(ref, slots.numpy(), kp, kn, vp, vn)
+    got = cache.cpu().numpy()
+    assert np.array_equal(got, ref), f"{int((got != ref).sum())} bytes differ"
