@@ -41,6 +41,19 @@ struct SlotLayout {
     }
 };
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 inline int32_t next_pow2_i32(int32_t n) {
     int32_t p = 1;
     while (p < n) p <<= 1;

@@ -17,12 +17,13 @@
 //           :184); pack byte j = (idx[2j] << 4) | idx[2j+1] (:187-188).
 //
 // How the kernel meets that contract cheaply:
-//   * divide: y = 1/d is computed once per row (correctly rounded); each element
-//     then takes q0 = x*y and two remainder corrections r = fma(-q, d, x),
-//     q = fma(r, y, q).  With y = RN(1/d) and the first correction bringing q
-//     within one ulp of x/d, the second gives RN(x/d) (Markstein's theorem),
-//     provided nothing underflows; rows or elements outside the guarded range
-//     (d > 2^40, or 0 < |x| < 2^-60) use the plain division instead.
+//   * divide: per row, y_hi = RN(1/d) and y_lo = RN(RN(1 - d*y_hi) * y_hi), so
+//     y_hi + y_lo is 1/d to about 2^-46.  Per element, q0 = fma(x, y_hi, x*y_lo)
+//     is then within one ulp of x/d, r = fma(-q0, d, x) is exact and
+//     fma(r, y_hi, q0) = RN(x/d) by Markstein's theorem (y_hi correctly rounded,
+//     q0 within one ulp), provided nothing underflows; rows or elements outside
+//     the guarded range (d > 2^40, or 0 < |x| < 2^-60) use the plain division.
+//     fp16 elements enter these fmas directly through v_fma_mix_f32.
 //   * index : a 64-cell table over a monotone map cell(v) = clamp(fma(v, s, c))
 //     replaces the 15 comparisons.  Because cell() is monotone, every boundary
 //     in a lower cell than v is < v and every boundary in a higher cell is > v;
@@ -30,11 +31,12 @@
 //     count is table[cell].n + (table[cell].b < v).  Boundary sets that fail the
 //     check (NaNs, unsorted, too close together) take the 15-comparison count.
 //
-// Work split: a workgroup of four waves owns 64 rows (one row = one (token,
-// head) of K or V).  Per-row source and destination addresses are resolved
-// once; the rows are staged through LDS with coalesced 16-byte loads; four
-// lanes per row reduce the norm's partial sums; D/8 lanes per row then produce
-// 8 indices each (one packed dword).
+// Work split: rows (one row = one (token, head) of K or V) go in groups of 64
+// to persistent workgroups of four waves, one group after another.  While a
+// group is processed, the next group's row addresses are resolved and its rows
+// are already loading into registers.  A group's rows are staged through LDS
+// with coalesced 16-byte loads; four lanes per row reduce the norm's partial
+// sums; D/8 lanes per row then produce 8 indices each (one packed dword).
 #include "rq_common.h"
 
 namespace rq {
@@ -74,16 +76,36 @@ struct RowRef {
     int32_t is_v, pad;
 };
 
-// LDS map of one workgroup (bytes).
-constexpr int kOffRefs = 0;                                  // RowRef[kRows]
-constexpr int kOffTbl = kOffRefs + kRows * 32;               // float2[2][kCells]: {boundary, count}
+// LDS map of one workgroup (bytes).  Row addresses and padding lists are
+// double-buffered: the next group's are resolved while the current one is used.
+constexpr int kOffRefs = 0;                                  // RowRef[2][kRows]
+constexpr int kOffTbl = kOffRefs + 2 * kRows * 32;           // float2[2][kCells]: {boundary, count}
 constexpr int kOffBnd = kOffTbl + 2 * kCells * 8;            // float[2][16]
 constexpr int kOffCell = kOffBnd + 2 * 16 * 4;               // int[2][16]
-constexpr int kOffPad = kOffCell + 2 * 16 * 4;               // uint8_t *[kRows / 2]
-constexpr int kOffMisc = kOffPad + (kRows / 2) * 8;          // int: pad count, table flag
-constexpr int kOffNorm = kOffMisc + 16;                      // float[kRows]
-constexpr int kOffRows = (kOffNorm + kRows * 4 + 15) / 16 * 16;
+constexpr int kOffPad = kOffCell + 2 * 16 * 4;               // uint8_t *[2][kRows / 2]
+constexpr int kOffMisc = kOffPad + 2 * (kRows / 2) * 8;      // int: pad count [2], table flag
+constexpr int kOffRowp = kOffMisc + 16;                      // float4[kRows]: d, y_hi, y_lo, fast
+constexpr int kOffRows = kOffRowp + kRows * 16;
 static_assert(sizeof(RowRef) == 32, "RowRef layout");
+
+// Global-memory view of a pointer that was read back from LDS (the compiler
+// cannot infer its address space; flat accesses would also count against the
+// LDS wait counter).
+// (The host pass of this single-source file only parses device code, so there
+// the view is the plain pointer.)
+#if defined(__HIP_DEVICE_COMPILE__)
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gbl(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *gbl(const T *p) {
+    return (const __attribute__((address_space(1))) T *)p;
+}
+#else
+template <typename T>
+__device__ __forceinline__ T *gbl(T *p) { return p; }
+#endif
 
 // Byte address of a token's slot given its slot id (nullptr when the slot is < 0
 // or past the cache).
@@ -101,20 +123,52 @@ __device__ __forceinline__ uint8_t *slot_base(const RowMap &m, int64_t s) {
     return m.cache + blk * m.stride_block + off * m.stride_token;
 }
 
-// Monotone (non-decreasing) map of a value to a lookup cell; NaN maps to 0.
+// Monotone (non-decreasing) map of a value to a lookup cell.  v_cvt_i32_f32
+// truncates and saturates (NaN -> 0), so the map is defined for every input.
 __device__ __forceinline__ int cell_of(float v, float s, float c) {
-    float t = __builtin_fmaf(v, s, c);
-    t = fminf(fmaxf(t, 0.f), (float)(kCells - 1));
-    return (int)t;
+    const float t = __builtin_fmaf(v, s, c);
+    int i;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(t));
+    return min(max(i, 0), kCells - 1);
 }
 
-// Correctly rounded x / d given y = RN(1 / d) (valid in the guarded range).
-__device__ __forceinline__ float div_corrected(float x, float d, float y) {
-    float q = x * y;
-    float r = __builtin_fmaf(-q, d, x);
-    q = __builtin_fmaf(r, y, q);
-    r = __builtin_fmaf(-q, d, x);
-    return __builtin_fmaf(r, y, q);
+// Mixed-precision fused multiply-adds (v_fma_mix_f32): the f16 operand is the
+// low (HI = 0) or high (HI = 1) half of a dword and enters the fma exactly.
+template <int HI>
+__device__ __forceinline__ float mix_fma(uint32_t w, float b, float c) {  // x * b + c
+    float d;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b), "v"(c));
+    else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b), "v"(c));
+    return d;
+}
+template <int HI>
+__device__ __forceinline__ float mix_fnma(float a, float b, uint32_t w) {  // -a * b + x
+    float d;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(b), "v"(w));
+    else asm("v_fma_mix_f32 %0, -%1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(b), "v"(w));
+    return d;
+}
+template <int HI>
+__device__ __forceinline__ float mix_sq(uint32_t w, float s) {  // x * x + s
+    float d;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(w), "v"(s));
+    else asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[0,0,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(w), "v"(s));
+    return d;
+}
+
+// x / d for the guarded range, from y_hi = RN(1/d) and y_lo = RN(RN(1 - d*y_hi) * y_hi)
+// (y_hi + y_lo = 1/d to about 2^-46): q0 = fma(x, y_hi, x*y_lo) is within one ulp of
+// x/d, r = fma(-q0, d, x) is exact, and fma(r, y_hi, q0) = RN(x/d) (Markstein).
+__device__ __forceinline__ float div_dd(float x, float d, float yh, float yl) {
+    const float q0 = __builtin_fmaf(x, yh, x * yl);
+    const float r = __builtin_fmaf(-q0, d, x);
+    return __builtin_fmaf(r, yh, q0);
+}
+template <int HI>
+__device__ __forceinline__ float div_dd_f16(uint32_t w, float d, float yh, float yl) {
+    const float q0 = mix_fma<HI>(w, yh, mix_fma<HI>(w, yl, 0.f));
+    const float r = mix_fnma<HI>(q0, d, w);
+    return __builtin_fmaf(r, yh, q0);
 }
 
 template <int DT> struct Src;
@@ -163,8 +217,19 @@ __device__ __forceinline__ void cell_params(const float *__restrict__ bnd, int n
     if (!(fabsf(c) < 1.0e30f)) { s = 0.f; c = 0.f; }
 }
 
+// Position of a group of kRows rows in store mode: first row, its token and the
+// row's index inside that token (rows of a token: K heads, then V heads).
+struct Cursor {
+    int64_t row0, tok0;
+    int rem0;
+};
+
+// Four resident waves per SIMD (at most 128 VGPRs) measured fastest for rotation
+// blocks up to 4; 8x8 blocks keep their registers.
+constexpr int compress_waves_per_eu(int blk) { return blk <= 4 ? 4 : 1; }
+
 template <int DT, int BLK>
-__global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_rows, int D,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compress_waves_per_eu(BLK)))) void compress_kernel(RowMap m, int64_t n_rows, int D,
                                                             const float *__restrict__ rt_even,
                                                             const float *__restrict__ rt_odd,
                                                             const float *__restrict__ kbnd, int nkb,
@@ -174,29 +239,80 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t row0 = (int64_t)blockIdx.x * kRows;
     const int row_bytes = D * EB;
     const int pitch = row_bytes + 16;  // +16 B keeps the per-row reads bank-conflict free
     const int half = D / 2;
+    const int two_h = 2 * m.H;
+    const int64_t n_groups = (n_rows + kRows - 1) / kRows;
+    const int64_t gstride = gridDim.x;
 
     extern __shared__ __align__(16) uint8_t lds[];
-    RowRef *refs = reinterpret_cast<RowRef *>(lds + kOffRefs);
+    RowRef *refs_all = reinterpret_cast<RowRef *>(lds + kOffRefs);
     float2 *tbl = reinterpret_cast<float2 *>(lds + kOffTbl);
     float *bnd = reinterpret_cast<float *>(lds + kOffBnd);
     int *cells = reinterpret_cast<int *>(lds + kOffCell);
-    uint8_t **pads = reinterpret_cast<uint8_t **>(lds + kOffPad);
+    uint8_t **pads_all = reinterpret_cast<uint8_t **>(lds + kOffPad);
     int *misc = reinterpret_cast<int *>(lds + kOffMisc);
-    float *lds_norm = reinterpret_cast<float *>(lds + kOffNorm);
+    float4 *rowp = reinterpret_cast<float4 *>(lds + kOffRowp);
     uint8_t *rows = lds + kOffRows;
 
+    // Quantize-step lane roles and this lane's R^T entries (loaded first).
+    const int lpr = D / 8;           // lanes per row
+    const int rpp = kThreads / lpr;  // rows per pass
+    const int part = tid % lpr;
+    const int sub = tid / lpr;
+    float rt[8][BLK];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int j = part * 8 + e;
+        const int k0 = (j / BLK) * BLK;
+        const float *col = (j & 1) ? rt_odd : rt_even;
+#pragma unroll
+        for (int i = 0; i < BLK; ++i) rt[e][i] = col[(int64_t)(k0 + i) * half + (j >> 1)];
+    }
     float sk, ck, sv, cv;
     cell_params(kbnd, nkb, sk, ck);
     cell_params(vbnd, nvb, sv, cv);
 
-    // ---- step 0: per-row addresses (wave 0), boundary cells (wave 1) -------
-    if (wave == 0) {
-        const int rr = lane;
-        const int64_t r = row0 + rr;
+    // Staging roles: 16-byte piece my_part of rows my_row + u * rpi.
+    const int C = row_bytes / 16;
+    const int rpi = kThreads / C;
+    const int my_part = tid % C, my_row = tid / C;
+    const int n_it = (kRows + rpi - 1) / rpi;
+
+    // Store-mode cursor over groups g, g + gstride, ... (wave 0 walks it).
+    Cursor cur{0, 0, 0};
+    int64_t step_tok = 0;
+    int step_rem = 0;
+    if (m.store) {
+        cur.row0 = (int64_t)blockIdx.x * kRows;
+        cur.tok0 = cur.row0 / two_h;
+        cur.rem0 = (int)(cur.row0 - cur.tok0 * two_h);
+        const int64_t step = gstride * kRows;
+        step_tok = step / two_h;
+        step_rem = (int)(step - step_tok * two_h);
+    }
+    auto advance = [&](Cursor c) {
+        c.row0 += gstride * kRows;
+        c.tok0 += step_tok;
+        c.rem0 += step_rem;
+        if (c.rem0 >= two_h) {
+            c.rem0 -= two_h;
+            c.tok0 += 1;
+        }
+        return c;
+    };
+    // Slot id of the token of this lane's row in the group at c (store mode, wave 0).
+    auto slot_id = [&](const Cursor &c) -> int64_t {
+        const int local = c.rem0 + lane;
+        const int j = local / two_h;
+        const int64_t t = c.tok0 + j;
+        if (c.row0 + lane >= n_rows) return -1;
+        return m.slot_mapping[t];
+    };
+    // Resolve the group's row addresses into buffer b (wave 0).
+    auto build_refs = [&](const Cursor &c, int64_t g, int b, int64_t sid) {
+        const int64_t r = g * kRows + lane;
         RowRef ref{nullptr, nullptr, nullptr, 0, 0};
         bool first = false;
         int pad_j = 0;
@@ -207,18 +323,16 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_
                 ref.idx_dst = m.packed + r * (int64_t)half;
                 ref.norm_dst = m.norms + r;
             } else {
-                const int two_h = 2 * m.H;
-                const int64_t tok0 = row0 / two_h;
-                const int rem0 = (int)(row0 - tok0 * two_h);
-                const int local = rem0 + rr;
+                const int local = c.rem0 + lane;
                 const int j = local / two_h;
                 const int rem = local - j * two_h;
                 const int is_v = rem >= m.H;
                 const int h = rem - is_v * m.H;
-                const int64_t t = tok0 + j;
-                const int64_t off = is_v ? t * m.v_st + (int64_t)h * m.v_sh : t * m.k_st + (int64_t)h * m.k_sh;
+                const int64_t t = c.tok0 + j;
+                const int64_t off =
+                    is_v ? t * m.v_st + (int64_t)h * m.v_sh : t * m.k_st + (int64_t)h * m.k_sh;
                 ref.src = reinterpret_cast<const uint8_t *>(is_v ? m.value : m.key) + off * EB;
-                base = slot_base(m, m.slot_mapping[t]);
+                base = slot_base(m, sid);
                 if (base != nullptr) {
                     const SlotLayout L(m.H, D);
                     ref.idx_dst = base + (is_v ? L.v_idx : L.k_idx) + h * half;
@@ -226,15 +340,37 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_
                 }
                 ref.is_v = is_v;
                 first = rem == 0;
-                pad_j = j - (rem0 != 0);
+                pad_j = j - (c.rem0 != 0);
             }
         }
-        refs[rr] = ref;
+        refs_all[b * kRows + lane] = ref;
         if (m.store) {
-            if (first) pads[pad_j] = base;
+            if (first) pads_all[b * (kRows / 2) + pad_j] = base;
             const int npad = __popcll(__ballot(first));
-            if (lane == 0) misc[0] = npad;
+            if (lane == 0) misc[b] = npad;
         }
+    };
+    // Batch 0 of a group's rows into registers (the rest, if any, is loaded in place).
+    auto load_batch0 = [&](int b, uint4 (&v)[4]) {
+        const RowRef *refs = refs_all + b * kRows;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int rr = my_row + u * rpi;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (my_row < rpi && u < n_it && rr < kRows) {
+                const uint8_t *src = refs[rr].src;
+                if (src != nullptr) v[u] = *gbl(reinterpret_cast<const uint4 *>(src + my_part * 16));
+            }
+        }
+    };
+
+    int64_t g = blockIdx.x;
+    int64_t sid_next = -1;
+    // ---- prologue: first group's addresses; boundary cells -----------------
+    if (wave == 0) {
+        const int64_t sid = m.store ? slot_id(cur) : -1;
+        if (m.store && g + gstride < n_groups) sid_next = slot_id(advance(cur));
+        build_refs(cur, g, 0, sid);
     } else if (wave == 1) {
         // lanes 0-15: K boundaries, lanes 32-47: V boundaries
         const int kind = lane >> 5, i = lane & 31;
@@ -255,161 +391,208 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(RowMap m, int64_t n_
         const int next = __shfl_down(cl, 1);
         const bool bad = i < nb && (b != b || (i + 1 < nb && !(cl < next)));
         const bool all_ok = __ballot(bad) == 0ull;  // whole-wave vote, taken before lane 0 stores it
-        if (lane == 0) misc[1] = all_ok;
+        if (lane == 0) misc[2] = all_ok;
     }
     __syncthreads();
+    uint4 v[4];
+    load_batch0(0, v);
+    if (tid < 2 * kCells) {
+        // table entry {boundary, count} of cell c for both sets
+        const int kind = tid / kCells, c = tid % kCells;
+        const int nb = kind ? nvb : nkb;
+        int n = 0;
+        for (int i = 0; i < nb; ++i) n += cells[kind * 16 + i] < c;
+        tbl[tid] = make_float2(bnd[kind * 16 + n], __int_as_float(n));
+    }
 
-    // ---- step 1: stage the rows in LDS; clear slot padding; build tables ---
-    {
-        const int C = row_bytes / 16;  // 16-byte pieces per row
-        const int rpi = kThreads / C;  // rows per iteration
-        const int my_part = tid % C, my_row = tid / C;
-        const int n_it = (kRows + rpi - 1) / rpi;
-        for (int u0 = 0; u0 < n_it; u0 += 4) {
-            uint4 v[4];
+    for (int buf = 0;; buf ^= 1) {
+        const RowRef *refs = refs_all + buf * kRows;
+        const int64_t gn = g + gstride;
+        const bool has_next = gn < n_groups;
+        // ---- (a) rows of g into LDS; slot padding; next group's addresses ----
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int rr = my_row + (u0 + u) * rpi;
-                v[u] = make_uint4(0, 0, 0, 0);
-                if (my_row < rpi && u0 + u < n_it && rr < kRows) {
-                    const uint8_t *src = refs[rr].src;
-                    if (src != nullptr) v[u] = *reinterpret_cast<const uint4 *>(src + my_part * 16);
+        for (int u = 0; u < 4; ++u) {
+            const int rr = my_row + u * rpi;
+            if (my_row < rpi && u < n_it && rr < kRows)
+                *reinterpret_cast<uint4 *>(rows + rr * pitch + my_part * 16) = v[u];
+        }
+        for (int u = 4; u < n_it; ++u) {
+            const int rr = my_row + u * rpi;
+            if (my_row < rpi && rr < kRows) {
+                const uint8_t *src = refs[rr].src;
+                uint4 w = make_uint4(0, 0, 0, 0);
+                if (src != nullptr) w = *gbl(reinterpret_cast<const uint4 *>(src + my_part * 16));
+                *reinterpret_cast<uint4 *>(rows + rr * pitch + my_part * 16) = w;
+            }
+        }
+        if (m.store) {
+            const int pay = SlotLayout(m.H, D).payload;
+            const int npad = misc[buf];
+            uint8_t *const *pads = pads_all + buf * (kRows / 2);
+            if (m.pad_vec) {
+                const int units = (m.total_bytes - pay) / 16;
+                for (int i = tid; i < npad * units; i += kThreads) {
+                    const int j = i / units;
+                    uint8_t *base = pads[j];
+                    if (base != nullptr)
+                        gbl(reinterpret_cast<uint4 *>(base + pay))[i - j * units] = make_uint4(0, 0, 0, 0);
+                }
+            } else {
+                const int units = (m.total_bytes - pay) / 4;
+                for (int i = tid; i < npad * units; i += kThreads) {
+                    const int j = i / units;
+                    uint8_t *base = pads[j];
+                    if (base != nullptr) gbl(reinterpret_cast<uint32_t *>(base + pay))[i - j * units] = 0u;
                 }
             }
-            if (u0 == 0) {
-                // table entry {boundary, count} of cell c for both sets
-                if (tid < 2 * kCells) {
-                    const int kind = tid / kCells, c = tid % kCells;
-                    const int nb = kind ? nvb : nkb;
-                    int n = 0;
-                    for (int i = 0; i < nb; ++i) n += cells[kind * 16 + i] < c;
-                    tbl[tid] = make_float2(bnd[kind * 16 + n], __int_as_float(n));
+        }
+        if (wave == 0 && has_next) {
+            const Cursor cn = m.store ? advance(cur) : cur;
+            const int64_t sid = sid_next;
+            if (m.store && gn + gstride < n_groups) sid_next = slot_id(advance(cn));
+            build_refs(cn, gn, buf ^ 1, sid);
+            cur = cn;
+        }
+        __syncthreads();
+        // ---- (b) next group's rows in flight while this one is processed -----
+        if (has_next) load_batch0(buf ^ 1, v);
+
+        // ---- (c) norms, four lanes per row ------------------------------------
+        // lane q of a row accumulates s_{2q} and s_{2q+1}; lane 0 adds s_0..s_7 in order
+        // and prepares the row's divisor d = n + 1e-10 and its split reciprocal.
+        {
+            const int rr = tid >> 2, q = tid & 3;
+            const uint8_t *rowq = rows + rr * pitch + 2 * q * EB;
+            float s0 = 0.f, s1 = 0.f;
+            for (int k = 0; k < D / 8; ++k) {
+                if constexpr (DT == RQ_DTYPE_F16) {
+                    const uint32_t w = *reinterpret_cast<const uint32_t *>(rowq + k * 8 * EB);
+                    s0 = mix_sq<0>(w, s0);
+                    s1 = mix_sq<1>(w, s1);
+                } else {
+                    float a, b;
+                    load2<S>(rowq + k * 8 * EB, a, b);
+                    s0 = __builtin_fmaf(a, a, s0);
+                    s1 = __builtin_fmaf(b, b, s1);
                 }
-                if (m.store) {
-                    const int pay = SlotLayout(m.H, D).payload;
-                    const int npad = misc[0];
-                    if (m.pad_vec) {
-                        const int units = (m.total_bytes - pay) / 16;
-                        for (int i = tid; i < npad * units; i += kThreads) {
-                            const int j = i / units;
-                            uint8_t *base = pads[j];
-                            if (base != nullptr)
-                                reinterpret_cast<uint4 *>(base + pay)[i - j * units] = make_uint4(0, 0, 0, 0);
-                        }
-                    } else {
-                        const int units = (m.total_bytes - pay) / 4;
-                        for (int i = tid; i < npad * units; i += kThreads) {
-                            const int j = i / units;
-                            uint8_t *base = pads[j];
-                            if (base != nullptr) reinterpret_cast<uint32_t *>(base + pay)[i - j * units] = 0u;
-                        }
+            }
+            const float s2 = __shfl_down(s0, 1), s3 = __shfl_down(s1, 1);
+            const float s4 = __shfl_down(s0, 2), s5 = __shfl_down(s1, 2);
+            const float s6 = __shfl_down(s0, 3), s7 = __shfl_down(s1, 3);
+            if (q == 0) {
+                float sum = s0 + s1;
+                sum = sum + s2;
+                sum = sum + s3;
+                sum = sum + s4;
+                sum = sum + s5;
+                sum = sum + s6;
+                sum = sum + s7;
+                const float n = __builtin_sqrtf(sum);
+                const float d = n + 1e-10f;
+                const float yh = 1.0f / d;
+                const float yl = __builtin_fmaf(-d, yh, 1.0f) * yh;
+                rowp[rr] = make_float4(d, yh, yl, d <= 0x1p40f ? 1.f : 0.f);
+                float *dst = refs[rr].norm_dst;
+                if (dst != nullptr) *gbl(dst) = n;
+            }
+        }
+        __syncthreads();
+
+        // ---- (d) D/8 lanes per row, 8 coordinates per lane ------------------
+        const bool use_tbl = __builtin_amdgcn_readfirstlane(misc[2]) != 0;
+        for (int rr = sub; sub < rpp && rr < kRows; rr += rpp) {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(refs[rr].idx_dst);
+            if (dst == nullptr) continue;
+            const int is_v = refs[rr].is_v;
+            const float4 rp = rowp[rr];
+            const float d = rp.x, yh = rp.y, yl = rp.z;
+            bool fast = rp.w != 0.f;
+            float xn[8];
+            if constexpr (DT == RQ_DTYPE_F16) {
+                // fp16 inputs are 0 or at least 2^-24 in magnitude: inside the guarded range
+                const uint4 w4 = *reinterpret_cast<const uint4 *>(rows + rr * pitch + part * 16);
+                const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+                if (fast) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xn[2 * i] = div_dd_f16<0>(w[i], d, yh, yl);
+                        xn[2 * i + 1] = div_dd_f16<1>(w[i], d, yh, yl);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xn[2 * i] = S::to_f32(w[i] & 0xffffu) / d;
+                        xn[2 * i + 1] = S::to_f32(w[i] >> 16) / d;
                     }
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int rr = my_row + (u0 + u) * rpi;
-                if (my_row < rpi && u0 + u < n_it && rr < kRows)
-                    *reinterpret_cast<uint4 *>(rows + rr * pitch + my_part * 16) = v[u];
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- step 2: norms, four lanes per row --------------------------------
-    // lane q of a row accumulates s_{2q} and s_{2q+1}; lane 0 adds s_0..s_7 in order.
-    {
-        const int rr = tid >> 2, q = tid & 3;
-        const uint8_t *rowp = rows + rr * pitch + 2 * q * EB;
-        float s0 = 0.f, s1 = 0.f;
-        for (int k = 0; k < D / 8; ++k) {
-            float a, b;
-            load2<S>(rowp + k * 8 * EB, a, b);
-            s0 = __builtin_fmaf(a, a, s0);
-            s1 = __builtin_fmaf(b, b, s1);
-        }
-        const float s2 = __shfl_down(s0, 1), s3 = __shfl_down(s1, 1);
-        const float s4 = __shfl_down(s0, 2), s5 = __shfl_down(s1, 2);
-        const float s6 = __shfl_down(s0, 3), s7 = __shfl_down(s1, 3);
-        if (q == 0) {
-            float sum = s0 + s1;
-            sum = sum + s2;
-            sum = sum + s3;
-            sum = sum + s4;
-            sum = sum + s5;
-            sum = sum + s6;
-            sum = sum + s7;
-            const float n = __builtin_sqrtf(sum);
-            lds_norm[rr] = n;
-            float *dst = refs[rr].norm_dst;
-            if (dst != nullptr) *dst = n;
-        }
-    }
-    __syncthreads();
-
-    // ---- step 3: D/8 lanes per row, 8 coordinates per lane ----------------
-    const int lpr = D / 8;
-    const int rpp = kThreads / lpr;  // rows per pass
-    const int part = tid % lpr;
-    const int sub = tid / lpr;
-    if (sub >= rpp) return;
-    const bool use_tbl = misc[1] != 0;
-    // R^T entries for this lane's 8 outputs: RT[k][j] for k in j's block.
-    float rt[8][BLK];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        int j = part * 8 + e;
-        int k0 = (j / BLK) * BLK;
-        const float *col = (j & 1) ? rt_odd : rt_even;
-#pragma unroll
-        for (int i = 0; i < BLK; ++i) rt[e][i] = col[(int64_t)(k0 + i) * half + (j >> 1)];
-    }
-    for (int rr = sub; rr < kRows; rr += rpp) {
-        uint32_t *dst = reinterpret_cast<uint32_t *>(refs[rr].idx_dst);
-        if (dst == nullptr) continue;
-        const int is_v = refs[rr].is_v;
-        float x[8];
-        load8<S>(rows + rr * pitch + part * 8 * EB, x);
-        const float den = lds_norm[rr] + 1e-10f;
-        float xn[8];
-        bool fast = den <= 0x1p40f;
-        if constexpr (DT != RQ_DTYPE_F16) {
-            // fp16 inputs are never below 2^-24 in magnitude; the others are checked
-#pragma unroll
-            for (int e = 0; e < 8; ++e) fast = fast && (x[e] == 0.f || fabsf(x[e]) >= 0x1p-60f);
-        }
-        if (fast) {
-            const float y = 1.0f / den;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xn[e] = div_corrected(x[e], den, y);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xn[e] = x[e] / den;
-        }
-        const float s = is_v ? sv : sk, c = is_v ? cv : ck;
-        const float2 *t = tbl + is_v * kCells;
-        const float *bb = bnd + is_v * 16;
-        const int nb = is_v ? nvb : nkb;
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int kb0 = (e / BLK) * BLK;  // block start inside this lane's 8 elements
-            float acc = xn[kb0] * rt[e][0];
-#pragma unroll
-            for (int i = 1; i < BLK; ++i) acc = __builtin_fmaf(xn[kb0 + i], rt[e][i], acc);
-            uint32_t idx;
-            if (use_tbl) {
-                const float2 ent = t[cell_of(acc, s, c)];
-                idx = (uint32_t)__float_as_int(ent.y) + (ent.x < acc ? 1u : 0u);
             } else {
-                idx = 0;
-                for (int b = 0; b < nb; ++b) idx += bb[b] < acc ? 1u : 0u;
+                float x[8];
+                load8<S>(rows + rr * pitch + part * 8 * EB, x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) fast = fast && (x[e] == 0.f || fabsf(x[e]) >= 0x1p-60f);
+                if (fast) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xn[e] = div_dd(x[e], d, yh, yl);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xn[e] = x[e] / d;
+                }
             }
-            // byte e/2: even coordinate in the high nibble, odd in the low one
-            word |= idx << (8 * (e >> 1) + ((e & 1) ? 0 : 4));
+            float acc[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int kb0 = (e / BLK) * BLK;  // block start inside this lane's 8 elements
+                float a = xn[kb0] * rt[e][0];
+#pragma unroll
+                for (int i = 1; i < BLK; ++i) a = __builtin_fmaf(xn[kb0 + i], rt[e][i], a);
+                acc[e] = a;
+            }
+            uint32_t word = 0;
+            if (use_tbl) {
+                const float s = is_v ? sv : sk, c = is_v ? cv : ck;
+                const float2 *t = tbl + is_v * kCells;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float2 ent = t[cell_of(acc[e], s, c)];
+                    const uint32_t idx = (uint32_t)__float_as_int(ent.y) + (ent.x < acc[e] ? 1u : 0u);
+                    // byte e/2: even coordinate in the high nibble, odd in the low one
+                    word |= idx << (8 * (e >> 1) + ((e & 1) ? 0 : 4));
+                }
+            } else {
+                const float *bb = bnd + is_v * 16;
+                const int nb = is_v ? nvb : nkb;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    uint32_t idx = 0;
+                    for (int b = 0; b < nb; ++b) idx += bb[b] < acc[e] ? 1u : 0u;
+                    word |= idx << (8 * (e >> 1) + ((e & 1) ? 0 : 4));
+                }
+            }
+            gbl(dst)[part] = word;
         }
-        dst[part] = word;
+        if (!has_next) break;
+        g = gn;
+        __syncthreads();  // rows and this buffer's addresses are reused next
     }
+}
+
+// Resident workgroups of a compress kernel on the current device (cached).
+template <int DT, int BLK>
+static int compress_grid(size_t lds, int64_t n_groups) {
+    static int per_cu[64] = {0};
+    static size_t for_lds[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (per_cu[dev] == 0 || for_lds[dev] != lds) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&compress_kernel<DT, BLK>),
+                                                         kThreads, lds) != hipSuccess || nb <= 0)
+            nb = 4;
+        per_cu[dev] = nb;
+        for_lds[dev] = lds;
+    }
+    const int64_t g = (int64_t)per_cu[dev] * device_cus();
+    return (int)(g < n_groups ? g : n_groups);
 }
 
 template <int DT, int BLK>
@@ -417,7 +600,7 @@ static int launch_compress_blk(const RowMap &m, int64_t n_rows, int D, const flo
                                const float *kb, int nkb, const float *vb, int nvb, hipStream_t st) {
     int eb = DT == RQ_DTYPE_F32 ? 4 : 2;
     size_t lds = (size_t)kOffRows + (size_t)kRows * (D * eb + 16);
-    int64_t grid = (n_rows + kRows - 1) / kRows;
+    const int grid = compress_grid<DT, BLK>(lds, (n_rows + kRows - 1) / kRows);
     hipLaunchKernelGGL((compress_kernel<DT, BLK>), dim3((unsigned)grid), dim3(kThreads), lds, st, m, n_rows, D, rte,
                        rto, kb, nkb, vb, nvb);
     return check_launch("compress_kernel");
