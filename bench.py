@@ -165,7 +165,11 @@ def time_decode(inp, steps, warmup, graphs=False):
 
 
 def time_compress(n_tokens=32768, H=8, D=128, steps=20):
-    """rq_compress_store of n_tokens K+V (fp16) into random slots: bytes = N * (2*H*D*2 + 136*H + 8)."""
+    """rq_compress_store of n_tokens K+V (fp16) into random slots.
+
+    Bytes per token: K and V rows read (2*H*D*2), the slot id (8) and the whole
+    256*H-byte slot written (payload plus the zeroed padding the cache format
+    requires)."""
     import torch
 
     from rotorquant_vllm import kernels as K
@@ -191,7 +195,7 @@ def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     e.record()
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / steps
-    nbytes = n_tokens * (2 * H * D * 2 + 136 * H + 8)
+    nbytes = n_tokens * (2 * H * D * 2 + 8 + 256 * H)
     return dict(tokens=n_tokens, us=ms * 1e3, GBps=nbytes / (ms * 1e-3) / 1e9)
 
 
