@@ -32,6 +32,7 @@ for _p in (os.path.join(ROOT, "rotorquant-vllm_amd"), os.path.join(ROOT, "oracle
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
 def cpu_model() -> str:
@@ -51,8 +52,12 @@ def config1_lens(B=64, cfg=1):
 
 
 def build_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=3, v_bits=3, iso_mode="fast",
-                        copies=3):
-    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store."""
+                        copies=3, kv="config0", kv_dtype="float16"):
+    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store.
+
+    kv: "config0" K and V N(0,1) * (1 + |N(0,3)|) per (head, channel); "kscale"
+    only K scaled that way, V N(0,1); "outlier" K N(0,1) with 4 seeded channels
+    per head at 10x, V N(0,1)."""
     import numpy as np
     import torch
 
@@ -69,12 +74,20 @@ def build_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bit
     gs = torch.Generator(device=dev).manual_seed(1000 * cfg + 2)
     k_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
     v_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
+    if kv != "config0":
+        v_scale = torch.ones(H, D, device=dev)
+    if kv == "outlier":
+        k_scale = torch.ones(H, D, device=dev)
+        go = torch.Generator().manual_seed(1000 * cfg + 2)
+        for h in range(H):
+            k_scale[h, torch.randperm(D, generator=go)[:4].to(dev)] = 10.0
+    kdt = getattr(torch, kv_dtype)
     rte, rto, kb, vb = (t.to(dev) for t in (p.rte, p.rto, p.kb, p.vb))
     chunk = 32768
     for s in range(0, slot_all.numel(), chunk):
         n = min(chunk, slot_all.numel() - s)
-        k = (torch.randn(n, H, D, generator=g, device=dev) * k_scale).to(torch.float16)
-        v = (torch.randn(n, H, D, generator=g, device=dev) * v_scale).to(torch.float16)
+        k = (torch.randn(n, H, D, generator=g, device=dev) * k_scale).to(kdt)
+        v = (torch.randn(n, H, D, generator=g, device=dev) * v_scale).to(kdt)
         K.compress_store(k, v, cache, slot_all[s:s + n], rte, rto, kb, vb, rot_block=p.blk)
     caches = [cache] + [cache.clone() for _ in range(copies - 1)]
     q = torch.randn(len(lens), HQ, D, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
@@ -162,6 +175,121 @@ def time_decode(inp, steps, warmup, graphs=False):
     exact = all(torch.equal(o, e) for o, e in zip(outs, eager))
     return dict(wall_s=wall, avg_ms=total_ms / steps, median_ms=per[len(per) // 2], min_ms=per[0],
                 graphs=bool(g_list), replay_matches_eager=exact), outs[0]
+
+
+def time_events(fn, steps, warmup=2):
+    """Average ms of `fn()` over `steps` calls bracketed by events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def decode_config(cfg, steps=10):
+    """Decode throughput on BASELINE config 2 (planar K4/V3, B 256, L log-uniform [2048, 32768])
+    or the decode part of config 4 (Qwen2.5-7B layout, iso full 3-bit, 1 x 131072 + 127 x U[512, 16384])."""
+    import torch
+
+    from rq_testlib import lens_loguniform
+    if cfg == 2:
+        lens = lens_loguniform(256, 2048, 32768, 2)
+        inp = build_decode_inputs(lens, cfg=2, mode="planar", k_bits=4, v_bits=3, copies=1, kv="outlier")
+        H, HQ = 8, 32
+    else:
+        lens = [131072] + torch.randint(512, 16384 + 1, (127,), generator=torch.Generator().manual_seed(4004)).tolist()
+        inp = build_decode_inputs(lens, H=4, HQ=28, cfg=4, mode="iso", iso_mode="full", copies=1, kv="kscale",
+                                  kv_dtype="bfloat16")
+        H, HQ = 4, 28
+    t, _ = time_decode(inp, steps, 3)
+    nb = decode_bytes(lens, H, HQ, 128, 16)
+    gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
+    out = dict(batch=len(lens), sum_ctx_tokens=int(sum(lens)), us=round(t["avg_ms"] * 1e3, 1), GBps=round(gbs, 1),
+               pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2), decode_tok_per_s=round(len(lens) / (t["avg_ms"] * 1e-3), 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
+def prefill_inputs(q_lens, ctx_lens, H, HQ, cfg, mode, bits, iso_mode="fast"):
+    """Cache holding every sequence's context (new tokens included) and bf16 N(0,1) queries for the new tokens."""
+    import numpy as np
+    import torch
+    inp = build_decode_inputs(ctx_lens, H=H, HQ=HQ, cfg=cfg, mode=mode, k_bits=bits, v_bits=bits, iso_mode=iso_mode,
+                              copies=1, kv="kscale", kv_dtype="bfloat16")
+    dev = inp["q"].device
+    T = int(sum(q_lens))
+    inp["q"] = torch.randn(T, HQ, 128, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
+                           device=dev).to(torch.bfloat16)
+    inp["cu"] = torch.from_numpy(np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)).to(dev)
+    inp["q_lens"] = list(q_lens)
+    return inp
+
+
+def prefill_call(inp):
+    from rotorquant_vllm import kernels as K
+    p, dev = inp["p"], inp["q"].device
+    kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
+    out = __import__("torch").empty_like(inp["q"])
+
+    def fn():
+        K.fused_paged_rq_int8_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], kc, vc, R, inp["H"], 128,
+                                      inp["BS"], out=out, cu_seqlens_q=inp["cu"], max_q_len=max(inp["q_lens"]))
+    return fn
+
+
+def causal_macs(q_lens, ctx_lens, HQ, D=128):
+    """Multiply-adds of Q K^T plus P V over the causal band (query i of a sequence sees ctx - q + i + 1 keys)."""
+    n = 0
+    for q, c in zip(q_lens, ctx_lens):
+        pre = c - q
+        n += q * pre + q * (q + 1) // 2
+    return 2 * n * HQ * D
+
+
+def time_prefill_cfg3(steps=5):
+    """8 x 4096 new tokens, causal, 32 q / 8 kv, iso fast 4-bit, int8 MFMA.
+
+    Algorithmic int8 ops = 2 x (Q K^T + P V multiply-adds over the causal band);
+    the kernel issues three int8 MFMAs per product (hi.hi, hi.lo, lo.hi parts),
+    so issued ops are about 3x that (plus the masked part of diagonal tiles)."""
+    import torch
+    q_lens = [4096] * 8
+    inp = prefill_inputs(q_lens, q_lens, 8, 32, 3, "iso", 4)
+    fn = prefill_call(inp)
+    ms = time_events(fn, steps)
+    ops = 2 * causal_macs(q_lens, q_lens, 32)
+    tops = ops / (ms * 1e-3) / 1e12
+    out = dict(tokens=sum(q_lens), us=round(ms * 1e3, 1), algorithmic_TOPS=round(tops, 1),
+               issued_int8_TOPS=round(3 * tops, 1), int8_peak_TOPS=INT8_PEAK_TOPS,
+               frac_peak_algorithmic=round(tops / INT8_PEAK_TOPS, 4),
+               frac_peak_issued=round(3 * tops / INT8_PEAK_TOPS, 4))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
+def time_mixed_cfg4(steps=5):
+    """BASELINE config 4's chunked-prefill part: 4 chunks of 2048 new tokens, each after a seeded
+    prefix of U[0, 16384] cached tokens (Qwen2.5-7B layout, iso full 3-bit)."""
+    import torch
+    pre = [16 * x for x in torch.randint(0, 1024 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()]
+    q_lens = [2048] * 4
+    ctx = [p + 2048 for p in pre]
+    inp = prefill_inputs(q_lens, ctx, 4, 28, 4, "iso", 3, iso_mode="full")
+    ms = time_events(prefill_call(inp), steps)
+    ops = 2 * causal_macs(q_lens, ctx, 28)
+    out = dict(chunks=4, prefix_tokens=pre, us=round(ms * 1e3, 1),
+               algorithmic_TOPS=round(ops / (ms * 1e-3) / 1e12, 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_compress(n_tokens=32768, H=8, D=128, steps=20):
@@ -252,6 +380,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a kernel of known traffic for counter calibration)")
@@ -307,6 +436,13 @@ def main():
     }
     if not args.no_compress:
         result["compress"] = time_compress()
+    if not args.no_extra:
+        del inp["caches"][1:]
+        torch.cuda.empty_cache()
+        result["prefill_config3"] = time_prefill_cfg3()
+        result["decode_config2"] = decode_config(2)
+        result["decode_config4"] = decode_config(4)
+        result["prefill_config4_chunks"] = time_mixed_cfg4()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(inp)
     print(json.dumps(result), flush=True)
