@@ -41,6 +41,32 @@ struct SlotLayout {
     }
 };
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(size_t)(lds_u8 *)p; }
+
+// Direct global -> LDS copies, issued as inline assembly so that the compiler
+// neither waits for them before unrelated LDS accesses nor counts them: the
+// kernel waits for them itself with s_waitcnt vmcnt.  Lane l writes its bytes
+// at LDS address m0 + l * size (m0 = wave-uniform destination).
+//   copy16:  16 bytes from the uniform base `src` + per-lane 32-bit offset.
+//   copy16v: 16 bytes from a per-lane address.
+//   copy4:   4 bytes from a per-lane address.
+__device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "s"(dst)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void copy16v(const uint8_t *src, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+__device__ __forceinline__ void copy4(const uint8_t *src, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_copies() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Compute units of the current device (cached per device).
 inline int device_cus() {
     static int cached[64] = {0};

@@ -63,6 +63,19 @@ __device__ __forceinline__ uint32_t lookup_i8(const Table8 &t, uint32_t sel) {
     }
 }
 
+// Integral x in [-128, 127] converted into byte `byte` of w (other bytes kept),
+// one v_cvt_i32_f32 with an SDWA byte destination.
+template <int UNUSED>
+__device__ __forceinline__ uint32_t cvt_i8_into(float x, uint32_t w, int byte) {
+    switch (byte) {
+        case 0: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
+        case 1: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
+        case 2: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
+        default: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
+    }
+    return w;
+}
+
 __device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
 
 struct PrefillArgs {
@@ -89,17 +102,27 @@ struct PrefillArgs {
 };
 
 // LDS layout (bytes).  The per-wave staging buffers (q_rot before the key
-// loop, out_rot after it) alias the tile area, which is idle then.
-constexpr int kLdsKhi = 0;                          // [64 keys][128] int8, dims permuted per 8
-constexpr int kLdsKlo = kLdsKhi + kKT * kPD;        // same, low parts
-constexpr int kLdsVthi = kLdsKlo + kKT * kPD;       // [128 dims][64 keys in MFMA k order] int8
-constexpr int kLdsVtlo = kLdsVthi + kKT * kPD;      // same, low parts
-constexpr int kLdsSk = kLdsVtlo + kKT * kPD;        // [64] float: k norm * kmax/127 * score_scale
-constexpr int kLdsSw = kLdsSk + kKT * 4;            // [64] float: v norm
-constexpr int kLdsSwTile = kLdsSw + kKT * 4;        // [4] float: tile max v norm / 127 (+ pad)
+// loop, out_rot after it) alias the tile area, which is idle then.  Row pitches
+// are padded (K 144 B, V^T 80 B) so that the 16 lanes of an MFMA operand read hit
+// 16 distinct 4-bank groups.
+constexpr int kKP = kPD + 16;                       // K row pitch
+constexpr int kVP = kKT + 16;                       // V^T row pitch
+constexpr int kRawVP = 4 * 64 + 16;                 // raw V chunk pitch (4 keys x 64 bytes, padded)
+constexpr int kLdsKhi = 0;                          // [64 keys][kKP] int8, dims permuted per 8
+constexpr int kLdsKlo = kLdsKhi + kKT * kKP;        // same, low parts
+constexpr int kLdsVthi = kLdsKlo + kKT * kKP;       // [128 dims][kVP] int8, keys in MFMA k order
+constexpr int kLdsVtlo = kLdsVthi + kPD * kVP;      // same, low parts
+constexpr int kLdsSk = kLdsVtlo + kPD * kVP;        // [64] float: k norm * kmax/127 * score_scale / 128
+constexpr int kLdsSw = kLdsSk + kKT * 4;            // [64] float: v norm / tile scale (w = p * this)
+constexpr int kLdsSwTile = kLdsSw + kKT * 4;        // [4] float: tile scale = max v norm / 127 (+ pad)
 constexpr int kLdsOff = kLdsSwTile + 16;            // [64] uint64 token byte offsets
-constexpr int kLdsEnd = kLdsOff + kKT * 8;
+constexpr int kLdsRawK = kLdsOff + kKT * 8;         // [64 keys][16] dwords: packed K indices of the next tile
+constexpr int kLdsRawV = kLdsRawK + kKT * 64;       // [16 key quads][kRawVP]: same for V
+constexpr int kLdsRawN = kLdsRawV + 16 * kRawVP;    // [2][64] float: K norms, V norms
+constexpr int kLdsTab = kLdsRawN + 2 * kKT * 4;     // 4 x Table8: K hi, K lo, V hi, V lo
+constexpr int kLdsEnd = kLdsTab + 4 * 16;
 constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave: 16 x 128 16-bit values
+constexpr int kRawChunks = 2 * 16 + 2;               // wave-wide copies per tile (256 bytes each)
 
 template <int DT, int KB, int VB>
 __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
@@ -114,7 +137,7 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
     if (qblk * a.qb >= T || T <= 0) return;
 
     const int tid = threadIdx.x, nthr = blockDim.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, col = lane & 15;
     const int gh = wave / a.npg;            // query head inside the GQA group
     const int pg = wave - gh * a.npg;       // 16-position group
@@ -160,6 +183,9 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
         tvh.w[w] = vhw;
         tvl.w[w] = vlw;
     }
+    // The tables live in LDS across the key loop (reloaded per tile for the decode
+    // step) so that they hold no registers during the attention math.
+    Table8 *tab = reinterpret_cast<Table8 *>(lds + kLdsTab);
     const float k_unit = kmax / 127.f * a.score_scale;  // k int8 unit, in log2-domain score units
     const float v_unit = vmax / 127.f;
 
@@ -234,85 +260,127 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) acc[m][i] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    for (int k0 = 0; k0 < kv_end; k0 += kKT) {
-        const int nk = min(kKT, kv_end - k0);
-        __syncthreads();  // previous tile fully consumed
-        // ---- token offsets and norms of this key tile ----
-        for (int t = tid; t < kKT; t += nthr) {
-            uint64_t off = 0;
-            float skv = 0.f, nv = 0.f;
-            if (t < nk) {
-                const int pos = k0 + t;
-                int lb, o;
-                if (a.bs_shift >= 0) {
-                    lb = pos >> a.bs_shift;
-                    o = pos & (a.block_size - 1);
-                } else {
-                    lb = pos / a.block_size;
-                    o = pos - lb * a.block_size;
-                }
-                int64_t phys = bt_row[lb];
-                phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
-                off = (uint64_t)(phys * a.stride_block + (int64_t)o * a.stride_token);
-                skv = *reinterpret_cast<const float *>(a.cache + off + SL.k_norm + 4 * h) * k_unit;
-                nv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
+    // ---- tile pipeline ------------------------------------------------------
+    // Tile t's packed bytes (K and V indices, norms) are copied global -> LDS
+    // (direct, wave-wide 256-byte copies) while tile t-1 is computed, and decoded
+    // into the int8 operand buffers at the top of tile t.  Block-table entries
+    // are loaded one tile earlier still, so token offsets are ready when the
+    // copies are issued.  Keys past the tile's end read slot 0 (offset 0) and are
+    // masked; their norms are zeroed.
+    const int n_tiles = (kv_end + kKT - 1) / kKT;
+    int32_t bt_next = 0;  // threads < 64: block-table entry of its key two tiles ahead
+    auto tile_keys = [&](int t) { return min(kKT, kv_end - t * kKT); };
+    auto bt_entry = [&](int t) -> int32_t {  // threads < 64, tile t (t < n_tiles)
+        const int pos = t * kKT + tid;
+        const int lb = a.bs_shift >= 0 ? (pos >> a.bs_shift) : pos / a.block_size;
+        return tid < tile_keys(t) ? bt_row[lb] : 0;
+    };
+    auto set_offset = [&](int t, int32_t phys_in) {  // threads < 64: token offset of key tid of tile t
+        const int pos = t * kKT + tid;
+        const int o = a.bs_shift >= 0 ? (pos & (a.block_size - 1)) : pos % a.block_size;
+        int64_t phys = phys_in;
+        phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
+        toff[tid] = tid < tile_keys(t) ? (uint64_t)(phys * a.stride_block + (int64_t)o * a.stride_token) : 0ull;
+    };
+    // Copies of one tile: chunks 0-15 K indices (4 keys x 64 bytes each), 16-31 V
+    // indices, 32 K norms, 33 V norms; chunk c goes to wave c % nwaves.
+    const int nwaves = nthr >> 6;
+    const uint32_t raw_lds = lds_addr(lds);
+    auto issue_raw = [&]() {
+        for (int ch = wave; ch < kRawChunks; ch += nwaves) {
+            if (ch < 32) {
+                const int kind = ch >> 4, cc = ch & 15;
+                const int tk = 4 * cc + (lane >> 4), dw = lane & 15;
+                const uint8_t *src = a.cache + toff[tk] + (kind ? SL.v_idx : SL.k_idx) + h * 64 + 4 * dw;
+                copy4(src, raw_lds + (kind ? kLdsRawV + kRawVP * cc : kLdsRawK + 256 * cc));
+            } else {
+                const int kind = ch - 32;
+                const uint8_t *src = a.cache + toff[lane] + (kind ? SL.v_norm : SL.k_norm) + 4 * h;
+                copy4(src, raw_lds + kLdsRawN + 256 * kind);
             }
-            toff[t] = off;
-            sk[t] = skv;
-            sw[t] = nv;
         }
+    };
+    const uint32_t *raw_k = reinterpret_cast<const uint32_t *>(lds + kLdsRawK);
+    const uint32_t *raw_v = reinterpret_cast<const uint32_t *>(lds + kLdsRawV);
+    const float *raw_n = reinterpret_cast<const float *>(lds + kLdsRawN);
+    if (n_tiles > 0) {
+        if (tid == 0) {
+            tab[0] = tkh;
+            tab[1] = tkl;
+            tab[2] = tvh;
+            tab[3] = tvl;
+        }
+        if (tid < kKT) {
+            set_offset(0, bt_entry(0));
+            if (n_tiles > 1) bt_next = bt_entry(1);
+        }
+        __syncthreads();  // offsets visible; every wave is done with its q staging (aliases this area)
+        issue_raw();
+        wait_copies<0>();
         __syncthreads();
-        // tile scale for w = p * v_norm: largest v norm of the tile / 127
-        if (wave == 0) {
-            float mx = fmaxf(sw[lane], 0.f);
+    }
+
+    for (int ti = 0; ti < n_tiles; ++ti) {
+        const int k0 = ti * kKT;
+        const int nk = tile_keys(ti);
+        // ---- decode tile ti from the raw copies into LDS; offsets of tile ti+1 ----
+        if (tid < kKT) {
+            const float nkv = tid < nk ? raw_n[tid] : 0.f, nvv = tid < nk ? raw_n[kKT + tid] : 0.f;
+            sk[tid] = nkv * (k_unit * (1.f / 128.f));
+            float mx = fmaxf(nvv, 0.f);  // tile scale for w = p * v_norm: largest v norm / 127
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-            if (lane == 0) sw_tile[0] = mx > 0.f ? mx / 127.f : 1.f;
+            const float s_w = mx > 0.f ? mx / 127.f : 1.f;
+            sw[tid] = nvv / s_w;  // in [0, 127]
+            if (tid == 0) sw_tile[0] = s_w;
         }
-        // ---- decode K (row-major, permuted dims, hi and lo) ----
+        const Table8 ukh = tab[0], ukl = tab[1];
         for (int w = tid; w < kKT * 16; w += nthr) {
-            const int t = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
-            uint32_t x = 0;
-            if (t < nk) x = *reinterpret_cast<const uint32_t *>(a.cache + toff[t] + SL.k_idx + h * 64 + 4 * dw);
+            const int tk = w >> 4, dw = w & 15;
+            const uint32_t x = raw_k[w];
             const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
-            uint2 hi = make_uint2(lookup_i8<KB>(tkh, even), lookup_i8<KB>(tkh, odd));
-            uint2 lo = make_uint2(lookup_i8<KB>(tkl, even), lookup_i8<KB>(tkl, odd));
-            *reinterpret_cast<uint2 *>(lds + kLdsKhi + t * kPD + 8 * dw) = hi;
-            *reinterpret_cast<uint2 *>(lds + kLdsKlo + t * kPD + 8 * dw) = lo;
+            uint2 hi = make_uint2(lookup_i8<KB>(ukh, even), lookup_i8<KB>(ukh, odd));
+            uint2 lo = make_uint2(lookup_i8<KB>(ukl, even), lookup_i8<KB>(ukl, odd));
+            *reinterpret_cast<uint2 *>(lds + kLdsKhi + tk * kKP + 8 * dw) = hi;
+            *reinterpret_cast<uint2 *>(lds + kLdsKlo + tk * kKP + 8 * dw) = lo;
         }
-        // ---- decode V transposed: Vt[dim][kk], kk = MFMA k index of key t:
-        //      key t = 16b + 4g + i  ->  kk = 16g + 4b + i ----
-        for (int w = tid; w < 16 * 16; w += nthr) {
-            const int tq = w >> 4, dw = w & 15;  // key quad (4 consecutive keys), dword position
-            uint32_t x[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 4 * tq + i;
-                x[i] = t < nk ? *reinterpret_cast<const uint32_t *>(a.cache + toff[t] + SL.v_idx + h * 64 + 4 * dw)
-                              : 0u;
-            }
-            const uint32_t A01 = perm(x[1], x[0], 0x05010400u), B01 = perm(x[1], x[0], 0x07030602u);
-            const uint32_t A23 = perm(x[3], x[2], 0x05010400u), B23 = perm(x[3], x[2], 0x07030602u);
+        // V transposed: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
+        const Table8 uvh = tab[2], uvl = tab[3];
+        for (int w = tid; w < 256; w += nthr) {
+            const int tq = w & 15, dw = w >> 4;  // a wave covers all 16 key quads of 4 dwords
+            const uint32_t *rq = raw_v + tq * (kRawVP / 4) + dw;
+            const uint32_t rv[4] = {rq[0], rq[16], rq[32], rq[48]};
+            const uint32_t A01 = perm(rv[1], rv[0], 0x05010400u), B01 = perm(rv[1], rv[0], 0x07030602u);
+            const uint32_t A23 = perm(rv[3], rv[2], 0x05010400u), B23 = perm(rv[3], rv[2], 0x07030602u);
             const uint32_t G4[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u),
                                     perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
-            const int t0 = 4 * tq;                  // = 16b + 4gg
+            const int t0 = 4 * tq;  // = 16b + 4gg
             const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int d = 8 * dw + 2 * j;
                 const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
-                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + d * kKT + kk) = lookup_i8<VB>(tvh, se);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + (d + 1) * kKT + kk) = lookup_i8<VB>(tvh, so);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + d * kKT + kk) = lookup_i8<VB>(tvl, se);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + (d + 1) * kKT + kk) = lookup_i8<VB>(tvl, so);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + d * kVP + kk) = lookup_i8<VB>(uvh, se);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + (d + 1) * kVP + kk) = lookup_i8<VB>(uvh, so);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + d * kVP + kk) = lookup_i8<VB>(uvl, se);
+                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + (d + 1) * kVP + kk) = lookup_i8<VB>(uvl, so);
             }
         }
+        if (tid < kKT && ti + 1 < n_tiles) {
+            set_offset(ti + 1, bt_next);
+            if (ti + 2 < n_tiles) bt_next = bt_entry(ti + 2);
+        }
         __syncthreads();
-        if (!wave_active) continue;
-        if (k0 > pos_base + i0 + kPQ - 1) continue;  // tile entirely above this wave's diagonal
+        // ---- next tile's bytes in flight during this tile's math ----
+        if (ti + 1 < n_tiles) issue_raw();
+        // (every wave reaches the barrier at the end of the iteration)
+        if (wave_active && k0 <= pos_base + i0 + kPQ - 1) {  // else: tile entirely above this wave's diagonal
         const float s_w = sw_tile[0];
+        // every key of the tile visible to all 16 positions of this wave: no mask
+        const bool full = nk == kKT && k0 + kKT - 1 <= pos_base + i0;
 
         // ---- S^T = K Q^T for 4 key blocks of 16 ----
+        // s = (hi.hi * 128 + hi.lo + lo.hi) * k scale; the score proper is s * sq.
         float s[16];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -320,8 +388,8 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const int row = 16 * b + col;  // key
-                const u32x4 kh = *reinterpret_cast<const u32x4 *>(lds + kLdsKhi + row * kPD + 64 * st + 16 * g);
-                const u32x4 kl = *reinterpret_cast<const u32x4 *>(lds + kLdsKlo + row * kPD + 64 * st + 16 * g);
+                const u32x4 kh = *reinterpret_cast<const u32x4 *>(lds + kLdsKhi + row * kKP + 64 * st + 16 * g);
+                const u32x4 kl = *reinterpret_cast<const u32x4 *>(lds + kLdsKlo + row * kKP + 64 * st + 16 * g);
                 chh = mfma_i8(kh, qh[st], chh);
                 cx = mfma_i8(kh, ql[st], cx);
                 cx = mfma_i8(kl, qh[st], cx);
@@ -330,9 +398,9 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             const float skv[4] = {skb.x, skb.y, skb.z, skb.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const float v = (float)((chh[i] << 7) + cx[i]) * skv[i];
                 const int key = k0 + 16 * b + 4 * g + i;
-                const float v = ((float)chh[i] + (float)cx[i] * (1.f / 128.f)) * sq * skv[i];
-                s[4 * b + i] = (key < k0 + nk && key <= my_pos) ? v : -INFINITY;
+                s[4 * b + i] = (full || (key < k0 + nk && key <= my_pos)) ? v : -INFINITY;
             }
         }
         // ---- online softmax over this lane's 16 keys + the other 3 key groups ----
@@ -343,7 +411,7 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float m_new = fmaxf(m_run, tmax);
         if (__any(m_new > m_run)) {
-            const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sq);
 #pragma unroll
             for (int m = 0; m < 8; ++m)
 #pragma unroll
@@ -351,41 +419,46 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             l_run *= alpha;
             m_run = m_new;
         }
-        // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i)
+        // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
+        // p <= 1 and v_norm <= 127 s_w, so hi = rint(w) is in [0, 127] and lo = rint((w - hi) * 128)
+        // in [-64, 64]: no clamping; each converts straight into its byte of the operand.
+        const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
         uint32_t wh[4], wl[4];
-        const float inv_sw = 1.f / s_w;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const float4 nvb = *reinterpret_cast<const float4 *>(sw + 16 * b + 4 * g);
-            const float nvv[4] = {nvb.x, nvb.y, nvb.z, nvb.w};
+            const float4 cwb = *reinterpret_cast<const float4 *>(sw + 16 * b + 4 * g);
+            const float cwv[4] = {cwb.x, cwb.y, cwb.z, cwb.w};
             uint32_t hw = 0, lw = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[4 * b + i] - m_run);
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], sq, -msq));
                 l_run += p;
-                const float x = p * nvv[i] * inv_sw;
-                const int xh = sat_i8(x);
-                const int xl = sat_i8((x - (float)xh) * 128.f);
-                hw |= (uint32_t)(xh & 0xff) << (8 * i);
-                lw |= (uint32_t)(xl & 0xff) << (8 * i);
+                const float x = p * cwv[i];
+                const float xh = __builtin_rintf(x);
+                const float xl = __builtin_rintf((x - xh) * 128.f);
+                hw = cvt_i8_into<0>(xh, hw, i);
+                lw = cvt_i8_into<0>(xl, lw, i);
             }
             wh[b] = hw;
             wl[b] = lw;
         }
         const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
         // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
-        const float o_unit = s_w * v_unit;
+        const float o_unit = s_w * v_unit * (1.f / 128.f);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const u32x4 vah = *reinterpret_cast<const u32x4 *>(lds + kLdsVthi + (16 * m + col) * kKT + 16 * g);
-            const u32x4 val = *reinterpret_cast<const u32x4 *>(lds + kLdsVtlo + (16 * m + col) * kKT + 16 * g);
+            const u32x4 vah = *reinterpret_cast<const u32x4 *>(lds + kLdsVthi + (16 * m + col) * kVP + 16 * g);
+            const u32x4 val = *reinterpret_cast<const u32x4 *>(lds + kLdsVtlo + (16 * m + col) * kVP + 16 * g);
             const i32x4 zero = i32x4{0, 0, 0, 0};
             const i32x4 oh = mfma_i8(vah, ph, zero);
             i32x4 ol = mfma_i8(vah, pl, zero);
             ol = mfma_i8(val, ph, ol);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[m][i] += ((float)oh[i] + (float)ol[i] * (1.f / 128.f)) * o_unit;
+            for (int i = 0; i < 4; ++i) acc[m][i] = __builtin_fmaf((float)((oh[i] << 7) + ol[i]), o_unit, acc[m][i]);
         }
+        }
+        wait_copies<0>();  // the next tile's raw bytes have landed
+        __syncthreads();   // ... for every wave; this tile's LDS is rewritten next
     }
     __syncthreads();  // the staging buffers below alias the tile area
     if (!wave_active) return;
