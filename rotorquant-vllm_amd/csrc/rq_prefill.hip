@@ -303,6 +303,9 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
     const uint32_t *raw_k = reinterpret_cast<const uint32_t *>(lds + kLdsRawK);
     const uint32_t *raw_v = reinterpret_cast<const uint32_t *>(lds + kLdsRawV);
     const float *raw_n = reinterpret_cast<const float *>(lds + kLdsRawN);
+    // The q staging buffers above alias the tables, offsets and raw area written
+    // below (with more than nine waves): every wave must be done with its own.
+    __syncthreads();
     if (n_tiles > 0) {
         if (tid == 0) {
             tab[0] = tkh;
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             set_offset(0, bt_entry(0));
             if (n_tiles > 1) bt_next = bt_entry(1);
         }
-        __syncthreads();  // offsets visible; every wave is done with its q staging (aliases this area)
+        __syncthreads();  // offsets and tables visible
         issue_raw();
         wait_copies<0>();
         __syncthreads();
@@ -397,11 +400,12 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             const float4 skb = *reinterpret_cast<const float4 *>(sk + 16 * b + 4 * g);
             const float skv[4] = {skb.x, skb.y, skb.z, skb.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = (float)((chh[i] << 7) + cx[i]) * skv[i];
-                const int key = k0 + 16 * b + 4 * g + i;
-                s[4 * b + i] = (full || (key < k0 + nk && key <= my_pos)) ? v : -INFINITY;
-            }
+            for (int i = 0; i < 4; ++i) s[4 * b + i] = (float)((chh[i] << 7) + cx[i]) * skv[i];
+        }
+        if (!full) {  // causal and tile-end mask: key < min(k0 + nk, position + 1)
+            const int lim = min(k0 + nk, my_pos + 1) - (k0 + 4 * g);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s[j] = (16 * (j >> 2) + (j & 3)) < lim ? s[j] : -INFINITY;
         }
         // ---- online softmax over this lane's 16 keys + the other 3 key groups ----
         float tmax = s[0];

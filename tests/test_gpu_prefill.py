@@ -90,6 +90,13 @@ def test_prefill_unit_scale_bf16_iso4():
     check(case, "unit-iso4-bf16", plain_max_abs=True)
 
 
+def test_prefill_gqa16_one_kv_head():
+    """16 query heads on one kv head: the widest workgroup (16 waves), where the per-wave
+    q staging buffers overlap the tile area."""
+    p = Params("iso", 4, 3)
+    check(prefill_case(9, [200, 77], [260, 77], 1, 16, p), "gqa16")
+
+
 def test_prefill_multi_sequence_requires_cu_seqlens():
     from rotorquant_vllm import kernels as K
     p = Params()
