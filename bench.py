@@ -240,7 +240,8 @@ def prefill_call(inp):
 
     def fn():
         K.fused_paged_rq_int8_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], kc, vc, R, inp["H"], 128,
-                                      inp["BS"], out=out, cu_seqlens_q=inp["cu"], max_q_len=max(inp["q_lens"]))
+                                      inp["BS"], out=out, cu_seqlens_q=inp["cu"], max_q_len=max(inp["q_lens"]),
+                                      max_seq_len=max(inp["lens_host"]))
     return fn
 
 

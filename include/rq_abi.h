@@ -196,7 +196,11 @@ int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_
  *   at position i; both agree when q_len == seq_len.
  *
  * q / out: total_q x num_q_heads x head_dim, strides as for rq_fused_decode.
- * max_q_len bounds every q_len_b.  Other arguments as for rq_fused_decode.
+ * max_q_len bounds every q_len_b; max_seq_len bounds every seq_lens[b] (keys
+ * past it are not read).  workspace: rq_int8_prefill_workspace_bytes() bytes,
+ * 16-byte aligned, no initialisation needed (two launches: a pack kernel
+ * decodes the cache's K/V into int8 tile images there, the attention kernel
+ * streams them).  Other arguments as for rq_fused_decode.
  */
 int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
                     int64_t q_stride_tok, int64_t q_stride_head,
@@ -205,12 +209,18 @@ int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q
                     int64_t stride_block, int64_t stride_token,
                     int32_t num_kv_heads, int32_t head_dim,
                     const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
-                    const int32_t *seq_lens,
+                    const int32_t *seq_lens, int64_t max_seq_len,
                     const float *k_centroids, int32_t n_k_centroids,
                     const float *v_centroids, int32_t n_v_centroids,
                     const float *rotation, int32_t rot_block, float sm_scale,
                     void *out, int64_t out_stride_tok, int64_t out_stride_head,
+                    void *workspace, int64_t workspace_bytes,
                     void *stream);
+
+/* Workspace bytes rq_int8_prefill needs: one int8 tile image (about 39 KB)
+ * per 64 keys of max_seq_len, per sequence and kv head.  No counterpart in the
+ * reference, which decodes K/V inside its attention kernel. */
+int64_t rq_int8_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len);
 
 #ifdef __cplusplus
 }

@@ -17,10 +17,18 @@
 //     with the per-token scale norm * max|centroid| / 127; w = p * v_norm
 //     per 64-key tile scaled by the tile's largest v norm.
 //
-// Work split: one workgroup per (query block of QB positions, kv head,
-// sequence).  Its waves are (query head of the GQA group, 16-position group);
-// each 64-key tile of K/V is decoded once into LDS (int8) and shared by all of
-// them.  MFMA v_mfma_i32_16x16x64_i8 (wave64, lane l, g = l / 16):
+// Two kernels per call:
+//   * prefill_pack_kernel decodes every 64-key tile of every (sequence, kv head)
+//     once into an int8 "tile image" in the caller's workspace: K hi/lo rows, V^T
+//     hi/lo rows, per-key score scales and V weights, laid out exactly as the
+//     attention kernel keeps them in LDS (padded rows included);
+//   * prefill_attn_kernel: one workgroup per (query block of QB positions, kv
+//     head, sequence); its waves are (query head of the GQA group, 16-position
+//     group).  It streams the tile images of its sequence and kv head into a
+//     double-buffered LDS area with direct global -> LDS copies (the copy of
+//     tile t+1 runs while tile t is computed), so the inner loop is MFMA,
+//     softmax and the int8 quantization of P only.
+// MFMA v_mfma_i32_16x16x64_i8 (wave64, lane l, g = l / 16):
 //   A (16 x 64): lane holds row l % 16, k = 16g .. 16g+15 (16 bytes)
 //   B (64 x 16): lane holds col l % 16, k = 16g .. 16g+15
 //   C (16 x 16): lane holds col l % 16, rows 4g .. 4g+3 (4 int32)
@@ -97,70 +105,42 @@ struct PrefillArgs {
     float score_scale;  // sm_scale * log2(e)
     int qb;             // query positions per workgroup (= 16 * position groups)
     int npg;            // position groups per workgroup
+    int64_t max_tiles;  // tile images per (sequence, kv head) in the workspace
+    uint8_t *ws;        // tile images [num_seqs][H][max_tiles][kImBytes]
     void *out;
     int64_t o_st, o_sh;
 };
 
-// LDS layout (bytes).  The per-wave staging buffers (q_rot before the key
-// loop, out_rot after it) alias the tile area, which is idle then.  Row pitches
-// are padded (K 144 B, V^T 80 B) so that the 16 lanes of an MFMA operand read hit
-// 16 distinct 4-bank groups.
+// Tile image (bytes), the same in the workspace and in LDS.  Row pitches are
+// padded (K 144 B, V^T 80 B) so that the 16 lanes of an MFMA operand read hit 16
+// distinct 4-bank groups; the pad bytes are never written or read.
 constexpr int kKP = kPD + 16;                       // K row pitch
 constexpr int kVP = kKT + 16;                       // V^T row pitch
-constexpr int kRawVP = 4 * 64 + 16;                 // raw V chunk pitch (4 keys x 64 bytes, padded)
-constexpr int kLdsKhi = 0;                          // [64 keys][kKP] int8, dims permuted per 8
-constexpr int kLdsKlo = kLdsKhi + kKT * kKP;        // same, low parts
-constexpr int kLdsVthi = kLdsKlo + kKT * kKP;       // [128 dims][kVP] int8, keys in MFMA k order
-constexpr int kLdsVtlo = kLdsVthi + kPD * kVP;      // same, low parts
-constexpr int kLdsSk = kLdsVtlo + kPD * kVP;        // [64] float: k norm * kmax/127 * score_scale / 128
-constexpr int kLdsSw = kLdsSk + kKT * 4;            // [64] float: v norm / tile scale (w = p * this)
-constexpr int kLdsSwTile = kLdsSw + kKT * 4;        // [4] float: tile scale = max v norm / 127 (+ pad)
-constexpr int kLdsOff = kLdsSwTile + 16;            // [64] uint64 token byte offsets
-constexpr int kLdsRawK = kLdsOff + kKT * 8;         // [64 keys][16] dwords: packed K indices of the next tile
-constexpr int kLdsRawV = kLdsRawK + kKT * 64;       // [16 key quads][kRawVP]: same for V
-constexpr int kLdsRawN = kLdsRawV + 16 * kRawVP;    // [2][64] float: K norms, V norms
-constexpr int kLdsTab = kLdsRawN + 2 * kKT * 4;     // 4 x Table8: K hi, K lo, V hi, V lo
-constexpr int kLdsEnd = kLdsTab + 4 * 16;
-constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave: 16 x 128 16-bit values
-constexpr int kRawChunks = 2 * 16 + 2;               // wave-wide copies per tile (256 bytes each)
+constexpr int kImKhi = 0;                           // [64 keys][kKP] int8, dims permuted per 8
+constexpr int kImKlo = kImKhi + kKT * kKP;          // same, low parts
+constexpr int kImVthi = kImKlo + kKT * kKP;         // [128 dims][kVP] int8, keys in MFMA k order
+constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
+constexpr int kImSk = kImVtlo + kPD * kVP;          // [64] float: k norm * kmax/127 * score_scale / 128
+constexpr int kImCw = kImSk + kKT * 4;              // [64] float: v norm / tile scale, in [0, 127]
+constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile scale * vmax/127 / 128
+constexpr int kImBytes = (kImUnit + 16 + 1023) / 1024 * 1024;  // whole 1 KB copies
+constexpr int kImChunks = kImBytes / 1024;
+constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave q / out staging: 16 x 128 16-bit values
+static_assert(2 * kImBytes >= 16 * kWaveBytes, "staging must fit in the tile buffers");
 
-template <int DT, int KB, int VB>
-__global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
-    const int qblk = blockIdx.x;
-    const int h = blockIdx.y;
-    const int64_t seq = blockIdx.z;
-    const int q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
-    const int T = q1 - q0;
-    const int L = a.seq_lens[seq];
-    const int pos_base = L - T;  // position of query 0
-    const int L_eff = (int)min((int64_t)L, a.max_blocks * a.block_size);  // table capacity bounds the keys
-    if (qblk * a.qb >= T || T <= 0) return;
-
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int g = lane >> 4, col = lane & 15;
-    const int gh = wave / a.npg;            // query head inside the GQA group
-    const int pg = wave - gh * a.npg;       // 16-position group
-    const int hq = h * a.G + gh;
-    const int i0 = qblk * a.qb + pg * kPQ;  // first query index of this wave
-    const bool wave_active = i0 < T;
-    const int my_i = i0 + col;              // query index of this lane's column
-    const int my_pos = pos_base + my_i;
-
-    extern __shared__ __align__(16) uint8_t lds[];
-    float *sk = reinterpret_cast<float *>(lds + kLdsSk);
-    float *sw = reinterpret_cast<float *>(lds + kLdsSw);
-    float *sw_tile = reinterpret_cast<float *>(lds + kLdsSwTile);
-    uint64_t *toff = reinterpret_cast<uint64_t *>(lds + kLdsOff);
-    uint16_t *wbuf = reinterpret_cast<uint16_t *>(lds + wave * kWaveBytes);
-
-    // ---- tables ----------------------------------------------------------------
+// int8 hi / lo tables of the K and V codebooks: entry = c * 127 / max|c| rounded,
+// lo = the residual * 128 rounded.
+struct CodeTables {
+    Table8 kh, kl, vh, vl;
+    float kmax, vmax;
+};
+__device__ __forceinline__ CodeTables make_code_tables(const PrefillArgs &a) {
+    CodeTables t;
     float kmax = 0.f, vmax = 0.f;
     for (int e = 0; e < a.nkc; ++e) kmax = fmaxf(kmax, fabsf(a.kc[e]));
     for (int e = 0; e < a.nvc; ++e) vmax = fmaxf(vmax, fabsf(a.vc[e]));
     kmax = kmax > 0.f ? kmax : 1.f;
     vmax = vmax > 0.f ? vmax : 1.f;
-    Table8 tkh, tkl, tvh, tvl;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         uint32_t hw = 0, lw = 0, vhw = 0, vlw = 0;
@@ -178,16 +158,131 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             vhw |= (uint32_t)(vh & 0xff) << (8 * i);
             vlw |= (uint32_t)(vl & 0xff) << (8 * i);
         }
-        tkh.w[w] = hw;
-        tkl.w[w] = lw;
-        tvh.w[w] = vhw;
-        tvl.w[w] = vlw;
+        t.kh.w[w] = hw;
+        t.kl.w[w] = lw;
+        t.vh.w[w] = vhw;
+        t.vl.w[w] = vlw;
     }
-    // The tables live in LDS across the key loop (reloaded per tile for the decode
-    // step) so that they hold no registers during the attention math.
-    Table8 *tab = reinterpret_cast<Table8 *>(lds + kLdsTab);
-    const float k_unit = kmax / 127.f * a.score_scale;  // k int8 unit, in log2-domain score units
-    const float v_unit = vmax / 127.f;
+    t.kmax = kmax;
+    t.vmax = vmax;
+    return t;
+}
+
+// Keys of a sequence the attention may read: its length, bounded by the block
+// table's capacity and by the workspace's tile images.
+__device__ __forceinline__ int visible_keys(const PrefillArgs &a, int64_t seq) {
+    const int64_t cap = min(a.max_blocks * a.block_size, a.max_tiles * kKT);
+    return (int)min((int64_t)a.seq_lens[seq], cap);
+}
+
+// ---- pack: one workgroup (256 threads) per (tile, kv head, sequence) --------
+template <int KB, int VB>
+__global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
+    const int tile = blockIdx.x, h = blockIdx.y;
+    const int64_t seq = blockIdx.z;
+    const int L_eff = visible_keys(a, seq);
+    const int k0 = tile * kKT;
+    if (k0 >= L_eff) return;
+    const int nk = min(kKT, L_eff - k0);
+    const int tid = threadIdx.x;
+    uint8_t *img = a.ws + (((int64_t)seq * a.H + h) * a.max_tiles + tile) * kImBytes;
+    const SlotLayout SL(a.H, kPD);
+    __shared__ uint64_t toff[kKT];
+    const CodeTables ct = make_code_tables(a);
+
+    if (tid < kKT) {
+        // token offset (keys past the tile's end read slot 0 and get zero norms)
+        uint64_t off = 0;
+        float nkv = 0.f, nvv = 0.f;
+        if (tid < nk) {
+            const int pos = k0 + tid;
+            int lb, o;
+            if (a.bs_shift >= 0) {
+                lb = pos >> a.bs_shift;
+                o = pos & (a.block_size - 1);
+            } else {
+                lb = pos / a.block_size;
+                o = pos - lb * a.block_size;
+            }
+            int64_t phys = a.bt[seq * a.bt_ss + lb];
+            phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
+            off = (uint64_t)(phys * a.stride_block + (int64_t)o * a.stride_token);
+            nkv = *reinterpret_cast<const float *>(a.cache + off + SL.k_norm + 4 * h);
+            nvv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
+        }
+        toff[tid] = off;
+        float mx = fmaxf(nvv, 0.f);  // tile scale for w = p * v_norm: largest v norm / 127
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float s_w = mx > 0.f ? mx / 127.f : 1.f;
+        reinterpret_cast<float *>(img + kImSk)[tid] = nkv * (ct.kmax / 127.f * a.score_scale * (1.f / 128.f));
+        reinterpret_cast<float *>(img + kImCw)[tid] = nvv / s_w;
+        if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_w * (ct.vmax / 127.f) * (1.f / 128.f);
+    }
+    __syncthreads();
+    // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
+    for (int w = tid; w < kKT * 16; w += 256) {
+        const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
+        const uint32_t x = *reinterpret_cast<const uint32_t *>(a.cache + toff[tk] + SL.k_idx + h * 64 + 4 * dw);
+        const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
+        *reinterpret_cast<uint2 *>(img + kImKhi + tk * kKP + 8 * dw) =
+            make_uint2(lookup_i8<KB>(ct.kh, even), lookup_i8<KB>(ct.kh, odd));
+        *reinterpret_cast<uint2 *>(img + kImKlo + tk * kKP + 8 * dw) =
+            make_uint2(lookup_i8<KB>(ct.kl, even), lookup_i8<KB>(ct.kl, odd));
+    }
+    // V^T rows: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
+    {
+        const int tq = tid & 15, dw = tid >> 4;  // key quad (4 consecutive keys), dword position
+        uint32_t x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            x[i] = *reinterpret_cast<const uint32_t *>(a.cache + toff[4 * tq + i] + SL.v_idx + h * 64 + 4 * dw);
+        const uint32_t A01 = perm(x[1], x[0], 0x05010400u), B01 = perm(x[1], x[0], 0x07030602u);
+        const uint32_t A23 = perm(x[3], x[2], 0x05010400u), B23 = perm(x[3], x[2], 0x07030602u);
+        const uint32_t G4[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u),
+                                perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
+        const int t0 = 4 * tq;  // = 16b + 4gg
+        const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = 8 * dw + 2 * j;
+            const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
+            *reinterpret_cast<uint32_t *>(img + kImVthi + d * kVP + kk) = lookup_i8<VB>(ct.vh, se);
+            *reinterpret_cast<uint32_t *>(img + kImVthi + (d + 1) * kVP + kk) = lookup_i8<VB>(ct.vh, so);
+            *reinterpret_cast<uint32_t *>(img + kImVtlo + d * kVP + kk) = lookup_i8<VB>(ct.vl, se);
+            *reinterpret_cast<uint32_t *>(img + kImVtlo + (d + 1) * kVP + kk) = lookup_i8<VB>(ct.vl, so);
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
+    const int qblk = blockIdx.x;
+    const int h = blockIdx.y;
+    const int64_t seq = blockIdx.z;
+    const int q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
+    const int T = q1 - q0;
+    const int L = a.seq_lens[seq];
+    const int pos_base = L - T;  // position of query 0
+    const int L_eff = visible_keys(a, seq);
+    if (qblk * a.qb >= T || T <= 0) return;
+
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int nwaves = nthr >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int gh = wave / a.npg;            // query head inside the GQA group
+    const int pg = wave - gh * a.npg;       // 16-position group
+    const int hq = h * a.G + gh;
+    const int i0 = qblk * a.qb + pg * kPQ;  // first query index of this wave
+    const bool wave_active = i0 < T;
+    const int my_i = i0 + col;              // query index of this lane's column
+    const int my_pos = pos_base + my_i;
+
+    // LDS: two tile-image buffers; the per-wave q / out staging aliases them
+    // before the key loop and after it.
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint16_t *wbuf = reinterpret_cast<uint16_t *>(lds + wave * kWaveBytes);
 
     // ---- Q^T operand (cols = this wave's 16 positions): q_rot rounded to the q dtype,
     //      quantised per position to hi/lo int8, dims in the permuted order of K ----
@@ -250,8 +345,7 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
     // ---- key range: causal bound of the whole workgroup --------------------------
     const int last_i = min(T, (qblk + 1) * a.qb) - 1;
     const int kv_end = min(L_eff, pos_base + last_i + 1);  // keys [0, kv_end) may be visible
-    const SlotLayout SL(a.H, kPD);
-    const int32_t *bt_row = a.bt + seq * a.bt_ss;
+    const int n_tiles = (kv_end + kKT - 1) / kKT;
 
     float acc[8][4];
 #pragma unroll
@@ -260,125 +354,38 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) acc[m][i] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    // ---- tile pipeline ------------------------------------------------------
-    // Tile t's packed bytes (K and V indices, norms) are copied global -> LDS
-    // (direct, wave-wide 256-byte copies) while tile t-1 is computed, and decoded
-    // into the int8 operand buffers at the top of tile t.  Block-table entries
-    // are loaded one tile earlier still, so token offsets are ready when the
-    // copies are issued.  Keys past the tile's end read slot 0 (offset 0) and are
-    // masked; their norms are zeroed.
-    const int n_tiles = (kv_end + kKT - 1) / kKT;
-    int32_t bt_next = 0;  // threads < 64: block-table entry of its key two tiles ahead
-    auto tile_keys = [&](int t) { return min(kKT, kv_end - t * kKT); };
-    auto bt_entry = [&](int t) -> int32_t {  // threads < 64, tile t (t < n_tiles)
-        const int pos = t * kKT + tid;
-        const int lb = a.bs_shift >= 0 ? (pos >> a.bs_shift) : pos / a.block_size;
-        return tid < tile_keys(t) ? bt_row[lb] : 0;
-    };
-    auto set_offset = [&](int t, int32_t phys_in) {  // threads < 64: token offset of key tid of tile t
-        const int pos = t * kKT + tid;
-        const int o = a.bs_shift >= 0 ? (pos & (a.block_size - 1)) : pos % a.block_size;
-        int64_t phys = phys_in;
-        phys = (phys < 0 || phys >= a.num_blocks) ? 0 : phys;
-        toff[tid] = tid < tile_keys(t) ? (uint64_t)(phys * a.stride_block + (int64_t)o * a.stride_token) : 0ull;
-    };
-    // Copies of one tile: chunks 0-15 K indices (4 keys x 64 bytes each), 16-31 V
-    // indices, 32 K norms, 33 V norms; chunk c goes to wave c % nwaves.
-    const int nwaves = nthr >> 6;
-    const uint32_t raw_lds = lds_addr(lds);
-    auto issue_raw = [&]() {
-        for (int ch = wave; ch < kRawChunks; ch += nwaves) {
-            if (ch < 32) {
-                const int kind = ch >> 4, cc = ch & 15;
-                const int tk = 4 * cc + (lane >> 4), dw = lane & 15;
-                const uint8_t *src = a.cache + toff[tk] + (kind ? SL.v_idx : SL.k_idx) + h * 64 + 4 * dw;
-                copy4(src, raw_lds + (kind ? kLdsRawV + kRawVP * cc : kLdsRawK + 256 * cc));
-            } else {
-                const int kind = ch - 32;
-                const uint8_t *src = a.cache + toff[lane] + (kind ? SL.v_norm : SL.k_norm) + 4 * h;
-                copy4(src, raw_lds + kLdsRawN + 256 * kind);
-            }
+    // Tile images of this (sequence, kv head), copied global -> LDS 1 KB per wave
+    // instruction; tile t+1's copy runs while tile t is computed.
+    const uint8_t *img0 = a.ws + ((int64_t)seq * a.H + h) * a.max_tiles * kImBytes;
+    const uint32_t lds0 = lds_addr(lds);
+    auto issue_tile = [&](int t) {
+        const uint8_t *src = img0 + (int64_t)t * kImBytes;
+        const uint32_t dst = lds0 + (t & 1) * kImBytes;
+        for (int c = wave; c < kImChunks; c += nwaves) {
+            // wave-uniform operands of the copy (the compiler cannot prove it here)
+            const uint64_t s = reinterpret_cast<uint64_t>(src + c * 1024);
+            const uint32_t slo = __builtin_amdgcn_readfirstlane((uint32_t)s);
+            const uint32_t shi = __builtin_amdgcn_readfirstlane((uint32_t)(s >> 32));
+            const uint8_t *su = reinterpret_cast<const uint8_t *>(((uint64_t)shi << 32) | slo);
+            copy16(su, 16 * lane, __builtin_amdgcn_readfirstlane(dst + c * 1024));
         }
     };
-    const uint32_t *raw_k = reinterpret_cast<const uint32_t *>(lds + kLdsRawK);
-    const uint32_t *raw_v = reinterpret_cast<const uint32_t *>(lds + kLdsRawV);
-    const float *raw_n = reinterpret_cast<const float *>(lds + kLdsRawN);
-    // The q staging buffers above alias the tables, offsets and raw area written
-    // below (with more than nine waves): every wave must be done with its own.
-    __syncthreads();
+    __syncthreads();  // every wave is done with its q staging (it aliases the tile buffers)
     if (n_tiles > 0) {
-        if (tid == 0) {
-            tab[0] = tkh;
-            tab[1] = tkl;
-            tab[2] = tvh;
-            tab[3] = tvl;
-        }
-        if (tid < kKT) {
-            set_offset(0, bt_entry(0));
-            if (n_tiles > 1) bt_next = bt_entry(1);
-        }
-        __syncthreads();  // offsets and tables visible
-        issue_raw();
+        issue_tile(0);
         wait_copies<0>();
         __syncthreads();
     }
 
     for (int ti = 0; ti < n_tiles; ++ti) {
         const int k0 = ti * kKT;
-        const int nk = tile_keys(ti);
-        // ---- decode tile ti from the raw copies into LDS; offsets of tile ti+1 ----
-        if (tid < kKT) {
-            const float nkv = tid < nk ? raw_n[tid] : 0.f, nvv = tid < nk ? raw_n[kKT + tid] : 0.f;
-            sk[tid] = nkv * (k_unit * (1.f / 128.f));
-            float mx = fmaxf(nvv, 0.f);  // tile scale for w = p * v_norm: largest v norm / 127
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-            const float s_w = mx > 0.f ? mx / 127.f : 1.f;
-            sw[tid] = nvv / s_w;  // in [0, 127]
-            if (tid == 0) sw_tile[0] = s_w;
-        }
-        const Table8 ukh = tab[0], ukl = tab[1];
-        for (int w = tid; w < kKT * 16; w += nthr) {
-            const int tk = w >> 4, dw = w & 15;
-            const uint32_t x = raw_k[w];
-            const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
-            uint2 hi = make_uint2(lookup_i8<KB>(ukh, even), lookup_i8<KB>(ukh, odd));
-            uint2 lo = make_uint2(lookup_i8<KB>(ukl, even), lookup_i8<KB>(ukl, odd));
-            *reinterpret_cast<uint2 *>(lds + kLdsKhi + tk * kKP + 8 * dw) = hi;
-            *reinterpret_cast<uint2 *>(lds + kLdsKlo + tk * kKP + 8 * dw) = lo;
-        }
-        // V transposed: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
-        const Table8 uvh = tab[2], uvl = tab[3];
-        for (int w = tid; w < 256; w += nthr) {
-            const int tq = w & 15, dw = w >> 4;  // a wave covers all 16 key quads of 4 dwords
-            const uint32_t *rq = raw_v + tq * (kRawVP / 4) + dw;
-            const uint32_t rv[4] = {rq[0], rq[16], rq[32], rq[48]};
-            const uint32_t A01 = perm(rv[1], rv[0], 0x05010400u), B01 = perm(rv[1], rv[0], 0x07030602u);
-            const uint32_t A23 = perm(rv[3], rv[2], 0x05010400u), B23 = perm(rv[3], rv[2], 0x07030602u);
-            const uint32_t G4[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u),
-                                    perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
-            const int t0 = 4 * tq;  // = 16b + 4gg
-            const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int d = 8 * dw + 2 * j;
-                const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
-                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + d * kVP + kk) = lookup_i8<VB>(uvh, se);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVthi + (d + 1) * kVP + kk) = lookup_i8<VB>(uvh, so);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + d * kVP + kk) = lookup_i8<VB>(uvl, se);
-                *reinterpret_cast<uint32_t *>(lds + kLdsVtlo + (d + 1) * kVP + kk) = lookup_i8<VB>(uvl, so);
-            }
-        }
-        if (tid < kKT && ti + 1 < n_tiles) {
-            set_offset(ti + 1, bt_next);
-            if (ti + 2 < n_tiles) bt_next = bt_entry(ti + 2);
-        }
-        __syncthreads();
-        // ---- next tile's bytes in flight during this tile's math ----
-        if (ti + 1 < n_tiles) issue_raw();
+        const int nk = min(kKT, kv_end - k0);
+        const uint8_t *tb = lds + (ti & 1) * kImBytes;
+        const float *sk = reinterpret_cast<const float *>(tb + kImSk);
+        const float *sw = reinterpret_cast<const float *>(tb + kImCw);
+        if (ti + 1 < n_tiles) issue_tile(ti + 1);
         // (every wave reaches the barrier at the end of the iteration)
         if (wave_active && k0 <= pos_base + i0 + kPQ - 1) {  // else: tile entirely above this wave's diagonal
-        const float s_w = sw_tile[0];
         // every key of the tile visible to all 16 positions of this wave: no mask
         const bool full = nk == kKT && k0 + kKT - 1 <= pos_base + i0;
 
@@ -391,8 +398,8 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const int row = 16 * b + col;  // key
-                const u32x4 kh = *reinterpret_cast<const u32x4 *>(lds + kLdsKhi + row * kKP + 64 * st + 16 * g);
-                const u32x4 kl = *reinterpret_cast<const u32x4 *>(lds + kLdsKlo + row * kKP + 64 * st + 16 * g);
+                const u32x4 kh = *reinterpret_cast<const u32x4 *>(tb + kImKhi + row * kKP + 64 * st + 16 * g);
+                const u32x4 kl = *reinterpret_cast<const u32x4 *>(tb + kImKlo + row * kKP + 64 * st + 16 * g);
                 chh = mfma_i8(kh, qh[st], chh);
                 cx = mfma_i8(kh, ql[st], cx);
                 cx = mfma_i8(kl, qh[st], cx);
@@ -448,11 +455,11 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
         }
         const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
         // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
-        const float o_unit = s_w * v_unit * (1.f / 128.f);
+        const float o_unit = *reinterpret_cast<const float *>(tb + kImUnit);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const u32x4 vah = *reinterpret_cast<const u32x4 *>(lds + kLdsVthi + (16 * m + col) * kVP + 16 * g);
-            const u32x4 val = *reinterpret_cast<const u32x4 *>(lds + kLdsVtlo + (16 * m + col) * kVP + 16 * g);
+            const u32x4 vah = *reinterpret_cast<const u32x4 *>(tb + kImVthi + (16 * m + col) * kVP + 16 * g);
+            const u32x4 val = *reinterpret_cast<const u32x4 *>(tb + kImVtlo + (16 * m + col) * kVP + 16 * g);
             const i32x4 zero = i32x4{0, 0, 0, 0};
             const i32x4 oh = mfma_i8(vah, ph, zero);
             i32x4 ol = mfma_i8(vah, pl, zero);
@@ -461,8 +468,8 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) acc[m][i] = __builtin_fmaf((float)((oh[i] << 7) + ol[i]), o_unit, acc[m][i]);
         }
         }
-        wait_copies<0>();  // the next tile's raw bytes have landed
-        __syncthreads();   // ... for every wave; this tile's LDS is rewritten next
+        wait_copies<0>();  // the next tile's image has landed
+        __syncthreads();   // ... for every wave; this buffer is refilled next
     }
     __syncthreads();  // the staging buffers below alias the tile area
     if (!wave_active) return;
@@ -491,35 +498,47 @@ __global__ __launch_bounds__(1024) void prefill_kernel(PrefillArgs a) {
     }
 }
 
-template <int DT, int KB, int VB>
-static void launch_prefill(const PrefillArgs &a, int64_t num_seqs, int64_t max_q_len, int nwaves, hipStream_t st) {
-    const size_t lds = std::max<size_t>(kLdsEnd, (size_t)nwaves * kWaveBytes);
-    dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)a.H, (unsigned)num_seqs);
-    hipLaunchKernelGGL((prefill_kernel<DT, KB, VB>), grid, dim3(64 * nwaves), lds, st, a);
+template <int KB, int VB>
+static void launch_pack(const PrefillArgs &a, int64_t num_seqs, hipStream_t st) {
+    dim3 grid((unsigned)a.max_tiles, (unsigned)a.H, (unsigned)num_seqs);
+    hipLaunchKernelGGL((prefill_pack_kernel<KB, VB>), grid, dim3(256), 0, st, a);
+}
+
+static void launch_pack_bits(const PrefillArgs &a, int64_t ns, int kb, int vb, hipStream_t st) {
+    if (kb == 3 && vb == 3) launch_pack<3, 3>(a, ns, st);
+    else if (kb == 3) launch_pack<3, 4>(a, ns, st);
+    else if (vb == 3) launch_pack<4, 3>(a, ns, st);
+    else launch_pack<4, 4>(a, ns, st);
 }
 
 template <int DT>
-static void launch_prefill_bits(const PrefillArgs &a, int64_t ns, int64_t mq, int nw, int kb, int vb,
-                                hipStream_t st) {
-    if (kb == 3 && vb == 3) launch_prefill<DT, 3, 3>(a, ns, mq, nw, st);
-    else if (kb == 3) launch_prefill<DT, 3, 4>(a, ns, mq, nw, st);
-    else if (vb == 3) launch_prefill<DT, 4, 3>(a, ns, mq, nw, st);
-    else launch_prefill<DT, 4, 4>(a, ns, mq, nw, st);
+static void launch_attn(const PrefillArgs &a, int64_t num_seqs, int64_t max_q_len, int nwaves, hipStream_t st) {
+    const size_t lds = 2 * (size_t)kImBytes;
+    dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)a.H, (unsigned)num_seqs);
+    hipLaunchKernelGGL((prefill_attn_kernel<DT>), grid, dim3(64 * nwaves), lds, st, a);
 }
+
+static int64_t prefill_tiles(int64_t max_seq_len) { return (max_seq_len + kKT - 1) / kKT; }
 
 }  // namespace rq
 
 using namespace rq;
+
+extern "C" int64_t rq_int8_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len) {
+    if (num_seqs <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
+    return num_seqs * num_kv_heads * prefill_tiles(max_seq_len) * kImBytes;
+}
 
 extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
                                int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
                                int64_t num_seqs, int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks,
                                int32_t block_size, int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
                                int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
-                               int64_t bt_stride_seq, const int32_t *seq_lens, const float *k_centroids,
-                               int32_t n_k_centroids, const float *v_centroids, int32_t n_v_centroids,
-                               const float *rotation, int32_t rot_block, float sm_scale, void *out,
-                               int64_t out_stride_tok, int64_t out_stride_head, void *stream) {
+                               int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
+                               const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
+                               int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
+                               void *out, int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
+                               int64_t workspace_bytes, void *stream) {
     RQ_CHECK_ARG(dtype == RQ_DTYPE_BF16 || dtype == RQ_DTYPE_F16, "prefill dtype must be f16 or bf16");
     RQ_CHECK_ARG(head_dim == kPD, "head_dim %d unsupported (only %d)", head_dim, kPD);
     RQ_CHECK_ARG(num_kv_heads >= 1 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 16,
@@ -527,11 +546,16 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     RQ_CHECK_ARG((n_k_centroids == 8 || n_k_centroids == 16) && (n_v_centroids == 8 || n_v_centroids == 16),
                  "centroid counts must be 8 or 16");
     RQ_CHECK_ARG(rot_block == 2 || rot_block == 4, "rot_block %d must be 2 or 4", rot_block);
-    RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0,
+    RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0 &&
+                     max_seq_len >= 0,
                  "bad sizes");
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache slots must be 4-byte aligned");
-    if (num_seqs == 0 || max_q_len == 0 || num_blocks == 0) return RQ_OK;
+    if (num_seqs == 0 || max_q_len == 0 || num_blocks == 0 || max_seq_len == 0) return RQ_OK;
+    const int64_t need = rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len);
+    RQ_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace % 16) == 0,
+                 "workspace must be 16-byte aligned and hold %lld bytes (got %lld)", (long long)need,
+                 (long long)workspace_bytes);
     PrefillArgs a{};
     a.q = q;
     a.q_st = q_stride_tok;
@@ -559,13 +583,18 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.score_scale = sm_scale * kLog2eP;
     a.npg = std::max(1, 8 / a.G);
     a.qb = kPQ * a.npg;
+    a.max_tiles = prefill_tiles(max_seq_len);
+    a.ws = static_cast<uint8_t *>(workspace);
     a.out = out;
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
     const int nwaves = a.G * a.npg;
     const int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == RQ_DTYPE_BF16) launch_prefill_bits<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, kb, vb, st);
-    else launch_prefill_bits<RQ_DTYPE_F16>(a, num_seqs, max_q_len, nwaves, kb, vb, st);
-    return check_launch("prefill_kernel");
+    launch_pack_bits(a, num_seqs, kb, vb, st);
+    int rc = check_launch("prefill_pack_kernel");
+    if (rc) return rc;
+    if (dtype == RQ_DTYPE_BF16) launch_attn<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, st);
+    else launch_attn<RQ_DTYPE_F16>(a, num_seqs, max_q_len, nwaves, st);
+    return check_launch("prefill_attn_kernel");
 }

@@ -249,13 +249,14 @@ def paged_decompress(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens
 _ws_cache: dict = {}
 
 
-def _workspace(dev, nbytes: int) -> torch.Tensor:
-    """Decode scratch (split-KV partials, query operands, work list), grown on
-    demand and reused; every call rewrites what it reads."""
-    buf = _ws_cache.get(dev)
+def _workspace(dev, nbytes: int, kind: str = "decode") -> torch.Tensor:
+    """Scratch of one kind per device (decode: split-KV partials, query operands,
+    work list; prefill: int8 tile images), grown on demand and reused; every call
+    rewrites what it reads."""
+    buf = _ws_cache.get((dev, kind))
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        _ws_cache[dev] = buf
+        _ws_cache[(dev, kind)] = buf
     return buf
 
 
@@ -346,7 +347,8 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
                                 rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
                                 sm_scale: float | None = None, out: torch.Tensor | None = None,
                                 cu_seqlens_q: torch.Tensor | None = None,
-                                max_q_len: int | None = None) -> torch.Tensor:
+                                max_q_len: int | None = None, max_seq_len: int | None = None,
+                                workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Causal prefill attention from the packed cache with Q K^T and P V on int8 MFMA.
 
     Reference: src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:247-363.
@@ -354,6 +356,9 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
     (num_seqs,) int32 total context lengths (new tokens included).
     cu_seqlens_q (num_seqs + 1,) int32 splits q among sequences; without it
     there must be one sequence (as in the reference).
+    max_seq_len bounds every seq_lens entry (default: the block table's capacity)
+    and sizes the int8 tile-image workspace; workspace may be passed to reuse a
+    buffer of rq_int8_prefill_workspace_bytes bytes.
     """
     num_tokens, H_Q, D = q.shape
     assert D == head_dim
@@ -385,11 +390,17 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
     R = _f32(rotation, dev)
     kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
     cu = cu_seqlens_q.to(torch.int32).contiguous()
-    rc = _lib.load().rq_int8_prefill(
+    if max_seq_len is None:
+        max_seq_len = bt.shape[1] * block_size
+    L = _lib.load()
+    need = L.rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len)
+    ws = workspace if workspace is not None and workspace.numel() >= need else _workspace(dev, need, "prefill")
+    rc = L.rq_int8_prefill(
         q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
         num_seqs, max_q_len, kv_cache.data_ptr(), kv_cache.shape[0], block_size, kv_cache.stride(0),
         kv_cache.stride(1), num_kv_heads, head_dim, bt.data_ptr(), bt.shape[1], bt.stride(0),
-        seq_lens.contiguous().data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(), blk,
-        float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(dev))
+        seq_lens.contiguous().data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(),
+        R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
+        _lib.stream_ptr(dev))
     _lib.check(rc, "rq_int8_prefill")
     return out

@@ -502,7 +502,8 @@ class RQAttentionImpl(_ImplBase):
                                                 attn_metadata.seq_lens, self._k_quantizer.centroids,
                                                 self._v_quantizer.centroids, self._rq_rot, self.num_kv_heads,
                                                 self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                                out=output[:num_actual_tokens])
+                                                out=output[:num_actual_tokens],
+                                                max_seq_len=getattr(attn_metadata, "max_seq_len", None))
             else:
                 _fused_paged_rq_int8_prefill_fn(query[:num_actual_tokens], kv_cache, attn_metadata.block_table,
                                                 attn_metadata.seq_lens, self._k_quantizer.centroids,
@@ -510,7 +511,8 @@ class RQAttentionImpl(_ImplBase):
                                                 self.head_size, kv_cache.shape[1], sm_scale=self.scale,
                                                 out=output[:num_actual_tokens],
                                                 cu_seqlens_q=attn_metadata.query_start_loc,
-                                                max_q_len=max_query_len)
+                                                max_q_len=max_query_len,
+                                                max_seq_len=getattr(attn_metadata, "max_seq_len", None))
             return output
 
         if getattr(attn_metadata, "use_cascade", False):
