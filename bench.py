@@ -382,6 +382,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
+    ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4"],
+                    help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a kernel of known traffic for counter calibration)")
@@ -393,6 +395,11 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    if args.only:
+        fn = {"compress": time_compress, "prefill3": time_prefill_cfg3, "decode2": lambda: decode_config(2),
+              "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4}[args.only]
+        print(json.dumps({"only": args.only, **fn()}), flush=True)
+        return
     if args.calib_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
