@@ -266,8 +266,8 @@ __device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
 // Per-call preparation; workgroup (seq, y):
 //   * y == 0: the fp16 query operands (and score scales) of every kv head of the
 //     sequence, stored in lane order so each decode lane loads its 64 bytes;
-//   * all: the tile descriptors of the sequence's tiles y, y + gridDim.y, ...,
-//     placed after the tiles of the sequences before it (the tiles of all
+//   * y >= 1: the tile descriptors of the sequence's tokens, four per thread and
+//     step, placed after the tiles of the sequences before it (the tiles of all
 //     sequences, in order, form the work the decode kernel splits evenly);
 //   * tile_prefix[seq] = tiles before the sequence; the last sequence also
 //     stores the total.
@@ -304,9 +304,12 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
         a.tile_prefix[seq] = prefix;
         if (seq == gridDim.x - 1) *a.n_tiles_total = prefix + n;
     }
+    if (y == 0) return;  // the query operands above are this workgroup's share
     const int32_t *bt_row = a.bt + seq * a.bt_ss;
-    // four consecutive tokens per thread and step (block-table loads issued together)
-    for (int j0 = 4 * (y * (int)blockDim.x + (int)threadIdx.x); j0 < n * kTile; j0 += 4 * gridDim.y * blockDim.x) {
+    // four consecutive tokens per thread and step (block-table loads issued together),
+    // on the workgroups y = 1 .. gridDim.y - 1
+    const int ny = gridDim.y - 1;
+    for (int j0 = 4 * ((y - 1) * (int)blockDim.x + (int)threadIdx.x); j0 < n * kTile; j0 += 4 * ny * blockDim.x) {
         int phys[4];
     #pragma unroll
         for (int u = 0; u < 4; ++u) {
