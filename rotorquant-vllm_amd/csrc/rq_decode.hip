@@ -730,7 +730,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     reinterpret_cast<uint32_t *>(dst)[lane] = packed;
 }
 
-// Compute units of the current device (cached per device).
 constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
 
 // Decode workgroups per kv-head group: as many as are resident at once.
