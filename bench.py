@@ -293,6 +293,33 @@ def time_mixed_cfg4(steps=5):
     return out
 
 
+def time_paged_decompress(inp, steps=10):
+    """rq_paged_decompress of config 1's cache (every referenced block expanded to bf16 K and V).
+
+    Bytes: the referenced blocks' payload read (136 * H per slot, whole blocks) plus the
+    16-bit K and V written (2 * H * D * 2 per slot), block table and marks ignored."""
+    import torch
+
+    from rotorquant_vllm import kernels as K
+    p, dev = inp["p"], inp["q"].device
+    kc, vc = p.kc.to(dev), p.vc.to(dev)
+    H, D, BS = inp["H"], inp["D"], inp["BS"]
+    NB = inp["caches"][0].shape[0]
+    out_k = torch.empty(NB, BS, H, D, dtype=torch.bfloat16, device=dev)
+    out_v = torch.empty_like(out_k)
+    from rotorquant_vllm import _lib
+    ws = torch.empty(_lib.load().rq_paged_decompress_workspace_bytes(NB), dtype=torch.uint8, device=dev)
+
+    def fn():
+        K.paged_decompress(inp["caches"][0], inp["bt"], inp["lens"], H, D, kc, vc, torch.bfloat16, out_k=out_k,
+                           out_v=out_v, workspace=ws)
+    ms = time_events(fn, steps)
+    n_blocks = sum((L + BS - 1) // BS for L in inp["lens_host"])  # blocks are distinct in the seeded layout
+    nbytes = n_blocks * BS * (136 * H + 2 * H * D * 2)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(blocks=n_blocks, us=round(ms * 1e3, 1), GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+
+
 def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     """rq_compress_store of n_tokens K+V (fp16) into random slots.
 
@@ -382,7 +409,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
-    ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4"],
+    ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -397,7 +424,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
     if args.only:
         fn = {"compress": time_compress, "prefill3": time_prefill_cfg3, "decode2": lambda: decode_config(2),
-              "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4}[args.only]
+              "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4,
+              "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1))}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -446,6 +474,7 @@ def main():
         result["compress"] = time_compress()
     if not args.no_extra:
         del inp["caches"][1:]
+        result["paged_decompress_config1"] = time_paged_decompress(inp)
         torch.cuda.empty_cache()
         result["prefill_config3"] = time_prefill_cfg3()
         result["decode_config2"] = decode_config(2)
