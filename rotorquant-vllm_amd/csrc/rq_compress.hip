@@ -228,14 +228,16 @@ struct Cursor {
 // blocks up to 4; 8x8 blocks keep their registers.
 constexpr int compress_waves_per_eu(int blk) { return blk <= 4 ? 4 : 1; }
 
-template <int DT, int BLK>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compress_waves_per_eu(BLK)))) void compress_kernel(RowMap m, int64_t n_rows, int D,
+// DC: head_dim fixed at compile time (128: every loop has a constant trip count), 0 = runtime D_in.
+template <int DT, int BLK, int DC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compress_waves_per_eu(BLK)))) void compress_kernel(RowMap m, int64_t n_rows, int D_in,
                                                             const float *__restrict__ rt_even,
                                                             const float *__restrict__ rt_odd,
                                                             const float *__restrict__ kbnd, int nkb,
                                                             const float *__restrict__ vbnd, int nvb) {
     using S = Src<DT>;
     constexpr int EB = S::bytes;
+    const int D = DC > 0 ? DC : D_in;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -577,7 +579,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compre
 }
 
 // Resident workgroups of a compress kernel on the current device (cached).
-template <int DT, int BLK>
+template <int DT, int BLK, int DC>
 static int compress_grid(size_t lds, int64_t n_groups) {
     static int per_cu[64] = {0};
     static size_t for_lds[64] = {0};
@@ -585,7 +587,7 @@ static int compress_grid(size_t lds, int64_t n_groups) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     if (per_cu[dev] == 0 || for_lds[dev] != lds) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&compress_kernel<DT, BLK>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&compress_kernel<DT, BLK, DC>),
                                                          kThreads, lds) != hipSuccess || nb <= 0)
             nb = 4;
         per_cu[dev] = nb;
@@ -595,15 +597,22 @@ static int compress_grid(size_t lds, int64_t n_groups) {
     return (int)(g < n_groups ? g : n_groups);
 }
 
+template <int DT, int BLK, int DC>
+static int launch_compress_dc(const RowMap &m, int64_t n_rows, int D, const float *rte, const float *rto,
+                              const float *kb, int nkb, const float *vb, int nvb, hipStream_t st) {
+    int eb = DT == RQ_DTYPE_F32 ? 4 : 2;
+    size_t lds = (size_t)kOffRows + (size_t)kRows * (D * eb + 16);
+    const int grid = compress_grid<DT, BLK, DC>(lds, (n_rows + kRows - 1) / kRows);
+    hipLaunchKernelGGL((compress_kernel<DT, BLK, DC>), dim3((unsigned)grid), dim3(kThreads), lds, st, m, n_rows, D, rte,
+                       rto, kb, nkb, vb, nvb);
+    return check_launch("compress_kernel");
+}
+
 template <int DT, int BLK>
 static int launch_compress_blk(const RowMap &m, int64_t n_rows, int D, const float *rte, const float *rto,
                                const float *kb, int nkb, const float *vb, int nvb, hipStream_t st) {
-    int eb = DT == RQ_DTYPE_F32 ? 4 : 2;
-    size_t lds = (size_t)kOffRows + (size_t)kRows * (D * eb + 16);
-    const int grid = compress_grid<DT, BLK>(lds, (n_rows + kRows - 1) / kRows);
-    hipLaunchKernelGGL((compress_kernel<DT, BLK>), dim3((unsigned)grid), dim3(kThreads), lds, st, m, n_rows, D, rte,
-                       rto, kb, nkb, vb, nvb);
-    return check_launch("compress_kernel");
+    if (D == 128) return launch_compress_dc<DT, BLK, 128>(m, n_rows, D, rte, rto, kb, nkb, vb, nvb, st);
+    return launch_compress_dc<DT, BLK, 0>(m, n_rows, D, rte, rto, kb, nkb, vb, nvb, st);
 }
 
 template <int DT>
