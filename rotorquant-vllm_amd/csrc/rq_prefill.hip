@@ -71,18 +71,21 @@ __device__ __forceinline__ uint32_t lookup_i8(const Table8 &t, uint32_t sel) {
     }
 }
 
-// Integral x in [-128, 127] converted into byte `byte` of w (other bytes kept),
-// one v_cvt_i32_f32 with an SDWA byte destination.
-template <int UNUSED>
+// x in (-129, 128) truncated toward zero into byte `byte` of w (other bytes kept):
+// one v_cvt_i32_f32 with an SDWA byte destination.  x must come from a VALU
+// instruction (inline assembly gets no MFMA -> VALU wait states).
 __device__ __forceinline__ uint32_t cvt_i8_into(float x, uint32_t w, int byte) {
+#define RQ_CVT_BYTE(B) asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_" #B " dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x))
     switch (byte) {
-        case 0: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
-        case 1: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
-        case 2: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
-        default: asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x)); break;
+        case 0: RQ_CVT_BYTE(0); break;
+        case 1: RQ_CVT_BYTE(1); break;
+        case 2: RQ_CVT_BYTE(2); break;
+        default: RQ_CVT_BYTE(3); break;
     }
+#undef RQ_CVT_BYTE
     return w;
 }
+
 
 __device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
 
@@ -431,8 +434,9 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             m_run = m_new;
         }
         // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
-        // p <= 1 and v_norm <= 127 s_w, so hi = rint(w) is in [0, 127] and lo = rint((w - hi) * 128)
-        // in [-64, 64]: no clamping; each converts straight into its byte of the operand.
+        // With x = w + 1/256: hi = floor(x) in [0, 127] (p <= 1, v_norm <= 127 s_w) and
+        // lo = floor(fract(x) * 128) in [0, 127], so hi + lo / 128 = round(128 w) / 128 (nearest).
+        // No clamping; both truncating converts write straight into their byte of the operand.
         const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
         uint32_t wh[4], wl[4];
 #pragma unroll
@@ -444,11 +448,9 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], sq, -msq));
                 l_run += p;
-                const float x = p * cwv[i];
-                const float xh = __builtin_rintf(x);
-                const float xl = __builtin_rintf((x - xh) * 128.f);
-                hw = cvt_i8_into<0>(xh, hw, i);
-                lw = cvt_i8_into<0>(xl, lw, i);
+                const float x = __builtin_fmaf(p, cwv[i], 1.f / 256.f);
+                hw = cvt_i8_into(x, hw, i);
+                lw = cvt_i8_into(__builtin_amdgcn_fractf(x) * 128.f, lw, i);
             }
             wh[b] = hw;
             wl[b] = lw;
