@@ -5,8 +5,9 @@
  * Every entry point takes plain device pointers, element or byte strides,
  * small integer enums and a hipStream_t passed as `void *`.  None of them
  * allocates device memory, synchronises the host or keeps state between calls:
- * scratch space (split-KV partials, block marks) is passed in by the caller, so
- * the calls can be captured in a HIP graph.  All launches go to `stream`.
+ * scratch space (split-KV partials, prefill tile images, block marks) is passed
+ * in by the caller, so the calls can be captured in a HIP graph.  All launches
+ * go to `stream`.
  *
  * Return value: RQ_OK (0) on success; a nonzero rq_status otherwise.  The text
  * of the last error of the calling thread is available from rq_last_error().
@@ -33,7 +34,7 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 1
+#define RQ_ABI_VERSION 2  /* 2: rq_int8_prefill takes max_seq_len and a workspace */
 
 enum rq_status {
     RQ_OK = 0,
