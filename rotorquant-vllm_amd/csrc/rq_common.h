@@ -51,6 +51,7 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_
 // at LDS address m0 + l * size (m0 = wave-uniform destination).
 //   copy16:  16 bytes from the uniform base `src` + per-lane 32-bit offset.
 //   copy16v: 16 bytes from a per-lane address.
+//   copy4s:  4 bytes from the uniform base `src` + per-lane 32-bit offset.
 //   copy4:   4 bytes from a per-lane address.
 __device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32_t dst) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "s"(dst)
@@ -58,6 +59,10 @@ __device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32
 }
 __device__ __forceinline__ void copy16v(const uint8_t *src, uint32_t dst) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+__device__ __forceinline__ void copy4s(const uint8_t *src, uint32_t voff, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(src), "s"(dst)
+                 : "memory", "m0");
 }
 __device__ __forceinline__ void copy4(const uint8_t *src, uint32_t dst) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(dst) : "memory", "m0");

@@ -119,7 +119,7 @@ struct DecodeArgs {
     TileDesc *descs;    // [total tiles] (prep kernel)
     int *tile_prefix;   // [seq] tiles before the sequence
     int *n_tiles_total;
-    uint32_t *qops;     // [seq][H][64 lanes][16] fp16 query operands
+    uint32_t *qops;     // [seq][H][16 cols][4 g][4 chunks][4 dwords]: fp16 query operands (cols < G written)
     float *qscale;      // [seq][H][16] score scales
     float *part_acc;    // [slot][HQ][D], slot = workgroup + seq
     float *part_ml;     // [slot][HQ][2]
@@ -154,6 +154,17 @@ __device__ __forceinline__ float rows_sum(float x) {
     x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+// The lane index, recomputed where it is used (two VALU ops, no input register).
+// Lane-derived values needed only at segment boundaries or by the copy issue are
+// built from it: the register allocator otherwise keeps them live across the tile
+// loop and, under pressure, spills them, and a spill reload inside the loop is a
+// vector-memory load whose wait also waits for every copy in flight.
+__device__ __forceinline__ uint32_t lane_now() {
+    uint32_t x;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(x));
+    return x;
 }
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
@@ -265,7 +276,8 @@ __device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
 
 // Per-call preparation; workgroup (seq, y):
 //   * y == 0: the fp16 query operands (and score scales) of every kv head of the
-//     sequence, stored in lane order so each decode lane loads its 64 bytes;
+//     sequence, stored per query-head column (256 bytes each, in the order the
+//     decode lanes (g, col) read them) so one copy moves a kv head's G columns;
 //   * y >= 1: the tile descriptors of the sequence's tokens, four per thread and
 //     step, placed after the tiles of the sequences before it (the tiles of all
 //     sequences, in order, form the work the decode kernel splits evenly);
@@ -285,9 +297,12 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
             u32x4 qop[4];
             float sc;
             query_operand<DT>(a, seq, h, wq_all[wave], qop, sc);
-            uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 64 + lane) * 16);
+            const int g = lane >> 4, col = lane & 15;
+            uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 16 + col) * 64 + g * 16);
+            if (col < a.G) {
     #pragma unroll
-            for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
+                for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
+            }
             if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
         }
     }
@@ -382,6 +397,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     uint8_t *const stage0 = lds;
     uint8_t *const stage1 = lds + stage_bytes;
     const TileDesc *const ring = reinterpret_cast<const TileDesc *>(lds + 2 * stage_bytes);
+    // Query operand slot: per wave, its kv head's G columns (256 bytes each), then
+    // the score scales of the hpw kv heads (16 floats each).
+    const int G = a.G;
+    uint8_t *const qarea = lds + 2 * stage_bytes + kRing * sizeof(TileDesc);
+    const float *const scarea = reinterpret_cast<const float *>(qarea + hpw * G * 256);
 
     // Descriptor of local tile i -> ring slot i % kRing (wave 0, one copy).
     auto issue_desc = [&](int i) {
@@ -393,7 +413,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     auto issue = [&](int i, const uint8_t *sb) {
         const TileDesc &d = ring[i % kRing];
         const int valid = __builtin_amdgcn_readfirstlane(d.valid);
-        const uint64_t base = d.off[tl];
+        const uint64_t base = d.off[lane_now() & 31];
         const uint32_t dst = lds_addr(sb);
         const uint32_t kv_src = lane < 4 * hpw ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * lane)
                                                : (uint32_t)(SL.v_idx + 64 * h0 + 16 * (lane - 4 * hpw));
@@ -412,8 +432,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             if (wave < kTile / TPI) {
                 const int qs = lane / NP, p = lane % NP;
                 const int tt = wave * TPI + 4 * (qs % (TPI / 4)) + qs / (TPI / 4);
-                const uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
-                                                : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
+                uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
+                                          : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
+                // recomputed per tile: a loop-invariant 64-bit per-lane address here was
+                // spilled, and its reload waited for every copy in flight
+                asm volatile("" : "+v"(src));
                 if (tt < valid) copy16v(a.cache + d.off[tt] + src, dst + norm_off + 1024 * wave);
             }
         } else {
@@ -425,6 +448,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         }
     };
 
+    // Query operand and score scales of sequence s -> the query slot (each wave its
+    // own kv head): ceil(G / 4) 16-byte copies and one 4-byte copy per wave.
+    auto issue_q = [&](int s) {
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(a.qops) + ((int64_t)s * a.H + h) * 16 * 256;
+        const uint32_t dst = lds_addr(qarea + wave * G * 256);
+        const uint32_t l16 = 16u * lane_now();
+        for (int j = 0; j < G * 256; j += 1024)
+            if (j + l16 < (uint32_t)(G * 256)) copy16(src, j + l16, dst + j);
+        if (l16 < 256)
+            copy4s(reinterpret_cast<const uint8_t *>(a.qscale + ((int64_t)s * a.H + h) * 16), l16 >> 2,
+                   lds_addr(reinterpret_cast<const uint8_t *>(scarea + wave * 16)));
+    };
+
     for (int i = 0; i < min(nt, kRing); ++i) issue_desc(i);
     wait_copies<0>();
     __syncthreads();
@@ -432,54 +468,60 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
     const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
 
-    // Per-segment state.  The query operand and score scale are compiler-visible
-    // loads, issued at a segment start before further copies (the compiler does
-    // not count the copies, so its wait for these loads also waits for them).
-    int seq = __builtin_amdgcn_readfirstlane(ring[0].seq);
+    // Per-segment state.  No compiler-visible global load is issued inside the tile
+    // loop: the compiler does not count the copies, so a wait it inserted for a load
+    // of its own would wait for every copy in flight and stall the pipeline.  The
+    // query operand therefore arrives by copy, in the same stream as the tiles.
+    int seq = -1;
     u32x4 qop[4];
     float sc;
     f32x4 acc[8];
     float m_run, l_run;
     int e_run;
     auto begin_segment = [&]() {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.qops + (((int64_t)seq * a.H + h) * 64 + lane) * 16);
+        const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + col * 256 + g * 64);
     #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const uint4 v = src[c];
+            const uint4 v = col < G ? src[c] : make_uint4(0, 0, 0, 0);
             qop[c] = u32x4{v.x, v.y, v.z, v.w};
         }
-        sc = a.qscale[((int64_t)seq * a.H + h) * 16 + col];
+        sc = col < G ? scarea[wave * 16 + col] : 0.f;
     #pragma unroll
         for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;  // running max (log2 domain) for query head `col`
         l_run = 0.f;        // this lane's partial sum of p
         e_run = -126;       // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
     };
-    // Partial of the current segment -> slot w + seq.
+    // Partial of the current segment -> slot w + seq.  Addresses are a uniform
+    // 64-bit base plus a 32-bit lane offset computed here (a hoisted 64-bit per-lane
+    // address would be spilled, and its reload would wait for the copies in flight).
     auto end_segment = [&]() {
         const float lsum = rows_sum(l_run);
         if (col < a.G) {
-            const int hq = h * a.G + col;
-            const int64_t pidx = (int64_t)(w + seq) * a.HQ + hq;
-            float *pa = a.part_acc + pidx * kD;
+            const int64_t slot = (int64_t)(w + seq) * a.HQ + h * a.G;  // uniform: query head h*G of the slot
+            uint8_t *pa = reinterpret_cast<uint8_t *>(a.part_acc + slot * kD);
+            uint8_t *pm = reinterpret_cast<uint8_t *>(a.part_ml + slot * 2);
+            const uint32_t ln = lane_now();
+            const uint32_t lo_off = ((ln & 15) * kD + 32 * (ln >> 4)) * 4;
             // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
             const float es = ldexpf(1.f, e_run);
     #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
                 float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
-                float4 *dst = reinterpret_cast<float4 *>(pa + 8 * (4 * g + i));
+                float4 *dst = reinterpret_cast<float4 *>(pa + lo_off + 32 * i);
                 dst[0] = lo;
                 dst[1] = hi;
             }
-            if (g == 0) {
-                a.part_ml[pidx * 2] = m_run;
-                a.part_ml[pidx * 2 + 1] = lsum;
-            }
+            if (g == 0) *reinterpret_cast<float2 *>(pm + 8u * (lane_now() & 15)) = make_float2(m_run, lsum);
         }
     };
-    begin_segment();
-
+    // The query slot holds the operand of the segment starting at local tile q_upto;
+    // the next one is copied once that segment has begun (its operand is then in
+    // registers), before the tile copies of the same iteration, so the wait for the
+    // tile that starts the new segment also covers it.
+    int q_upto = 0;
+    issue_q(__builtin_amdgcn_readfirstlane(ring[0].seq));
     issue(0, stage0);
     if (nt > 1) issue(1, stage1);
 
@@ -504,7 +546,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         const int tseq = __builtin_amdgcn_readfirstlane(ring[t % kRing].seq);
         const int valid = __builtin_amdgcn_readfirstlane(ring[t % kRing].valid);
         if (tseq != seq) {  // a new sequence starts at this tile
-            end_segment();
+            if (seq >= 0) end_segment();
             seq = tseq;
             begin_segment();
         }
@@ -541,7 +583,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         }
         __syncthreads();  // the stage and descriptor slot t are free once every wave holds its operands
 
-        // ---- descriptor t+4 and tile t+2 ---------------------------------------------
+        // ---- next query operand, descriptor t+4 and tile t+2 -------------------------
+        if (q_upto <= t && t + 1 < nt) {
+            const int s1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].seq);
+            if (s1 != seq) {
+                issue_q(s1);
+                q_upto = t + 1;
+            } else if (t + 2 < nt) {
+                const int s2 = __builtin_amdgcn_readfirstlane(ring[(t + 2) % kRing].seq);
+                if (s2 != s1) {
+                    issue_q(s2);
+                    q_upto = t + 2;
+                }
+            }
+        }
         if (t + kRing < nt) issue_desc(t + kRing);
         if (t + 2 < nt) issue(t + 2, sb);
 
@@ -878,7 +933,7 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.o_ss = out_stride_seq;
     a.o_sh = out_stride_head;
     a.grid_w = 1;
-    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc);
+    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * (a.G * 256 + 64);
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
         const dim3 pgrid((unsigned)num_seqs, 4), pblock(64 * std::min(a.H, kMaxWaves));
