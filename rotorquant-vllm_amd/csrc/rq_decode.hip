@@ -57,13 +57,21 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                       0, 0, 0);
 }
 
-// Centroids (fp32, 16-byte aligned, n = 8 or 16) -> 16-bit table split in low /
-// high bytes.  The loads are uniform vector loads issued together.
-template <int DT>
-__device__ __forceinline__ Table16 make_table(const float *c, int n) {
+// Centroids (fp32, 16-byte aligned, n = 8 or 16): uniform vector loads issued
+// together (entries past n read as zero).
+struct Centroids {
+    float4 v4[4];
+};
+__device__ __forceinline__ Centroids load_centroids(const float *c, int n) {
     const float4 *c4 = reinterpret_cast<const float4 *>(c);
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 v4[4] = {c4[0], c4[1], n > 8 ? c4[2] : z, n > 8 ? c4[3] : z};
+    return Centroids{{c4[0], c4[1], n > 8 ? c4[2] : z, n > 8 ? c4[3] : z}};
+}
+
+// Centroids -> 16-bit table split in low / high bytes.
+template <int DT>
+__device__ __forceinline__ Table16 make_table(const Centroids &cv) {
+    const float4 *v4 = cv.v4;
     Table16 t;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -257,6 +265,17 @@ __device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, 
         qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
     }
     __builtin_amdgcn_wave_barrier();
+}
+
+// s_waitcnt vmcnt(min(n, MAXN)) for a wave-uniform n.
+template <int MAXN>
+__device__ __forceinline__ void wait_copies_n(int n) {
+    if constexpr (MAXN > 0) {
+        if (n >= MAXN) wait_copies<MAXN>();
+        else wait_copies_n<MAXN - 1>(n);
+    } else {
+        wait_copies<0>();
+    }
 }
 
 // Tile descriptor: one 32-token tile of one sequence, written by the prep kernel
@@ -461,12 +480,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                    lds_addr(reinterpret_cast<const uint8_t *>(scarea + wave * 16)));
     };
 
+    // The centroid loads are compiler-visible: issued before the descriptor copies
+    // and covered by their wait, so no wait of the compiler's for them lands after
+    // the first tile copies (it would wait for those too).
+    const Centroids ck = load_centroids(a.kc, a.nkc), cv = load_centroids(a.vc, a.nvc);
     for (int i = 0; i < min(nt, kRing); ++i) issue_desc(i);
     wait_copies<0>();
     __syncthreads();
 
-    const Table16 tk = make_table<RQ_DTYPE_F16>(a.kc, a.nkc);
-    const Table16 tv = make_table<RQ_DTYPE_F16>(a.vc, a.nvc);
+    const Table16 tk = make_table<RQ_DTYPE_F16>(ck);
+    const Table16 tv = make_table<RQ_DTYPE_F16>(cv);
 
     // Per-segment state.  No compiler-visible global load is issued inside the tile
     // loop: the compiler does not count the copies, so a wait it inserted for a load
@@ -485,12 +508,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             const uint4 v = col < G ? src[c] : make_uint4(0, 0, 0, 0);
             qop[c] = u32x4{v.x, v.y, v.z, v.w};
         }
-        sc = col < G ? scarea[wave * 16 + col] : 0.f;
+        sc = col < G ? scarea[wave * 16 + col] : 1.f;  // columns >= G: zero queries, any positive scale
     #pragma unroll
         for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;  // running max (log2 domain) for query head `col`
         l_run = 0.f;        // this lane's partial sum of p
-        e_run = -126;       // P operand = p * v_norm * 2^-e_run <= 1 (fp16); acc carries the same scale
+        e_run = -126;       // P operand = p * v_norm * 2^-e_run <= 2^8 (fp16); acc carries the same scale
     };
     // Partial of the current segment -> slot w + seq.  Addresses are a uniform
     // 64-bit base plus a 32-bit lane offset computed here (a hoisted 64-bit per-lane
@@ -527,17 +550,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
 
     for (int t = 0; t < nt; ++t) {
         const uint8_t *const sb = (t & 1) ? stage1 : stage0;
-        // Tile t landed?  Issued after its copies: descriptor t+3 (wave 0, from
-        // iteration t-1; the prologue issues descriptors 0..3 before tile 0) and tile
-        // t+1, which may stay in flight when it is full.
-        if (HPW > 0 && t + 1 < nt && __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid) == kTile) {
-            // per wave and full tile: kTile / HPW token copies, plus one norm copy on
-            // the first kTile / (128 / HPW) waves
-            constexpr int NC = kTile / (HPW > 0 ? HPW : 1);
-            const int extra = (wave < kTile * (HPW > 0 ? HPW : 1) / 128 ? 1 : 0) + (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
-            if (extra == 2) wait_copies<NC + 2>();
-            else if (extra == 1) wait_copies<NC + 1>();
-            else wait_copies<NC>();
+        // Tile t landed?  Issued after its copies, and allowed to stay in flight:
+        // this wave's copies of tile t+1 (iteration t-1) and descriptor t+3 (wave 0,
+        // iteration t-1; the prologue issues descriptors 0..3 before tile 0).  The
+        // query operand copies of an iteration precede both.
+        if (HPW > 0 && t + 1 < nt) {
+            constexpr int HP = HPW > 0 ? HPW : 8, TPI = 128 / HP;
+            const int v1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid);
+            // token copies tt = wave, wave + HPW, ... < v1; a norm copy on the waves
+            // whose token range [wave * TPI, +TPI) starts below v1
+            const int n = (v1 > wave ? (v1 - wave + HP - 1) / HP : 0) + (wave < kTile / TPI && wave * TPI < v1 ? 1 : 0) +
+                          (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
+            wait_copies_n<kTile / HP + 2>(n);
         } else {
             wait_copies<0>();
         }
@@ -638,10 +662,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             }
         }
         // ---- scale by K norm, mask, online softmax ---------------------------
+        // s = score / sc; the score scale sc > 0 enters the exponent's fma (and the
+        // max, which it commutes with).
         float s[8] = {s0.x * nk[0], s0.y * nk[1], s0.z * nk[2], s0.w * nk[3],
                       s1.x * nk[4], s1.y * nk[5], s1.z * nk[6], s1.w * nk[7]};
-    #pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] *= sc;
         if (valid < kTile) {
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -650,8 +674,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             }
         }
         float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-        tmax = rows_max(tmax);
-        if (__any(tmax > m_run)) {
+        tmax = rows_max(tmax) * sc;
+        // Lazy running max: rescale only when a column's max exceeds m_run by more
+        // than 8 (log2 units).  In between, p = 2^(score - m_run) <= 2^8, so the
+        // fp16 P operand (p * v_norm * 2^-e_run <= 2^8) stays in range; acc and l_run
+        // are relative to the same m_run, so the result does not depend on when the
+        // rescale happens.
+        if (__any(tmax > m_run + 8.f)) {
             const float m_new = fmaxf(m_run, tmax);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
     #pragma unroll
@@ -663,7 +692,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         float p[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sc, -m_run));
             l_run += p[i];
             nv[i] *= pf;
         }
