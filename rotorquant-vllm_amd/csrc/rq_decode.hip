@@ -124,9 +124,13 @@ struct DecodeArgs {
     int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
     int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
     int grid_w;         // decode workgroups per kv-head group (the tile ranges)
+    int split_c;        // workgroups w < split_c weigh wt0 parts of the tiles, the others wt1
+    int wt0, wt1;
+    uint64_t split_r;   // floor((2^64 - 1) / (split_c wt0 + (grid_w - split_c) wt1))
     TileDesc *descs;    // [total tiles] (prep kernel)
-    int *tile_prefix;   // [seq] tiles before the sequence
+    int *tile_prefix;   // [seq][2]: first workgroup whose range covers the sequence, number of such workgroups
     int *n_tiles_total;
+    uint64_t *split_m;  // M of the range split (prep kernel)
     uint32_t *qops;     // [seq][H][16 cols][4 g][4 chunks][4 dwords]: fp16 query operands (cols < G written)
     float *qscale;      // [seq][H][16] score scales
     float *part_acc;    // [slot][HQ][D], slot = workgroup + seq
@@ -288,6 +292,32 @@ static_assert(sizeof(TileDesc) == 16 + 8 * kTile, "TileDesc layout");
 constexpr int kDescPieces = (int)sizeof(TileDesc) / 16;  // 16-byte copy pieces per descriptor
 constexpr int kRing = 4;                                   // descriptors staged ahead in LDS
 
+// First tile of workgroup w's range, w in [0, grid_w]: the tiles of all
+// sequences are split into contiguous ranges by weight.  With two workgroups per
+// CU, the first one dispatched onto each CU (w < split_c) is favoured by the wave
+// arbiter and runs ~1.4x as fast as its neighbour (measured); weighting its range
+// accordingly lets both end together instead of one CU slot idling for the tail.
+// The split is s(w) * M >> 32 with M ~ NT 2^32 / s(grid_w) (M = the high half of
+// (NT << 32) * split_r, at most the exact quotient), computed once by the prep
+// kernel; the decode and the merge kernel evaluate exactly this, and the last
+// range ends at NT.
+struct RangeSplit {
+    int c, wt0, wt1, G, NT;
+    uint64_t M;
+};
+__device__ __forceinline__ uint64_t split_multiplier(const DecodeArgs &a, int NT) {
+    return __umul64hi((uint64_t)NT << 32, a.split_r);
+}
+__device__ __forceinline__ RangeSplit make_split(const DecodeArgs &a, int NT) {
+    return RangeSplit{a.split_c, a.wt0, a.wt1, a.grid_w, NT, *a.split_m};
+}
+__device__ __forceinline__ int range_start(const RangeSplit &r, int w) {
+    if (w >= r.G) return r.NT;
+    const uint64_t s = w <= r.c ? (uint64_t)w * r.wt0 : (uint64_t)r.c * r.wt0 + (uint64_t)(w - r.c) * r.wt1;
+    return (int)((s * r.M) >> 32);
+}
+
+
 __device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
     const int L = min(a.seq_lens[b], a.max_len);
     return L > 0 ? (L + kTile - 1) / kTile : 0;
@@ -299,9 +329,10 @@ __device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
 //     decode lanes (g, col) read them) so one copy moves a kv head's G columns;
 //   * y >= 1: the tile descriptors of the sequence's tokens, four per thread and
 //     step, placed after the tiles of the sequences before it (the tiles of all
-//     sequences, in order, form the work the decode kernel splits evenly);
-//   * tile_prefix[seq] = tiles before the sequence; the last sequence also
-//     stores the total.
+//     sequences, in order, form the work the decode kernel splits by range);
+//   * tile_prefix[seq] = the first decode workgroup whose range covers the
+//     sequence and the number of such workgroups (for the merge); the last
+//     sequence also stores the total tile count and the range-split multiplier.
 template <int DT>
 __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.x;
@@ -310,7 +341,7 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
     __shared__ __align__(16) uint16_t wq_all[kMaxWaves][16 * kD];
-    __shared__ int part[kMaxWaves];
+    __shared__ int part[2 * kMaxWaves];
     if (y == 0) {
         for (int h = wave; h < a.H; h += nw) {
             u32x4 qop[4];
@@ -325,18 +356,52 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
             if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
         }
     }
-    int cnt = 0;
-    for (int64_t b = threadIdx.x; b < seq; b += blockDim.x) cnt += seq_tiles(a, b);
-    for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o);
-    if (lane == 0) part[wave] = cnt;
+    // tiles before this sequence (prefix) and in all sequences (NT)
+    int cnt = 0, tot = 0;
+    for (int64_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+        const int nb = seq_tiles(a, b);
+        cnt += b < seq ? nb : 0;
+        tot += nb;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        cnt += __shfl_xor(cnt, o);
+        tot += __shfl_xor(tot, o);
+    }
+    if (lane == 0) {
+        part[wave] = cnt;
+        part[kMaxWaves + wave] = tot;
+    }
     __syncthreads();
-    int prefix = 0;
-    for (int w = 0; w < nw; ++w) prefix += part[w];
+    int prefix = 0, NT = 0;
+    for (int w = 0; w < nw; ++w) {
+        prefix += part[w];
+        NT += part[kMaxWaves + w];
+    }
     const int n = seq_tiles(a, seq);
     const int L = min(a.seq_lens[seq], a.max_len);
-    if (y == 0 && threadIdx.x == 0) {
-        a.tile_prefix[seq] = prefix;
-        if (seq == gridDim.x - 1) *a.n_tiles_total = prefix + n;
+    if (y == 0 && wave == 0) {
+        // The decode workgroups whose ranges cover this sequence (for the merge):
+        // the owner of tile t is the number of w in [1, G) with range_start(w) <= t
+        // (range_start is non-decreasing and range_start(0) = 0).
+        const RangeSplit r{a.split_c, a.wt0, a.wt1, a.grid_w, NT, split_multiplier(a, NT)};
+        int c_lo = 0, c_hi = 0;
+        for (int w = 1 + lane; w < r.G; w += 64) {
+            const int rs = range_start(r, w);
+            c_lo += rs <= prefix ? 1 : 0;
+            c_hi += rs <= prefix + n - 1 ? 1 : 0;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            c_lo += __shfl_xor(c_lo, o);
+            c_hi += __shfl_xor(c_hi, o);
+        }
+        if (lane == 0) {
+            a.tile_prefix[2 * seq] = n > 0 ? c_lo : 0;
+            a.tile_prefix[2 * seq + 1] = n > 0 ? c_hi - c_lo + 1 : 0;
+            if (seq == gridDim.x - 1) {
+                *a.n_tiles_total = NT;
+                *a.split_m = r.M;
+            }
+        }
     }
     if (y == 0) return;  // the query operands above are this workgroup's share
     const int32_t *bt_row = a.bt + seq * a.bt_ss;
@@ -394,8 +459,9 @@ template <int DT, int KB, int VB, int HPW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
     const int w = blockIdx.x;
     const int NT = *a.n_tiles_total;
-    const int k0 = (int)((int64_t)w * NT / gridDim.x);
-    const int nt = (int)((int64_t)(w + 1) * NT / gridDim.x) - k0;
+    const RangeSplit rsp = make_split(a, NT);
+    const int k0 = range_start(rsp, w);
+    const int nt = range_start(rsp, w + 1) - k0;
     if (nt <= 0) return;
 
     // HPW > 0: heads per workgroup fixed at compile time (LDS offsets become immediates)
@@ -747,21 +813,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     #pragma unroll
         for (int i = 0; i < 4; ++i) rr[e][i] = i < a.rot_block ? a.R[(k0 + i) * kD + d] : 0.f;
     }
-    // Workgroups whose tile ranges cover the sequence: workgroup w owns tiles
-    // [w NT / G, (w+1) NT / G), so tile t belongs to w(t) = ((t + 1) G - 1) / NT.
-    // Partials sit at slots w + seq for w in [w(first tile), w(last tile)];
-    // workgroups with an empty range (more workgroups than tiles) wrote nothing.
+    // Workgroups whose tile ranges cover the sequence (found by the prep kernel):
+    // partials sit at slots w + seq for w in [w_lo, w_lo + nch); workgroups with an
+    // empty range (more workgroups than tiles) wrote nothing.
+    // (the prep kernel does not run when no sequence has tokens: then nch = 0)
     const int n = seq_tiles(a, seq);
-    int nch = 0, w_lo = 0;
-    int64_t NT = 1, G = 1;
-    if (n > 0) {
-        NT = *a.n_tiles_total;
-        G = a.grid_w;
-        const int64_t P = a.tile_prefix[seq];
-        w_lo = (int)(((P + 1) * G - 1) / NT);
-        nch = (int)(((P + n) * G - 1) / NT) - w_lo + 1;
-    }
-    auto has_tiles = [&](int64_t w) { return (w + 1) * NT / G > w * NT / G; };
+    const int w_lo = n > 0 ? a.tile_prefix[2 * seq] : 0, nch = n > 0 ? a.tile_prefix[2 * seq + 1] : 0;
+    const RangeSplit rsp = make_split(a, *a.n_tiles_total);
+    auto has_tiles = [&](int w) { return range_start(rsp, w + 1) > range_start(rsp, w); };
     const float *ml = a.part_ml + (w_lo + seq) * (int64_t)a.HQ * 2 + hq * 2;
     const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
@@ -816,44 +875,66 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
 
-// Decode workgroups per kv-head group: as many as are resident at once.
+// Resident decode workgroups per CU for an LDS size (cached per device and size).
 template <int DT, int KB, int VB, int HPW>
-static int decode_grid(const DecodeArgs &a, size_t lds) {
-    static int per_cu[64] = {0};
+static int decode_per_cu(const DecodeArgs &a, size_t lds) {
+    static int cache[64][8][2] = {};  // [device][entry] = {lds, workgroups per CU}
     int dev = 0;
     (void)hipGetDevice(&dev);
     dev = dev < 0 || dev >= 64 ? 0 : dev;
-    if (per_cu[dev] == 0) {
-        int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW>),
-                                                          64 * a.hpw, lds) != hipSuccess || nb <= 0)
-            nb = 1;
-        per_cu[dev] = std::min(nb, kMaxWgPerCu);
-    }
-    const int groups = a.H / a.hpw;
-    return std::max(1, per_cu[dev] * device_cus() / groups);
+    for (auto &e : cache[dev])
+        if (e[0] == (int)lds && e[1] > 0) return e[1];
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW>),
+                                                      64 * a.hpw, lds) != hipSuccess || nb <= 0)
+        nb = 1;
+    nb = std::min(nb, kMaxWgPerCu);
+    for (auto &e : cache[dev])
+        if (e[1] == 0) {
+            e[0] = (int)lds;
+            e[1] = nb;
+            break;
+        }
+    return nb;
 }
 
+// configure: set the grid and range split only (before the prep kernel, which
+// needs them); otherwise launch.
 template <int DT, int KB, int VB, int HPW>
-static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st) {
-    a.grid_w = decode_grid<DT, KB, VB, HPW>(a, lds);
-    hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw), lds,
-                       st, a);
+static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
+    if (!configure) {
+        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw),
+                           lds, st, a);
+        return;
+    }
+    // as many workgroups per kv-head group as are resident at once
+    const int per_cu = decode_per_cu<DT, KB, VB, HPW>(a, lds);
+    const int groups = a.H / a.hpw;
+    a.grid_w = std::max(1, per_cu * device_cus() / groups);
+    if (groups == 1 && per_cu == 2) {
+        a.split_c = a.grid_w / 2;  // workgroups [0, CUs) are dispatched first, one per CU
+        a.wt0 = 58;
+        a.wt1 = 42;
+    } else {
+        a.split_c = a.grid_w;
+        a.wt0 = a.wt1 = 1;
+    }
+    a.split_r = UINT64_MAX / ((uint64_t)a.split_c * a.wt0 + (uint64_t)(a.grid_w - a.split_c) * a.wt1);
 }
 
 template <int DT, int KB, int VB>
-static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st) {
-    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, lds, st);
-    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, lds, st);
-    else launch_decode_h<DT, KB, VB, 0>(a, lds, st);
+static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, lds, st, configure);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, lds, st, configure);
+    else launch_decode_h<DT, KB, VB, 0>(a, lds, st, configure);
 }
 
 template <int DT>
-static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, hipStream_t st) {
-    if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st);
-    else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st);
-    else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st);
-    else launch_decode<DT, 4, 4>(a, lds, st);
+static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, hipStream_t st, bool configure) {
+    if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st, configure);
+    else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st, configure);
+    else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st, configure);
+    else launch_decode<DT, 4, 4>(a, lds, st, configure);
 }
 
 // Workspace layout (256-byte aligned regions).
@@ -869,8 +950,8 @@ struct DecodeWorkspace {
         qscale = al(qops + num_seqs * num_q_heads * 64 * 16 * 4);  // kv heads <= query heads
         descs = al(qscale + num_seqs * num_q_heads * 16 * 4);
         tile_prefix = al(descs + max_tiles * (int64_t)sizeof(TileDesc));
-        n_tiles = al(tile_prefix + num_seqs * 4);
-        total = al(n_tiles + 4);
+        n_tiles = al(tile_prefix + num_seqs * 8);  // NT (int) at +0, range-split multiplier (uint64) at +8
+        total = al(n_tiles + 16);
     }
 };
 
@@ -946,6 +1027,7 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
         a.descs = reinterpret_cast<TileDesc *>(base + W.descs);
         a.tile_prefix = reinterpret_cast<int *>(base + W.tile_prefix);
         a.n_tiles_total = reinterpret_cast<int *>(base + W.n_tiles);
+        a.split_m = reinterpret_cast<uint64_t *>(base + W.n_tiles + 8);
     }
     a.num_blocks = num_blocks;
     a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
@@ -962,16 +1044,21 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.o_ss = out_stride_seq;
     a.o_sh = out_stride_head;
     a.grid_w = 1;
+    a.split_c = 1;
+    a.wt0 = a.wt1 = 1;
+    a.split_r = UINT64_MAX;
     const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * (a.G * 256 + 64);
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, true);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st, true);
         const dim3 pgrid((unsigned)num_seqs, 4), pblock(64 * std::min(a.H, kMaxWaves));
         if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, 0, st, a);
         else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, 0, st, a);
         int rc = check_launch("decode_prep_kernel");
         if (rc) return rc;
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, false);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st, false);
         rc = check_launch("decode_kernel");
         if (rc) return rc;
     }
