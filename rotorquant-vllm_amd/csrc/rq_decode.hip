@@ -516,13 +516,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             // banks) and tokens i, i+1, ... 256 bytes apart.
             constexpr int NP = HPW / 2, TPI = 64 / NP;
             if (wave < kTile / TPI) {
-                const int qs = lane / NP, p = lane % NP;
+                const uint32_t l = lane_now();  // lane-derived values rebuilt here, not kept live
+                const int qs = l / NP, p = l % NP;
                 const int tt = wave * TPI + 4 * (qs % (TPI / 4)) + qs / (TPI / 4);
-                uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
-                                          : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
-                // recomputed per tile: a loop-invariant 64-bit per-lane address here was
-                // spilled, and its reload waited for every copy in flight
-                asm volatile("" : "+v"(src));
+                const uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
+                                                : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
                 if (tt < valid) copy16v(a.cache + d.off[tt] + src, dst + norm_off + 1024 * wave);
             }
         } else {
@@ -569,13 +567,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     float m_run, l_run;
     int e_run;
     auto begin_segment = [&]() {
-        const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + col * 256 + g * 64);
+        const uint32_t ln = lane_now(), lc = ln & 15;  // rebuilt here, not kept live across the loop
+        const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + lc * 256 + (ln >> 4) * 64);
     #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const uint4 v = col < G ? src[c] : make_uint4(0, 0, 0, 0);
+            const uint4 v = (int)lc < G ? src[c] : make_uint4(0, 0, 0, 0);
             qop[c] = u32x4{v.x, v.y, v.z, v.w};
         }
-        sc = col < G ? scarea[wave * 16 + col] : 1.f;  // columns >= G: zero queries, any positive scale
+        sc = (int)lc < G ? scarea[wave * 16 + lc] : 1.f;  // columns >= G: zero queries, any positive scale
     #pragma unroll
         for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;  // running max (log2 domain) for query head `col`
