@@ -124,9 +124,9 @@ struct DecodeArgs {
     int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
     int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
     int grid_w;         // decode workgroups per kv-head group (the tile ranges)
-    int split_c;        // workgroups w < split_c weigh wt0 parts of the tiles, the others wt1
-    int wt0, wt1;
-    uint64_t split_r;   // floor((2^64 - 1) / (split_c wt0 + (grid_w - split_c) wt1))
+    int split_c;        // workgroups per rank: workgroup w has rank min(w / split_c, 3)
+    int wt[4];          // tile weight of a workgroup of each rank
+    uint64_t split_r;   // floor((2^64 - 1) / total weight)
     TileDesc *descs;    // [total tiles] (prep kernel)
     int *tile_prefix;   // [seq][2]: first workgroup whose range covers the sequence, number of such workgroups
     int *n_tiles_total;
@@ -293,28 +293,35 @@ constexpr int kDescPieces = (int)sizeof(TileDesc) / 16;  // 16-byte copy pieces 
 constexpr int kRing = 4;                                   // descriptors staged ahead in LDS
 
 // First tile of workgroup w's range, w in [0, grid_w]: the tiles of all
-// sequences are split into contiguous ranges by weight.  With two workgroups per
-// CU, the first one dispatched onto each CU (w < split_c) is favoured by the wave
-// arbiter and runs well ahead of its neighbour (measured: with equal ranges it
-// ends at ~0.7x the other's time); weighting the ranges 65:35 (the best of a
-// 50..80 sweep) shortens the tail in which one CU slot idles.
+// sequences are split into contiguous ranges by weight.  With several workgroups
+// per CU, the ones dispatched first onto each CU (rank 0: w < split_c, one per CU)
+// are favoured by the wave arbiter and run well ahead of the later ones
+// (measured: with equal ranges and two per CU, rank 0 ends at ~0.7x the other's
+// time); weighting the ranks (65:35 for two per CU, the best of a sweep) shortens
+// the tail in which CU slots idle.
 // The split is s(w) * M >> 32 with M ~ NT 2^32 / s(grid_w) (M = the high half of
 // (NT << 32) * split_r, at most the exact quotient), computed once by the prep
 // kernel; the decode and the merge kernel evaluate exactly this, and the last
 // range ends at NT.
 struct RangeSplit {
-    int c, wt0, wt1, G, NT;
+    int c, G, NT;
+    int wt[4];
     uint64_t M;
 };
 __device__ __forceinline__ uint64_t split_multiplier(const DecodeArgs &a, int NT) {
     return __umul64hi((uint64_t)NT << 32, a.split_r);
 }
 __device__ __forceinline__ RangeSplit make_split(const DecodeArgs &a, int NT) {
-    return RangeSplit{a.split_c, a.wt0, a.wt1, a.grid_w, NT, *a.split_m};
+    return RangeSplit{a.split_c, a.grid_w, NT, {a.wt[0], a.wt[1], a.wt[2], a.wt[3]}, *a.split_m};
 }
 __device__ __forceinline__ int range_start(const RangeSplit &r, int w) {
     if (w >= r.G) return r.NT;
-    const uint64_t s = w <= r.c ? (uint64_t)w * r.wt0 : (uint64_t)r.c * r.wt0 + (uint64_t)(w - r.c) * r.wt1;
+    const int rank = min(w / r.c, 3);  // selects, not an indexed array (that would live in scratch)
+    const int wr = rank == 0 ? r.wt[0] : rank == 1 ? r.wt[1] : rank == 2 ? r.wt[2] : r.wt[3];
+    uint64_t s = (uint64_t)(w - rank * r.c) * wr;
+    if (rank > 0) s += (uint64_t)r.c * r.wt[0];
+    if (rank > 1) s += (uint64_t)r.c * r.wt[1];
+    if (rank > 2) s += (uint64_t)r.c * r.wt[2];
     return (int)((s * r.M) >> 32);
 }
 
@@ -384,7 +391,7 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
         // The decode workgroups whose ranges cover this sequence (for the merge):
         // the owner of tile t is the number of w in [1, G) with range_start(w) <= t
         // (range_start is non-decreasing and range_start(0) = 0).
-        const RangeSplit r{a.split_c, a.wt0, a.wt1, a.grid_w, NT, split_multiplier(a, NT)};
+        const RangeSplit r{a.split_c, a.grid_w, NT, {a.wt[0], a.wt[1], a.wt[2], a.wt[3]}, split_multiplier(a, NT)};
         int c_lo = 0, c_hi = 0;
         for (int w = 1 + lane; w < r.G; w += 64) {
             const int rs = range_start(r, w);
@@ -911,15 +918,18 @@ static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool conf
     const int per_cu = decode_per_cu<DT, KB, VB, HPW>(a, lds);
     const int groups = a.H / a.hpw;
     a.grid_w = std::max(1, per_cu * device_cus() / groups);
-    if (groups == 1 && per_cu == 2) {
-        a.split_c = a.grid_w / 2;  // workgroups [0, CUs) are dispatched first, one per CU
-        a.wt0 = 65;
-        a.wt1 = 35;
-    } else {
-        a.split_c = a.grid_w;
-        a.wt0 = a.wt1 = 1;
+    // rank weights by workgroups per CU (workgroups [r CUs, (r+1) CUs) are
+    // dispatched r-th onto each CU)
+    static const int kRankWt[5][4] = {{1, 1, 1, 1}, {1, 1, 1, 1}, {65, 35, 35, 35}, {1, 1, 1, 1}, {1, 1, 1, 1}};
+    const int pc = groups == 1 ? std::min(per_cu, 4) : 1;
+    a.split_c = pc > 1 ? a.grid_w / pc : a.grid_w;
+    uint64_t tot = 0;
+    for (int r = 0; r < 4; ++r) {
+        a.wt[r] = kRankWt[pc][r];
+        const int n_r = r < 3 ? std::max(0, std::min(a.split_c, a.grid_w - r * a.split_c)) : std::max(0, a.grid_w - 3 * a.split_c);
+        tot += (uint64_t)n_r * a.wt[r];
     }
-    a.split_r = UINT64_MAX / ((uint64_t)a.split_c * a.wt0 + (uint64_t)(a.grid_w - a.split_c) * a.wt1);
+    a.split_r = UINT64_MAX / tot;
 }
 
 template <int DT, int KB, int VB>
@@ -1045,7 +1055,7 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     a.o_sh = out_stride_head;
     a.grid_w = 1;
     a.split_c = 1;
-    a.wt0 = a.wt1 = 1;
+    a.wt[0] = a.wt[1] = a.wt[2] = a.wt[3] = 1;
     a.split_r = UINT64_MAX;
     const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * (a.G * 256 + 64);
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
