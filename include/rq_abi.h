@@ -196,8 +196,8 @@ int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_
  *   (kernel :43-239).  The reference accepts one sequence and places query i
  *   at position i; both agree when q_len == seq_len.
  *
- * q / out: total_q x num_q_heads x head_dim, strides as for rq_fused_decode.
- * max_q_len bounds every q_len_b; max_seq_len bounds every seq_lens[b] (keys
+ * q / out: total_q x num_q_heads x head_dim, strides as for rq_fused_decode
+ * (q rows and the rotation 16-byte aligned).  max_q_len bounds every q_len_b; max_seq_len bounds every seq_lens[b] (keys
  * past it are not read).  workspace: rq_int8_prefill_workspace_bytes() bytes,
  * 16-byte aligned, no initialisation needed (two launches: a pack kernel
  * decodes the cache's K/V into int8 tile images there, the attention kernel

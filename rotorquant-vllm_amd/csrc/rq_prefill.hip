@@ -292,26 +292,51 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     u32x4 qh[2], ql[2];
     float sq = 0.f;
     if (wave_active) {
-        // q_rot of the 16 positions into wbuf [16][128] (fp32 of the dtype-rounded value)
-        for (int idx = lane; idx < kPQ * kPD; idx += 64) {
-            const int r = idx / kPD, j = idx - r * kPD;
-            const int qi = i0 + r;
-            uint32_t v = 0;
-            if (qi < T) {
-                const uint16_t *qrow =
-                    reinterpret_cast<const uint16_t *>(a.q) + (int64_t)(q0 + qi) * a.q_st + (int64_t)hq * a.q_sh;
-                const int k0 = (j / a.rot_block) * a.rot_block;
-                float acc = 0.f;
-                for (int i = 0; i < a.rot_block; ++i)
-                    acc = __builtin_fmaf(Elem<DT>::to_f32(qrow[k0 + i]), a.R[j * kPD + k0 + i], acc);
-                v = Elem<DT>::from_f32(acc);
+        // Lane (g, col) holds the operand of position i0 + col at dims 64s + 16g .. +15
+        // (s = 0, 1): it rotates exactly those 32 dims (rotation blocks are aligned
+        // to 2 or 4 dims), q_rot rounded to the q dtype.
+        const int qi = i0 + col;
+        const bool qvalid = qi < T;
+        const uint16_t *qrow = reinterpret_cast<const uint16_t *>(a.q) + (int64_t)(q0 + (qvalid ? qi : 0)) * a.q_st +
+                               (int64_t)hq * a.q_sh;
+        const int rb = a.rot_block;
+        float qr[32];  // [s][16]: dims 64s + 16g + k
+#pragma unroll
+        for (int s_ = 0; s_ < 2; ++s_) {
+            const int base = 64 * s_ + 16 * g;
+            uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+            if (qvalid) {
+                raw[0] = *reinterpret_cast<const uint4 *>(qrow + base);
+                raw[1] = *reinterpret_cast<const uint4 *>(qrow + base + 8);
             }
-            wbuf[idx] = (uint16_t)v;
+            const uint32_t w16[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+            float xin[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) xin[k] = Elem<DT>::to_f32((w16[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int j = base + k;
+                float acc;
+                if (rb == 4) {  // R[j][4 (j / 4) + i], i < 4
+                    const float4 r = *reinterpret_cast<const float4 *>(a.R + (int64_t)j * kPD + (j & ~3));
+                    const int b0 = k & ~3;
+                    acc = __builtin_fmaf(xin[b0], r.x, 0.f);
+                    acc = __builtin_fmaf(xin[b0 + 1], r.y, acc);
+                    acc = __builtin_fmaf(xin[b0 + 2], r.z, acc);
+                    acc = __builtin_fmaf(xin[b0 + 3], r.w, acc);
+                } else {  // R[j][2 (j / 2) + i], i < 2
+                    const float2 r = *reinterpret_cast<const float2 *>(a.R + (int64_t)j * kPD + (j & ~1));
+                    const int b0 = k & ~1;
+                    acc = __builtin_fmaf(xin[b0], r.x, 0.f);
+                    acc = __builtin_fmaf(xin[b0 + 1], r.y, acc);
+                }
+                qr[16 * s_ + k] = Elem<DT>::to_f32(Elem<DT>::from_f32(acc));
+            }
         }
-        __builtin_amdgcn_wave_barrier();
-        // per-position absmax over 128 dims: lane (g, col) covers dims 32g .. 32g+31
+        // per-position absmax over 128 dims: this lane's 32, then the other three lane groups
         float amax = 0.f;
-        for (int d = 0; d < 32; ++d) amax = fmaxf(amax, fabsf(Elem<DT>::to_f32(wbuf[col * kPD + 32 * g + d])));
+#pragma unroll
+        for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qr[k]));
         amax = fmaxf(amax, __shfl_xor(amax, 16));
         amax = fmaxf(amax, __shfl_xor(amax, 32));
         sq = amax > 0.f ? amax / 127.f : 1.f;
@@ -319,16 +344,15 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         // k-step s covers dims 64s .. 64s+63; lane group g holds dims 64s + 16g .. +15,
         // stored as two 8-dim groups in the order e0 e2 e4 e6 e1 e3 e5 e7.
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s_ = 0; s_ < 2; ++s_) {
             uint32_t hw[4], lw[4];
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
-                const int base = 64 * s + 16 * g + 8 * half;
                 const int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
                 uint32_t h2[2] = {0, 0}, l2[2] = {0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float x = Elem<DT>::to_f32(wbuf[col * kPD + base + order[e]]) * inv;
+                    const float x = qr[16 * s_ + 8 * half + order[e]] * inv;
                     const int xh = sat_i8(x);
                     const int xl = sat_i8((x - (float)xh) * 128.f);
                     h2[e >> 2] |= (uint32_t)(xh & 0xff) << (8 * (e & 3));
@@ -339,10 +363,9 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
                 lw[2 * half] = l2[0];
                 lw[2 * half + 1] = l2[1];
             }
-            qh[s] = u32x4{hw[0], hw[1], hw[2], hw[3]};
-            ql[s] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+            qh[s_] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            ql[s_] = u32x4{lw[0], lw[1], lw[2], lw[3]};
         }
-        __builtin_amdgcn_wave_barrier();
     }
 
     // ---- key range: causal bound of the whole workgroup --------------------------
@@ -553,6 +576,9 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
                  "bad sizes");
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache slots must be 4-byte aligned");
+    RQ_CHECK_ARG(((uintptr_t)q % 16) == 0 && (q_stride_tok * 2) % 16 == 0 && (q_stride_head * 2) % 16 == 0,
+                 "q rows must be 16-byte aligned");
+    RQ_CHECK_ARG(((uintptr_t)rotation % 16) == 0, "rotation must be 16-byte aligned");
     if (num_seqs == 0 || max_q_len == 0 || num_blocks == 0 || max_seq_len == 0) return RQ_OK;
     const int64_t need = rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len);
     RQ_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace % 16) == 0,
