@@ -45,6 +45,22 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(size_t)(lds_u8 *)p; }
 
+// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows) with the
+// gfx950 row-swap permutes: swapping a register with itself leaves lane l
+// holding {x[l], x[l^32]} (resp. {x[l], x[l^16]}) in the two results.
+__device__ __forceinline__ float rows_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
 // Direct global -> LDS copies, issued as inline assembly so that the compiler
 // neither waits for them before unrelated LDS accesses nor counts them: the
 // kernel waits for them itself with s_waitcnt vmcnt.  Lane l writes its bytes

@@ -152,22 +152,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     }
 }
 
-// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows) with the
-// gfx950 row-swap permutes: swapping a register with itself leaves lane l
-// holding {x[l], x[l^32]} (resp. {x[l], x[l^16]}) in the two results.
-__device__ __forceinline__ float rows_max(float x) {
-    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
-}
-__device__ __forceinline__ float rows_sum(float x) {
-    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
-}
-
 // The lane index, recomputed where it is used (two VALU ops, no input register).
 // Lane-derived values needed only at segment boundaries or by the copy issue are
 // built from it: the register allocator otherwise keeps them live across the tile

@@ -337,8 +337,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         float amax = 0.f;
 #pragma unroll
         for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qr[k]));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        amax = rows_max(amax);
         sq = amax > 0.f ? amax / 127.f : 1.f;
         const float inv = 1.f / sq;
         // k-step s covers dims 64s .. 64s+63; lane group g holds dims 64s + 16g .. +15,
@@ -444,8 +443,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         float tmax = s[0];
 #pragma unroll
         for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = rows_max(tmax);
         const float m_new = fmaxf(m_run, tmax);
         if (__any(m_new > m_run)) {
             const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sq);
@@ -500,8 +498,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     if (!wave_active) return;
 
     // ---- epilogue: normalise, round to the q dtype, rotate back by R, round ----
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = rows_sum(l_run);
     const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
     // acc[m][i] = O[position col][dim 16m + 4g + i]
     __builtin_amdgcn_wave_barrier();
