@@ -114,15 +114,21 @@ struct PrefillArgs {
     int64_t o_st, o_sh;
 };
 
-// Tile image (bytes), the same in the workspace and in LDS.  Row pitches are
-// padded (K 144 B, V^T 80 B) so that the 16 lanes of an MFMA operand read hit 16
-// distinct 4-bank groups; the pad bytes are never written or read.
-constexpr int kKP = kPD + 16;                       // K row pitch
-constexpr int kVP = kKT + 16;                       // V^T row pitch
+// Tile image (bytes), the same in the workspace and in LDS.  Rows are unpadded;
+// their 16-byte pieces are stored XOR-swizzled so that the ds_read_b128 operand
+// reads of an MFMA (16 lanes: 16 rows, one piece each) run without bank
+// conflicts.  Padded pitches of 144 / 80 bytes measured two-way conflicts on
+// gfx950; these swizzles measured conflict-free (same speed as contiguous reads).
+//   K row r, piece c (0..7):   r * 128 + 16 * (c ^ (r & 7))
+//   V^T row d, piece c (0..3): d * 64 + 16 * (c ^ ((d >> 1) & 3))
+constexpr int kKP = kPD;                            // K row pitch
+constexpr int kVP = kKT;                            // V^T row pitch
 constexpr int kImKhi = 0;                           // [64 keys][kKP] int8, dims permuted per 8
 constexpr int kImKlo = kImKhi + kKT * kKP;          // same, low parts
 constexpr int kImVthi = kImKlo + kKT * kKP;         // [128 dims][kVP] int8, keys in MFMA k order
 constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
+__host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
+__host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
 constexpr int kImSk = kImVtlo + kPD * kVP;          // [64] float: k norm * kmax/127 * score_scale / 128
 constexpr int kImCw = kImSk + kKT * 4;              // [64] float: v norm / tile scale, in [0, 127]
 constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile scale * vmax/127 / 128
@@ -228,9 +234,10 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
         const uint32_t x = *reinterpret_cast<const uint32_t *>(a.cache + toff[tk] + SL.k_idx + h * 64 + 4 * dw);
         const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
-        *reinterpret_cast<uint2 *>(img + kImKhi + tk * kKP + 8 * dw) =
+        const int ko = k_piece(tk, dw >> 1) + 8 * (dw & 1);
+        *reinterpret_cast<uint2 *>(img + kImKhi + ko) =
             make_uint2(lookup_i8<KB>(ct.kh, even), lookup_i8<KB>(ct.kh, odd));
-        *reinterpret_cast<uint2 *>(img + kImKlo + tk * kKP + 8 * dw) =
+        *reinterpret_cast<uint2 *>(img + kImKlo + ko) =
             make_uint2(lookup_i8<KB>(ct.kl, even), lookup_i8<KB>(ct.kl, odd));
     }
     // V^T rows: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
@@ -250,10 +257,11 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         for (int j = 0; j < 4; ++j) {
             const int d = 8 * dw + 2 * j;
             const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
-            *reinterpret_cast<uint32_t *>(img + kImVthi + d * kVP + kk) = lookup_i8<VB>(ct.vh, se);
-            *reinterpret_cast<uint32_t *>(img + kImVthi + (d + 1) * kVP + kk) = lookup_i8<VB>(ct.vh, so);
-            *reinterpret_cast<uint32_t *>(img + kImVtlo + d * kVP + kk) = lookup_i8<VB>(ct.vl, se);
-            *reinterpret_cast<uint32_t *>(img + kImVtlo + (d + 1) * kVP + kk) = lookup_i8<VB>(ct.vl, so);
+            const int o0 = vt_piece(d, kk >> 4) + (kk & 15), o1 = vt_piece(d + 1, kk >> 4) + (kk & 15);
+            *reinterpret_cast<uint32_t *>(img + kImVthi + o0) = lookup_i8<VB>(ct.vh, se);
+            *reinterpret_cast<uint32_t *>(img + kImVthi + o1) = lookup_i8<VB>(ct.vh, so);
+            *reinterpret_cast<uint32_t *>(img + kImVtlo + o0) = lookup_i8<VB>(ct.vl, se);
+            *reinterpret_cast<uint32_t *>(img + kImVtlo + o1) = lookup_i8<VB>(ct.vl, so);
         }
     }
 }
@@ -274,6 +282,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nwaves = nthr >> 6;
     const int g = lane >> 4, col = lane & 15;
+    // this lane's operand pieces in a tile image: key col, pieces g and 4 + g; dim col, piece g
+    const int koff0 = k_piece(col, g), koff1 = k_piece(col, 4 + g), voff = vt_piece(col, g);
     const int gh = wave / a.npg;            // query head inside the GQA group
     const int pg = wave - gh * a.npg;       // 16-position group
     const int hq = h * a.G + gh;
@@ -422,9 +432,10 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             i32x4 chh = i32x4{0, 0, 0, 0}, cx = chh;
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
-                const int row = 16 * b + col;  // key
-                const u32x4 kh = *reinterpret_cast<const u32x4 *>(tb + kImKhi + row * kKP + 64 * st + 16 * g);
-                const u32x4 kl = *reinterpret_cast<const u32x4 *>(tb + kImKlo + row * kKP + 64 * st + 16 * g);
+                // key 16b + col, piece 4st + g (the swizzle term of key 16b + col is col & 7)
+                const int ko = 16 * b * kKP + (st ? koff1 : koff0);
+                const u32x4 kh = *reinterpret_cast<const u32x4 *>(tb + kImKhi + ko);
+                const u32x4 kl = *reinterpret_cast<const u32x4 *>(tb + kImKlo + ko);
                 chh = mfma_i8(kh, qh[st], chh);
                 cx = mfma_i8(kh, ql[st], cx);
                 cx = mfma_i8(kl, qh[st], cx);
@@ -481,8 +492,9 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const float o_unit = *reinterpret_cast<const float *>(tb + kImUnit);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const u32x4 vah = *reinterpret_cast<const u32x4 *>(tb + kImVthi + (16 * m + col) * kVP + 16 * g);
-            const u32x4 val = *reinterpret_cast<const u32x4 *>(tb + kImVtlo + (16 * m + col) * kVP + 16 * g);
+            // dim 16m + col, piece g (the swizzle term of dim 16m + col is (col >> 1) & 3)
+            const u32x4 vah = *reinterpret_cast<const u32x4 *>(tb + kImVthi + 16 * m * kVP + voff);
+            const u32x4 val = *reinterpret_cast<const u32x4 *>(tb + kImVtlo + 16 * m * kVP + voff);
             const i32x4 zero = i32x4{0, 0, 0, 0};
             const i32x4 oh = mfma_i8(vah, ph, zero);
             i32x4 ol = mfma_i8(vah, pl, zero);
