@@ -56,6 +56,8 @@ __device__ __forceinline__ i32x4 mfma_i8(u32x4 a, u32x4 b, i32x4 c) {
 
 // int8 table: 16 signed bytes (index -> value) in 4 dwords; lookup of four
 // indices (selector bytes) with v_perm, merging on index bit 3 for 16 entries.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
 struct Table8 {
     uint32_t w[4];
 };
@@ -70,22 +72,6 @@ __device__ __forceinline__ uint32_t lookup_i8(const Table8 &t, uint32_t sel) {
         return (perm(t.w[1], t.w[0], s7) & ~m) | (perm(t.w[3], t.w[2], s7) & m);
     }
 }
-
-// x in (-129, 128) truncated toward zero into byte `byte` of w (other bytes kept):
-// one v_cvt_i32_f32 with an SDWA byte destination.  x must come from a VALU
-// instruction (inline assembly gets no MFMA -> VALU wait states).
-__device__ __forceinline__ uint32_t cvt_i8_into(float x, uint32_t w, int byte) {
-#define RQ_CVT_BYTE(B) asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_" #B " dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(w) : "v"(x))
-    switch (byte) {
-        case 0: RQ_CVT_BYTE(0); break;
-        case 1: RQ_CVT_BYTE(1); break;
-        case 2: RQ_CVT_BYTE(2); break;
-        default: RQ_CVT_BYTE(3); break;
-    }
-#undef RQ_CVT_BYTE
-    return w;
-}
-
 
 __device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
 
@@ -130,7 +116,7 @@ constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
 __host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
 constexpr int kImSk = kImVtlo + kPD * kVP;          // [64] float: k norm * kmax/127 * score_scale / 128
-constexpr int kImCw = kImSk + kKT * 4;              // [64] float: v norm / tile scale, in [0, 127]
+constexpr int kImCw = kImSk + kKT * 4;              // [64] float: 128 * v norm / tile scale, in [0, 128 * 127]
 constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile scale * vmax/127 / 128
 constexpr int kImBytes = (kImUnit + 16 + 1023) / 1024 * 1024;  // whole 1 KB copies
 constexpr int kImChunks = kImBytes / 1024;
@@ -225,7 +211,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
         const float s_w = mx > 0.f ? mx / 127.f : 1.f;
         reinterpret_cast<float *>(img + kImSk)[tid] = nkv * (ct.kmax / 127.f * a.score_scale * (1.f / 128.f));
-        reinterpret_cast<float *>(img + kImCw)[tid] = nvv / s_w;
+        reinterpret_cast<float *>(img + kImCw)[tid] = nvv / s_w * 128.f;
         if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_w * (ct.vmax / 127.f) * (1.f / 128.f);
     }
     __syncthreads();
@@ -466,26 +452,29 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             m_run = m_new;
         }
         // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
-        // With x = w + 1/256: hi = floor(x) in [0, 127] (p <= 1, v_norm <= 127 s_w) and
-        // lo = floor(fract(x) * 128) in [0, 127], so hi + lo / 128 = round(128 w) / 128 (nearest).
-        // No clamping; both truncating converts write straight into their byte of the operand.
+        // z = trunc(128 w + 1/2) = round(128 w) in [0, 16256] (p <= 1, v_norm <= 127 s_w), so
+        // hi = z >> 7 and lo = z & 127 are both in [0, 127] and hi + lo / 128 = round(128 w) / 128.
+        // Four z go to 16-bit pairs (one perm per pair), are shifted as pairs, and their
+        // bytes are gathered by perms: 15 VALU per four scores, no clamping.
         const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
         uint32_t wh[4], wl[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const float4 cwb = *reinterpret_cast<const float4 *>(sw + 16 * b + 4 * g);
             const float cwv[4] = {cwb.x, cwb.y, cwb.z, cwb.w};
-            uint32_t hw = 0, lw = 0;
+            uint32_t z[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], sq, -msq));
                 l_run += p;
-                const float x = __builtin_fmaf(p, cwv[i], 1.f / 256.f);
-                hw = cvt_i8_into(x, hw, i);
-                lw = cvt_i8_into(__builtin_amdgcn_fractf(x) * 128.f, lw, i);
+                z[i] = (uint32_t)__builtin_fmaf(p, cwv[i], 0.5f);
             }
-            wh[b] = hw;
-            wl[b] = lw;
+            const uint32_t z01 = perm(z[1], z[0], 0x05040100u), z23 = perm(z[3], z[2], 0x05040100u);
+            const u16x2 seven = {7, 7};
+            const uint32_t h01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, z01) >> seven);
+            const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, z23) >> seven);
+            wh[b] = perm(h23, h01, 0x06040200u);
+            wl[b] = perm(z23, z01, 0x06040200u) & 0x7f7f7f7fu;
         }
         const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
         // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
