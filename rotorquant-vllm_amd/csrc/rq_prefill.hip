@@ -254,9 +254,23 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
 
 template <int DT>
 __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
-    const int qblk = blockIdx.x;
-    const int h = blockIdx.y;
-    const int64_t seq = blockIdx.z;
+    // Work order.  Workgroups are dispatched round-robin over the 8 XCDs, each with
+    // its own L2.  When the (sequence, kv head) pairs divide into 8, XCD j takes
+    // pairs j, j + 8, ... one after another, so all query blocks that stream one
+    // pair's tile images share one L2; within a pair the last (heaviest) query
+    // blocks go first.  Any other grid keeps the plain order.  Both are bijections
+    // of the grid onto (query block, kv head, sequence).
+    const uint32_t nx = gridDim.x, ny = gridDim.y;
+    const uint32_t lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    uint32_t pair = blockIdx.y + ny * blockIdx.z, xo = blockIdx.x;
+    if ((ny * gridDim.z) % 8u == 0) {
+        const uint32_t k = lin >> 3;  // rank of this workgroup on its XCD
+        pair = (lin & 7u) + 8u * (k / nx);
+        xo = k % nx;
+    }
+    const int qblk = (int)(nx - 1 - xo);
+    const int h = (int)(pair % ny);
+    const int64_t seq = pair / ny;
     const int q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
     const int T = q1 - q0;
     const int L = a.seq_lens[seq];
