@@ -292,10 +292,36 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int my_i = i0 + col;              // query index of this lane's column
     const int my_pos = pos_base + my_i;
 
-    // LDS: two tile-image buffers; the per-wave q / out staging aliases them
-    // before the key loop and after it.
+    // LDS: two tile-image buffers; the per-wave output staging aliases them after
+    // the key loop.
     extern __shared__ __align__(16) uint8_t lds[];
     uint16_t *wbuf = reinterpret_cast<uint16_t *>(lds + wave * kWaveBytes);
+
+    // ---- key range: causal bound of the whole workgroup --------------------------
+    const int last_i = min(T, (qblk + 1) * a.qb) - 1;
+    const int kv_end = min(L_eff, pos_base + last_i + 1);  // keys [0, kv_end) may be visible
+    const int n_tiles = (kv_end + kKT - 1) / kKT;
+
+    // Tile images of this (sequence, kv head), copied global -> LDS 1 KB per wave
+    // instruction into two buffers; tile t+1's copy runs while tile t is computed.
+    // Tiles 0 and 1 are issued first, so that their copies overlap the query
+    // operand's loads and arithmetic (the query operand uses no LDS).
+    const uint8_t *img0 = a.ws + ((int64_t)seq * a.H + h) * a.max_tiles * kImBytes;
+    const uint32_t lds0 = lds_addr(lds);
+    auto issue_tile = [&](int t) {
+        const uint8_t *src = img0 + (int64_t)t * kImBytes;
+        const uint32_t dst = lds0 + (t & 1) * kImBytes;
+        for (int c = wave; c < kImChunks; c += nwaves) {
+            // wave-uniform operands of the copy (the compiler cannot prove it here)
+            const uint64_t s = reinterpret_cast<uint64_t>(src + c * 1024);
+            const uint32_t slo = __builtin_amdgcn_readfirstlane((uint32_t)s);
+            const uint32_t shi = __builtin_amdgcn_readfirstlane((uint32_t)(s >> 32));
+            const uint8_t *su = reinterpret_cast<const uint8_t *>(((uint64_t)shi << 32) | slo);
+            copy16(su, 16 * lane, __builtin_amdgcn_readfirstlane(dst + c * 1024));
+        }
+    };
+    if (n_tiles > 0) issue_tile(0);
+    if (n_tiles > 1) issue_tile(1);
 
     // ---- Q^T operand (cols = this wave's 16 positions): q_rot rounded to the q dtype,
     //      quantised per position to hi/lo int8, dims in the permuted order of K ----
@@ -377,10 +403,6 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         }
     }
 
-    // ---- key range: causal bound of the whole workgroup --------------------------
-    const int last_i = min(T, (qblk + 1) * a.qb) - 1;
-    const int kv_end = min(L_eff, pos_base + last_i + 1);  // keys [0, kv_end) may be visible
-    const int n_tiles = (kv_end + kKT - 1) / kKT;
 
     float acc[8][4];
 #pragma unroll
@@ -389,25 +411,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) acc[m][i] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    // Tile images of this (sequence, kv head), copied global -> LDS 1 KB per wave
-    // instruction; tile t+1's copy runs while tile t is computed.
-    const uint8_t *img0 = a.ws + ((int64_t)seq * a.H + h) * a.max_tiles * kImBytes;
-    const uint32_t lds0 = lds_addr(lds);
-    auto issue_tile = [&](int t) {
-        const uint8_t *src = img0 + (int64_t)t * kImBytes;
-        const uint32_t dst = lds0 + (t & 1) * kImBytes;
-        for (int c = wave; c < kImChunks; c += nwaves) {
-            // wave-uniform operands of the copy (the compiler cannot prove it here)
-            const uint64_t s = reinterpret_cast<uint64_t>(src + c * 1024);
-            const uint32_t slo = __builtin_amdgcn_readfirstlane((uint32_t)s);
-            const uint32_t shi = __builtin_amdgcn_readfirstlane((uint32_t)(s >> 32));
-            const uint8_t *su = reinterpret_cast<const uint8_t *>(((uint64_t)shi << 32) | slo);
-            copy16(su, 16 * lane, __builtin_amdgcn_readfirstlane(dst + c * 1024));
-        }
-    };
-    __syncthreads();  // every wave is done with its q staging (it aliases the tile buffers)
+    // The first two tile images landed while the query operand was built.
     if (n_tiles > 0) {
-        issue_tile(0);
         wait_copies<0>();
         __syncthreads();
     }
@@ -418,7 +423,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const uint8_t *tb = lds + (ti & 1) * kImBytes;
         const float *sk = reinterpret_cast<const float *>(tb + kImSk);
         const float *sw = reinterpret_cast<const float *>(tb + kImCw);
-        if (ti + 1 < n_tiles) issue_tile(ti + 1);
+        if (ti >= 1 && ti + 1 < n_tiles) issue_tile(ti + 1);  // tile 1 went out with tile 0
         // (every wave reaches the barrier at the end of the iteration)
         if (wave_active && k0 <= pos_base + i0 + kPQ - 1) {  // else: tile entirely above this wave's diagonal
         // every key of the tile visible to all 16 positions of this wave: no mask
