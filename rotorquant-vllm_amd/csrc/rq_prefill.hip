@@ -19,9 +19,9 @@
 //
 // Two kernels per call:
 //   * prefill_pack_kernel decodes every 64-key tile of every (sequence, kv head)
-//     once into an int8 "tile image" in the caller's workspace: K hi/lo rows, V^T
-//     hi/lo rows, per-key score scales and V weights, laid out exactly as the
-//     attention kernel keeps them in LDS (padded rows included);
+//     once into an int8 "tile image" in the caller's workspace: K hi/lo rows (key
+//     norms included), V^T hi/lo rows, the tile's score unit and per-key V
+//     weights, laid out exactly as the attention kernel keeps them in LDS;
 //   * prefill_attn_kernel: one workgroup per (query block of QB positions, kv
 //     head, sequence); its waves are (query head of the GQA group, 16-position
 //     group).  It streams the tile images of its sequence and kv head into a
@@ -115,7 +115,7 @@ constexpr int kImVthi = kImKlo + kKT * kKP;         // [128 dims][kVP] int8, key
 constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
 __host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
-constexpr int kImSk = kImVtlo + kPD * kVP;          // [64] float: k norm * kmax/127 * score_scale / 128
+constexpr int kImSk = kImVtlo + kPD * kVP;          // float [0]: score unit = tile k scale * kmax/127 * score_scale / 128
 constexpr int kImCw = kImSk + kKT * 4;              // [64] float: 128 * v norm / tile scale, in [0, 128 * 127]
 constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile scale * vmax/127 / 128
 constexpr int kImBytes = (kImUnit + 16 + 1023) / 1024 * 1024;  // whole 1 KB copies
@@ -185,6 +185,11 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     __shared__ uint64_t toff[kKT];
     const CodeTables ct = make_code_tables(a);
 
+    // K codebook in int8 units; each K element is c * 127 / kmax * (k norm / tile k scale),
+    // so the key norms are part of the K operand and the score unit is one per tile.
+    __shared__ float ktab[16];
+    __shared__ float krho[kKT];
+    if (tid < 16) ktab[tid] = tid < a.nkc ? a.kc[tid] * (127.f / ct.kmax) : 0.f;
     if (tid < kKT) {
         // token offset (keys past the tile's end read slot 0 and get zero norms)
         uint64_t off = 0;
@@ -206,11 +211,17 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
             nvv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
         }
         toff[tid] = off;
-        float mx = fmaxf(nvv, 0.f);  // tile scale for w = p * v_norm: largest v norm / 127
+        // tile scales: largest v norm / 127 (for w = p * v_norm) and largest k norm
+        float mx = fmaxf(nvv, 0.f), kx = fmaxf(nkv, 0.f);
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        for (int o = 32; o >= 1; o >>= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+            kx = fmaxf(kx, __shfl_xor(kx, o));
+        }
         const float s_w = mx > 0.f ? mx / 127.f : 1.f;
-        reinterpret_cast<float *>(img + kImSk)[tid] = nkv * (ct.kmax / 127.f * a.score_scale * (1.f / 128.f));
+        const float s_k = kx > 0.f ? kx : 1.f;
+        krho[tid] = nkv / s_k;
+        if (tid == 0) *reinterpret_cast<float *>(img + kImSk) = s_k * (ct.kmax / 127.f * a.score_scale * (1.f / 128.f));
         reinterpret_cast<float *>(img + kImCw)[tid] = nvv / s_w * 128.f;
         if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_w * (ct.vmax / 127.f) * (1.f / 128.f);
     }
@@ -219,12 +230,25 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     for (int w = tid; w < kKT * 16; w += 256) {
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
         const uint32_t x = *reinterpret_cast<const uint32_t *>(a.cache + toff[tk] + SL.k_idx + h * 64 + 4 * dw);
-        const uint32_t odd = x & 0x0f0f0f0fu, even = (x >> 4) & 0x0f0f0f0fu;
+        const float rho = krho[tk];
+        uint32_t hw[2], lw[2];  // [0]: even dims (high nibbles), [1]: odd dims (low nibbles)
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            uint32_t hv = 0, lv = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float t = ktab[(x >> (8 * j + (par ? 0 : 4))) & 15u] * rho;  // |t| <= 127
+                const int hi = sat_i8(t);
+                const int lo = sat_i8((t - (float)hi) * 128.f);
+                hv |= (uint32_t)(hi & 0xff) << (8 * j);
+                lv |= (uint32_t)(lo & 0xff) << (8 * j);
+            }
+            hw[par] = hv;
+            lw[par] = lv;
+        }
         const int ko = k_piece(tk, dw >> 1) + 8 * (dw & 1);
-        *reinterpret_cast<uint2 *>(img + kImKhi + ko) =
-            make_uint2(lookup_i8<KB>(ct.kh, even), lookup_i8<KB>(ct.kh, odd));
-        *reinterpret_cast<uint2 *>(img + kImKlo + ko) =
-            make_uint2(lookup_i8<KB>(ct.kl, even), lookup_i8<KB>(ct.kl, odd));
+        *reinterpret_cast<uint2 *>(img + kImKhi + ko) = make_uint2(hw[0], hw[1]);
+        *reinterpret_cast<uint2 *>(img + kImKlo + ko) = make_uint2(lw[0], lw[1]);
     }
     // V^T rows: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
     {
@@ -421,7 +445,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const int k0 = ti * kKT;
         const int nk = min(kKT, kv_end - k0);
         const uint8_t *tb = lds + (ti & 1) * kImBytes;
-        const float *sk = reinterpret_cast<const float *>(tb + kImSk);
+        const float s_unit = *reinterpret_cast<const float *>(tb + kImSk);  // score unit of this tile
         const float *sw = reinterpret_cast<const float *>(tb + kImCw);
         if (ti >= 1 && ti + 1 < n_tiles) issue_tile(ti + 1);  // tile 1 went out with tile 0
         // (every wave reaches the barrier at the end of the iteration)
@@ -430,7 +454,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const bool full = nk == kKT && k0 + kKT - 1 <= pos_base + i0;
 
         // ---- S^T = K Q^T for 4 key blocks of 16 ----
-        // s = (hi.hi * 128 + hi.lo + lo.hi) * k scale; the score proper is s * sq.
+        // s = hi.hi * 128 + hi.lo + lo.hi; the score proper is s * s_unit * sq.
         float s[16];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -445,10 +469,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
                 cx = mfma_i8(kh, ql[st], cx);
                 cx = mfma_i8(kl, qh[st], cx);
             }
-            const float4 skb = *reinterpret_cast<const float4 *>(sk + 16 * b + 4 * g);
-            const float skv[4] = {skb.x, skb.y, skb.z, skb.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[4 * b + i] = (float)((chh[i] << 7) + cx[i]) * skv[i];
+            for (int i = 0; i < 4; ++i) s[4 * b + i] = (float)((chh[i] << 7) + cx[i]);
         }
         if (!full) {  // causal and tile-end mask: key < min(k0 + nk, position + 1)
             const int lim = min(k0 + nk, my_pos + 1) - (k0 + 4 * g);
@@ -459,7 +481,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         float tmax = s[0];
 #pragma unroll
         for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-        tmax = rows_max(tmax);
+        tmax = rows_max(tmax) * s_unit;
         const float m_new = fmaxf(m_run, tmax);
         if (__any(m_new > m_run)) {
             const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sq);
@@ -476,6 +498,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         // Four z go to 16-bit pairs (one perm per pair), are shifted as pairs, and their
         // bytes are gathered by perms: 15 VALU per four scores, no clamping.
         const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
+        const float usq = s_unit * sq;
         uint32_t wh[4], wl[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -484,7 +507,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             uint32_t z[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], sq, -msq));
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], usq, -msq));
                 l_run += p;
                 z[i] = (uint32_t)__builtin_fmaf(p, cwv[i], 0.5f);
             }
