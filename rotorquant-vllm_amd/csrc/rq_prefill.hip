@@ -54,24 +54,8 @@ __device__ __forceinline__ i32x4 mfma_i8(u32x4 a, u32x4 b, i32x4 c) {
                                                  0);
 }
 
-// int8 table: 16 signed bytes (index -> value) in 4 dwords; lookup of four
-// indices (selector bytes) with v_perm, merging on index bit 3 for 16 entries.
+// Two 16-bit lanes in one dword (P packing shifts both with one v_pk_lshrrev_b16).
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
-struct Table8 {
-    uint32_t w[4];
-};
-
-template <int BITS>
-__device__ __forceinline__ uint32_t lookup_i8(const Table8 &t, uint32_t sel) {
-    if constexpr (BITS == 3) {
-        return perm(t.w[1], t.w[0], sel);
-    } else {
-        const uint32_t s7 = sel & 0x07070707u;
-        const uint32_t m = ((sel >> 3) & 0x01010101u) * 0xFFu;
-        return (perm(t.w[1], t.w[0], s7) & ~m) | (perm(t.w[3], t.w[2], s7) & m);
-    }
-}
 
 __device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
 
@@ -116,51 +100,18 @@ constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
 __host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
 constexpr int kImSk = kImVtlo + kPD * kVP;          // float [0]: score unit = tile k scale * kmax/127 * score_scale / 128
-constexpr int kImCw = kImSk + kKT * 4;              // [64] float: 128 * v norm / tile scale, in [0, 128 * 127]
-constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile scale * vmax/127 / 128
+constexpr int kImCw = kImSk + kKT * 4;              // [64] float: unused
+constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile v scale * vmax / (127 * 127 * 128)
 constexpr int kImBytes = (kImUnit + 16 + 1023) / 1024 * 1024;  // whole 1 KB copies
 constexpr int kImChunks = kImBytes / 1024;
 constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave q / out staging: 16 x 128 16-bit values
 static_assert(2 * kImBytes >= 16 * kWaveBytes, "staging must fit in the tile buffers");
 
-// int8 hi / lo tables of the K and V codebooks: entry = c * 127 / max|c| rounded,
-// lo = the residual * 128 rounded.
-struct CodeTables {
-    Table8 kh, kl, vh, vl;
-    float kmax, vmax;
-};
-__device__ __forceinline__ CodeTables make_code_tables(const PrefillArgs &a) {
-    CodeTables t;
-    float kmax = 0.f, vmax = 0.f;
-    for (int e = 0; e < a.nkc; ++e) kmax = fmaxf(kmax, fabsf(a.kc[e]));
-    for (int e = 0; e < a.nvc; ++e) vmax = fmaxf(vmax, fabsf(a.vc[e]));
-    kmax = kmax > 0.f ? kmax : 1.f;
-    vmax = vmax > 0.f ? vmax : 1.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        uint32_t hw = 0, lw = 0, vhw = 0, vlw = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * w + i;
-            const float tk = e < a.nkc ? a.kc[e] * (127.f / kmax) : 0.f;
-            const int kh = sat_i8(tk);
-            const int kl = sat_i8((tk - (float)kh) * 128.f);
-            const float tv = e < a.nvc ? a.vc[e] * (127.f / vmax) : 0.f;
-            const int vh = sat_i8(tv);
-            const int vl = sat_i8((tv - (float)vh) * 128.f);
-            hw |= (uint32_t)(kh & 0xff) << (8 * i);
-            lw |= (uint32_t)(kl & 0xff) << (8 * i);
-            vhw |= (uint32_t)(vh & 0xff) << (8 * i);
-            vlw |= (uint32_t)(vl & 0xff) << (8 * i);
-        }
-        t.kh.w[w] = hw;
-        t.kl.w[w] = lw;
-        t.vh.w[w] = vhw;
-        t.vl.w[w] = vlw;
-    }
-    t.kmax = kmax;
-    t.vmax = vmax;
-    return t;
+// Largest |centroid| of a codebook (1 when all are zero): int8 unit = this / 127.
+__device__ __forceinline__ float codebook_max(const float *c, int n) {
+    float m = 0.f;
+    for (int e = 0; e < n; ++e) m = fmaxf(m, fabsf(c[e]));
+    return m > 0.f ? m : 1.f;
 }
 
 // Keys of a sequence the attention may read: its length, bounded by the block
@@ -171,7 +122,6 @@ __device__ __forceinline__ int visible_keys(const PrefillArgs &a, int64_t seq) {
 }
 
 // ---- pack: one workgroup (256 threads) per (tile, kv head, sequence) --------
-template <int KB, int VB>
 __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     const int tile = blockIdx.x, h = blockIdx.y;
     const int64_t seq = blockIdx.z;
@@ -183,13 +133,17 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     uint8_t *img = a.ws + (((int64_t)seq * a.H + h) * a.max_tiles + tile) * kImBytes;
     const SlotLayout SL(a.H, kPD);
     __shared__ uint64_t toff[kKT];
-    const CodeTables ct = make_code_tables(a);
+    const float kmax = codebook_max(a.kc, a.nkc), vmax = codebook_max(a.vc, a.nvc);
 
     // K codebook in int8 units; each K element is c * 127 / kmax * (k norm / tile k scale),
     // so the key norms are part of the K operand and the score unit is one per tile.
-    __shared__ float ktab[16];
-    __shared__ float krho[kKT];
-    if (tid < 16) ktab[tid] = tid < a.nkc ? a.kc[tid] * (127.f / ct.kmax) : 0.f;
+    // Likewise V: c * 127 / vmax * (v norm / tile v scale).
+    __shared__ float ktab[16], vtab[16];
+    __shared__ float krho[kKT], vrho[kKT];
+    if (tid < 16) {
+        ktab[tid] = tid < a.nkc ? a.kc[tid] * (127.f / kmax) : 0.f;
+        vtab[tid] = tid < a.nvc ? a.vc[tid] * (127.f / vmax) : 0.f;
+    }
     if (tid < kKT) {
         // token offset (keys past the tile's end read slot 0 and get zero norms)
         uint64_t off = 0;
@@ -211,19 +165,20 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
             nvv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
         }
         toff[tid] = off;
-        // tile scales: largest v norm / 127 (for w = p * v_norm) and largest k norm
+        // tile scales: the largest v norm and the largest k norm
         float mx = fmaxf(nvv, 0.f), kx = fmaxf(nkv, 0.f);
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) {
             mx = fmaxf(mx, __shfl_xor(mx, o));
             kx = fmaxf(kx, __shfl_xor(kx, o));
         }
-        const float s_w = mx > 0.f ? mx / 127.f : 1.f;
+        const float s_v = mx > 0.f ? mx : 1.f;
         const float s_k = kx > 0.f ? kx : 1.f;
         krho[tid] = nkv / s_k;
-        if (tid == 0) *reinterpret_cast<float *>(img + kImSk) = s_k * (ct.kmax / 127.f * a.score_scale * (1.f / 128.f));
-        reinterpret_cast<float *>(img + kImCw)[tid] = nvv / s_w * 128.f;
-        if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_w * (ct.vmax / 127.f) * (1.f / 128.f);
+        vrho[tid] = nvv / s_v;
+        if (tid == 0) *reinterpret_cast<float *>(img + kImSk) = s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f));
+        // P V = sum_k (w_k / 127) V_k with w = 127 p: one unit per tile
+        if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_v * (vmax / (127.f * 127.f * 128.f));
     }
     __syncthreads();
     // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
@@ -263,17 +218,29 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
                                 perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
         const int t0 = 4 * tq;  // = 16b + 4gg
         const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
+        float rv[4];  // byte i of a transposed word is key t0 + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rv[i] = vrho[t0 + i];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int d = 8 * dw + 2 * j;
-            const uint32_t se = (G4[j] >> 4) & 0x0f0f0f0fu, so = G4[j] & 0x0f0f0f0fu;
-            const int o0 = vt_piece(d, kk >> 4) + (kk & 15), o1 = vt_piece(d + 1, kk >> 4) + (kk & 15);
-            *reinterpret_cast<uint32_t *>(img + kImVthi + o0) = lookup_i8<VB>(ct.vh, se);
-            *reinterpret_cast<uint32_t *>(img + kImVthi + o1) = lookup_i8<VB>(ct.vh, so);
-            *reinterpret_cast<uint32_t *>(img + kImVtlo + o0) = lookup_i8<VB>(ct.vl, se);
-            *reinterpret_cast<uint32_t *>(img + kImVtlo + o1) = lookup_i8<VB>(ct.vl, so);
-        }
-    }
+#pragma unroll
+            for (int par = 0; par < 2; ++par) {  // dim d: high nibbles, dim d + 1: low nibbles
+                const uint32_t sel = par ? (G4[j] & 0x0f0f0f0fu) : ((G4[j] >> 4) & 0x0f0f0f0fu);
+                uint32_t hv = 0, lv = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float t = vtab[(sel >> (8 * i)) & 15u] * rv[i];  // |t| <= 127
+                    const int hi = sat_i8(t);
+                    const int lo = sat_i8((t - (float)hi) * 128.f);
+                    hv |= (uint32_t)(hi & 0xff) << (8 * i);
+                    lv |= (uint32_t)(lo & 0xff) << (8 * i);
+                }
+                const int o = vt_piece(d + par, kk >> 4) + (kk & 15);
+                *reinterpret_cast<uint32_t *>(img + kImVthi + o) = hv;
+                *reinterpret_cast<uint32_t *>(img + kImVtlo + o) = lv;
+            }
+        }    }
 }
 
 template <int DT>
@@ -446,7 +413,6 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const int nk = min(kKT, kv_end - k0);
         const uint8_t *tb = lds + (ti & 1) * kImBytes;
         const float s_unit = *reinterpret_cast<const float *>(tb + kImSk);  // score unit of this tile
-        const float *sw = reinterpret_cast<const float *>(tb + kImCw);
         if (ti >= 1 && ti + 1 < n_tiles) issue_tile(ti + 1);  // tile 1 went out with tile 0
         // (every wave reaches the barrier at the end of the iteration)
         if (wave_active && k0 <= pos_base + i0 + kPQ - 1) {  // else: tile entirely above this wave's diagonal
@@ -492,24 +458,23 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             l_run *= alpha;
             m_run = m_new;
         }
-        // w = p * v_norm / s_w in [0, 127]: hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
-        // z = trunc(128 w + 1/2) = round(128 w) in [0, 16256] (p <= 1, v_norm <= 127 s_w), so
-        // hi = z >> 7 and lo = z & 127 are both in [0, 127] and hi + lo / 128 = round(128 w) / 128.
-        // Four z go to 16-bit pairs (one perm per pair), are shifted as pairs, and their
-        // bytes are gathered by perms: 15 VALU per four scores, no clamping.
+        // w = 127 p in [0, 127] (p <= 1): hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
+        // z = trunc(128 w + 1/2) = round(128 w) in [0, 16256], so hi = z >> 7 and lo = z & 127
+        // are both in [0, 127] and hi + lo / 128 = z / 128.  Four z go to 16-bit pairs (one
+        // perm per pair), are shifted as pairs, and their bytes are gathered by perms.  The
+        // row sum comes from the same bytes (z = 128 hi + lo, one v_dot4 per word), so the
+        // numerator and the denominator use the same quantised weights.
         const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
         const float usq = s_unit * sq;
         uint32_t wh[4], wl[4];
+        uint32_t zsum = 0;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const float4 cwb = *reinterpret_cast<const float4 *>(sw + 16 * b + 4 * g);
-            const float cwv[4] = {cwb.x, cwb.y, cwb.z, cwb.w};
             uint32_t z[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], usq, -msq));
-                l_run += p;
-                z[i] = (uint32_t)__builtin_fmaf(p, cwv[i], 0.5f);
+                z[i] = (uint32_t)__builtin_fmaf(p, 128.f * 127.f, 0.5f);
             }
             const uint32_t z01 = perm(z[1], z[0], 0x05040100u), z23 = perm(z[3], z[2], 0x05040100u);
             const u16x2 seven = {7, 7};
@@ -517,7 +482,10 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, z23) >> seven);
             wh[b] = perm(h23, h01, 0x06040200u);
             wl[b] = perm(z23, z01, 0x06040200u) & 0x7f7f7f7fu;
+            zsum = __builtin_amdgcn_udot4(wh[b], 0x80808080u, zsum, false);
+            zsum = __builtin_amdgcn_udot4(wl[b], 0x01010101u, zsum, false);
         }
+        l_run = __builtin_fmaf((float)zsum, 1.f / (128.f * 127.f), l_run);  // zsum < 2^24: exact
         const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
         // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
         const float o_unit = *reinterpret_cast<const float *>(tb + kImUnit);
@@ -563,17 +531,9 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     }
 }
 
-template <int KB, int VB>
 static void launch_pack(const PrefillArgs &a, int64_t num_seqs, hipStream_t st) {
     dim3 grid((unsigned)a.max_tiles, (unsigned)a.H, (unsigned)num_seqs);
-    hipLaunchKernelGGL((prefill_pack_kernel<KB, VB>), grid, dim3(256), 0, st, a);
-}
-
-static void launch_pack_bits(const PrefillArgs &a, int64_t ns, int kb, int vb, hipStream_t st) {
-    if (kb == 3 && vb == 3) launch_pack<3, 3>(a, ns, st);
-    else if (kb == 3) launch_pack<3, 4>(a, ns, st);
-    else if (vb == 3) launch_pack<4, 3>(a, ns, st);
-    else launch_pack<4, 4>(a, ns, st);
+    hipLaunchKernelGGL(prefill_pack_kernel, grid, dim3(256), 0, st, a);
 }
 
 template <int DT>
@@ -657,9 +617,8 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
     const int nwaves = a.G * a.npg;
-    const int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     hipStream_t st = (hipStream_t)stream;
-    launch_pack_bits(a, num_seqs, kb, vb, st);
+    launch_pack(a, num_seqs, st);
     int rc = check_launch("prefill_pack_kernel");
     if (rc) return rc;
     if (dtype == RQ_DTYPE_BF16) launch_attn<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, st);
