@@ -218,7 +218,7 @@ int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q
                     void *workspace, int64_t workspace_bytes,
                     void *stream);
 
-/* Workspace bytes rq_int8_prefill needs: one int8 tile image (about 39 KB)
+/* Workspace bytes rq_int8_prefill needs: one int8 tile image (33 KB)
  * per 64 keys of max_seq_len, per sequence and kv head.  No counterpart in the
  * reference, which decodes K/V inside its attention kernel. */
 int64_t rq_int8_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len);

@@ -99,10 +99,9 @@ constexpr int kImVthi = kImKlo + kKT * kKP;         // [128 dims][kVP] int8, key
 constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
 __host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
-constexpr int kImSk = kImVtlo + kPD * kVP;          // float [0]: score unit = tile k scale * kmax/127 * score_scale / 128
-constexpr int kImCw = kImSk + kKT * 4;              // [64] float: unused
-constexpr int kImUnit = kImCw + kKT * 4;            // float: output unit = tile v scale * vmax / (127 * 127 * 128)
-constexpr int kImBytes = (kImUnit + 16 + 1023) / 1024 * 1024;  // whole 1 KB copies
+constexpr int kImSk = kImVtlo + kPD * kVP;          // float: score unit = tile k scale * kmax/127 * score_scale / 128
+constexpr int kImUnit = kImSk + 4;                  // float: output unit = tile v scale * vmax / (127 * 127 * 128)
+constexpr int kImBytes = (kImUnit + 4 + 1023) / 1024 * 1024;  // whole 1 KB copies
 constexpr int kImChunks = kImBytes / 1024;
 constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave q / out staging: 16 x 128 16-bit values
 static_assert(2 * kImBytes >= 16 * kWaveBytes, "staging must fit in the tile buffers");
