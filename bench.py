@@ -108,8 +108,9 @@ def time_decode(inp, steps, warmup, graphs=False):
     kernels) issued through a pre-validated launcher, so the host issues a step
     in a few microseconds and the GPU does not wait for Python.  With
     graphs=True the calls are instead captured in HIP graphs and replayed (the
-    replays' outputs are checked bit for bit against eager calls).  Events
-    bracket every step on the launch stream."""
+    replays' outputs are checked bit for bit against eager calls).  Two events
+    bracket the timed steps on the launch stream (avg_ms); a second pass with an
+    event after every step gives the per-step median and minimum."""
     import torch
 
     from rotorquant_vllm import _lib
@@ -159,16 +160,25 @@ def time_decode(inp, steps, warmup, graphs=False):
     for i in range(warmup):
         run(i)
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    # Timed region: the steps back to back, one event before and one after (an event
+    # between steps adds a few microseconds of queue work to every step).
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        run(i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    # Per-step spread, from a second pass with an event after every step.
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
     for i in range(steps):
         run(i)
         ev[i + 1].record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-    total_ms = ev[0].elapsed_time(ev[steps])
     for i in range(n):  # replays must reproduce the eager results exactly
         run(i)
     torch.cuda.synchronize()

@@ -289,23 +289,25 @@ constexpr int kRing = 4;                                   // descriptors staged
 // range ends at NT.
 struct RangeSplit {
     int c, G, NT;
-    int wt[4];
+    int w0, w1, w2, w3;  // rank weights
     uint64_t M;
 };
 __device__ __forceinline__ uint64_t split_multiplier(const DecodeArgs &a, int NT) {
     return __umul64hi((uint64_t)NT << 32, a.split_r);
 }
 __device__ __forceinline__ RangeSplit make_split(const DecodeArgs &a, int NT) {
-    return RangeSplit{a.split_c, a.grid_w, NT, {a.wt[0], a.wt[1], a.wt[2], a.wt[3]}, *a.split_m};
+    return RangeSplit{a.split_c, a.grid_w, NT, a.wt[0], a.wt[1], a.wt[2], a.wt[3], *a.split_m};
 }
-__device__ __forceinline__ int range_start(const RangeSplit &r, int w) {
+// r by value: through a reference the rank select below is turned into an indexed
+// load of the struct, which the compiler then moves to LDS.
+__device__ __forceinline__ int range_start(const RangeSplit r, int w) {
     if (w >= r.G) return r.NT;
-    const int rank = min(w / r.c, 3);  // selects, not an indexed array (that would live in scratch)
-    const int wr = rank == 0 ? r.wt[0] : rank == 1 ? r.wt[1] : rank == 2 ? r.wt[2] : r.wt[3];
+    const int rank = min(w / r.c, 3);
+    const int wr = rank == 0 ? r.w0 : rank == 1 ? r.w1 : rank == 2 ? r.w2 : r.w3;
     uint64_t s = (uint64_t)(w - rank * r.c) * wr;
-    if (rank > 0) s += (uint64_t)r.c * r.wt[0];
-    if (rank > 1) s += (uint64_t)r.c * r.wt[1];
-    if (rank > 2) s += (uint64_t)r.c * r.wt[2];
+    if (rank > 0) s += (uint64_t)r.c * r.w0;
+    if (rank > 1) s += (uint64_t)r.c * r.w1;
+    if (rank > 2) s += (uint64_t)r.c * r.w2;
     return (int)((s * r.M) >> 32);
 }
 
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
         // The decode workgroups whose ranges cover this sequence (for the merge):
         // the owner of tile t is the number of w in [1, G) with range_start(w) <= t
         // (range_start is non-decreasing and range_start(0) = 0).
-        const RangeSplit r{a.split_c, a.grid_w, NT, {a.wt[0], a.wt[1], a.wt[2], a.wt[3]}, split_multiplier(a, NT)};
+        const RangeSplit r{a.split_c, a.grid_w, NT, a.wt[0], a.wt[1], a.wt[2], a.wt[3], split_multiplier(a, NT)};
         int c_lo = 0, c_hi = 0;
         for (int w = 1 + lane; w < r.G; w += 64) {
             const int rs = range_start(r, w);
@@ -808,10 +810,15 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     // partials sit at slots w + seq for w in [w_lo, w_lo + nch); workgroups with an
     // empty range (more workgroups than tiles) wrote nothing.
     // (the prep kernel does not run when no sequence has tokens: then nch = 0)
+    // The merge is a short chain of dependent loads, so the words it needs first are
+    // loaded together, unconditionally (they are in-bounds workspace words, written by
+    // the prep kernel for every sequence), and used only when the sequence has tiles.
+    const int tp_lo = a.tile_prefix[2 * seq], tp_n = a.tile_prefix[2 * seq + 1];
+    const int ntt = *a.n_tiles_total;
     const int n = seq_tiles(a, seq);
-    const int w_lo = n > 0 ? a.tile_prefix[2 * seq] : 0, nch = n > 0 ? a.tile_prefix[2 * seq + 1] : 0;
-    const RangeSplit rsp = make_split(a, *a.n_tiles_total);
-    auto has_tiles = [&](int w) { return range_start(rsp, w + 1) > range_start(rsp, w); };
+    const int w_lo = n > 0 ? tp_lo : 0, nch = n > 0 ? tp_n : 0;
+    const RangeSplit rsp = make_split(a, ntt);
+    auto has_tiles = [rsp](int w) { return range_start(rsp, w + 1) > range_start(rsp, w); };
     const float *ml = a.part_ml + (w_lo + seq) * (int64_t)a.HQ * 2 + hq * 2;
     const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
