@@ -336,6 +336,8 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     const int nw = blockDim.x >> 6;
     __shared__ __align__(16) uint16_t wq_all[kMaxWaves][16 * kD];
     __shared__ int part[2 * kMaxWaves];
+    // a descriptor workgroup past the end of its sequence's tokens has nothing to do
+    if (y >= 1 && 4 * (y - 1) * (int)blockDim.x >= seq_tiles(a, seq) * kTile) return;
     if (y == 0) {
         for (int h = wave; h < a.H; h += nw) {
             u32x4 qop[4];
@@ -1053,7 +1055,12 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     if (a.max_len > 0) {
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, true);
         else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st, true);
-        const dim3 pgrid((unsigned)num_seqs, 4), pblock(64 * std::min(a.H, kMaxWaves));
+        // Descriptor workgroups per sequence (y >= 1): enough that each thread writes at
+        // most two steps of four tokens of the longest sequence (a fixed three made the
+        // prep kernel of a 131072-token sequence take ~49 us).
+        const int pthreads = 64 * std::min(a.H, kMaxWaves);
+        const int ny = std::min(64, std::max(3, (a.max_len + 8 * pthreads - 1) / (8 * pthreads)));
+        const dim3 pgrid((unsigned)num_seqs, (unsigned)(1 + ny)), pblock(pthreads);
         if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, 0, st, a);
         else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, 0, st, a);
         int rc = check_launch("decode_prep_kernel");
