@@ -334,7 +334,7 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
-    __shared__ __align__(16) uint16_t wq_all[kMaxWaves][16 * kD];
+    extern __shared__ __align__(16) uint8_t prep_lds[];  // query staging, 16 x kD 16-bit values per wave
     __shared__ int part[2 * kMaxWaves];
     // a descriptor workgroup past the end of its sequence's tokens has nothing to do
     if (y >= 1 && 4 * (y - 1) * (int)blockDim.x >= seq_tiles(a, seq) * kTile) return;
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
         for (int h = wave; h < a.H; h += nw) {
             u32x4 qop[4];
             float sc;
-            query_operand<DT>(a, seq, h, wq_all[wave], qop, sc);
+            query_operand<DT>(a, seq, h, reinterpret_cast<uint16_t *>(prep_lds) + wave * 16 * kD, qop, sc);
             const int g = lane >> 4, col = lane & 15;
             uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 16 + col) * 64 + g * 16);
             if (col < a.G) {
@@ -1061,8 +1061,10 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
         const int pthreads = 64 * std::min(a.H, kMaxWaves);
         const int ny = std::min(64, std::max(3, (a.max_len + 8 * pthreads - 1) / (8 * pthreads)));
         const dim3 pgrid((unsigned)num_seqs, (unsigned)(1 + ny)), pblock(pthreads);
-        if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, 0, st, a);
-        else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, 0, st, a);
+        // query staging sized by the waves launched (it bounds how many workgroups a CU holds)
+        const size_t plds = (size_t)(pthreads / 64) * 16 * kD * sizeof(uint16_t);
+        if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_BF16>, pgrid, pblock, plds, st, a);
+        else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, plds, st, a);
         int rc = check_launch("decode_prep_kernel");
         if (rc) return rc;
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, false);
