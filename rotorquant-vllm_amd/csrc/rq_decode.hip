@@ -786,10 +786,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     end_segment();
 }
 
+// Segments per merge pass: lane c < kMergePass loads segment c's (m, l), and every
+// lane loads its two dims of all of them before any is used (one round trip per pass).
+constexpr int kMergePass = 32;
+
 // Merge the partials of (seq, query head): log-sum-exp over the segments, round
 // to the query dtype (the reference's out_rot, fused_paged_rq_decode.py:201-206),
 // rotate back by R in fp32 and round again (:308).  One wave per query head,
-// two head dims per lane; per pass of 16 segments, the (m, l) of each segment
+// two head dims per lane; per pass of kMergePass segments, the (m, l) of each segment
 // and the lane's accumulator entries of all of them are loaded together.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
@@ -825,19 +829,19 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
     float lsum = 0.f, o0 = 0.f, o1 = 0.f, M = -INFINITY;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-        // lane c (< 16) loads segment c0 + c's (m, l); every lane loads its two dims of
-        // up to 16 segments' accumulators -- all issued before any is used
-        const int c = c0 + (lane & 15);
+    for (int c0 = 0; c0 < nch; c0 += kMergePass) {
+        // lane c (< kMergePass) loads segment c0 + c's (m, l); every lane loads its two
+        // dims of up to kMergePass segments' accumulators -- all issued before any is used
+        const int c = c0 + (lane & (kMergePass - 1));
         const bool ok = c < nch && has_tiles(w_lo + c);
-        const uint64_t okm = __ballot(ok && lane < 16);
+        const uint64_t okm = __ballot(ok && lane < kMergePass);
         const float2 v = ok ? *reinterpret_cast<const float2 *>(ml + c * cs_ml) : make_float2(-INFINITY, 0.f);
-        float2 x[16];
+        float2 x[kMergePass];
     #pragma unroll
-        for (int u = 0; u < 16; ++u)
+        for (int u = 0; u < kMergePass; ++u)
             x[u] = (okm >> u) & 1 ? reinterpret_cast<const float2 *>(pa + (c0 + u) * cs_acc)[lane] : make_float2(0.f, 0.f);
-        float pm = lane < 16 ? v.x : -INFINITY;
-        for (int o = 8; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
+        float pm = lane < kMergePass ? v.x : -INFINITY;
+        for (int o = kMergePass / 2; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
         pm = __shfl(pm, 0);
         const float Mn = fmaxf(M, pm);
         const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // -inf - finite -> 0 on the first pass
@@ -845,12 +849,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         o1 *= alpha;
         lsum *= alpha;
         M = Mn;
-        const float w = ok && lane < 16 ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
+        const float w = ok && lane < kMergePass ? __builtin_amdgcn_exp2f(v.x - M) : 0.f;
         float wl = w * v.y;
-        for (int o = 8; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
+        for (int o = kMergePass / 2; o >= 1; o >>= 1) wl += __shfl_xor(wl, o);
         lsum += __shfl(wl, 0);
     #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < kMergePass; ++u) {
             const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
             o0 += wu * x[u].x;
             o1 += wu * x[u].y;
