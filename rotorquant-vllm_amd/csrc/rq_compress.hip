@@ -24,8 +24,8 @@
 //     q0 within one ulp), provided nothing underflows; rows or elements outside
 //     the guarded range (d > 2^40, or 0 < |x| < 2^-60) use the plain division.
 //     fp16 elements enter these fmas directly through v_fma_mix_f32.
-//   * index : a 64-cell table over a monotone map cell(v) = clamp(fma(v, s, c))
-//     replaces the 15 comparisons.  Because cell() is monotone, every boundary
+//   * index : a 256-cell table over a monotone map cell(v) = u8(fma(v, s, c))
+//     (one saturating convert) replaces the 15 comparisons.  Because cell() is monotone, every boundary
 //     in a lower cell than v is < v and every boundary in a higher cell is > v;
 //     when each cell holds at most one boundary (checked per workgroup), the
 //     count is table[cell].n + (table[cell].b < v).  Boundary sets that fail the
@@ -45,7 +45,7 @@ constexpr int kRows = 64;        // rows per workgroup
 constexpr int kThreads = 256;    // four waves
 constexpr int kMaxBounds = 15;
 constexpr int kMaxD = 256;
-constexpr int kCells = 64;       // bucketize lookup cells per boundary set
+constexpr int kCells = 256;      // bucketize lookup cells per boundary set (the u8 convert's range)
 
 // Where the rows come from and where their bytes go.
 struct RowMap {
@@ -123,13 +123,14 @@ __device__ __forceinline__ uint8_t *slot_base(const RowMap &m, int64_t s) {
     return m.cache + blk * m.stride_block + off * m.stride_token;
 }
 
-// Monotone (non-decreasing) map of a value to a lookup cell.  v_cvt_i32_f32
-// truncates and saturates (NaN -> 0), so the map is defined for every input.
+// Monotone (non-decreasing) map of a value to a lookup cell: v_cvt_pk_u8_f32 rounds
+// to an integer and saturates to [0, 255] (NaN -> 0) in one instruction, so the map
+// is defined for every input and needs no clamp.
 __device__ __forceinline__ int cell_of(float v, float s, float c) {
     const float t = __builtin_fmaf(v, s, c);
-    int i;
-    asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(t));
-    return min(max(i, 0), kCells - 1);
+    uint32_t i;
+    asm("v_cvt_pk_u8_f32 %0, %1, 0, 0" : "=v"(i) : "v"(t));
+    return (int)i;
 }
 
 // Mixed-precision fused multiply-adds (v_fma_mix_f32): the f16 operand is the
@@ -398,13 +399,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compre
     __syncthreads();
     uint4 v[4];
     load_batch0(0, v);
-    if (tid < 2 * kCells) {
+    for (int e = tid; e < 2 * kCells; e += kThreads) {
         // table entry {boundary, count} of cell c for both sets
-        const int kind = tid / kCells, c = tid % kCells;
+        const int kind = e / kCells, c = e % kCells;
         const int nb = kind ? nvb : nkb;
         int n = 0;
         for (int i = 0; i < nb; ++i) n += cells[kind * 16 + i] < c;
-        tbl[tid] = make_float2(bnd[kind * 16 + n], __int_as_float(n));
+        tbl[e] = make_float2(bnd[kind * 16 + n], __int_as_float(n));
     }
 
     for (int buf = 0;; buf ^= 1) {
