@@ -92,7 +92,8 @@ def test_prefill_unit_scale_bf16_iso4():
 
 def test_prefill_gqa16_one_kv_head():
     """16 query heads on one kv head: the widest workgroup (16 waves), where the per-wave
-    q staging buffers overlap the tile area."""
+    output staging buffers fill the tile area; two (sequence, kv head) pairs also take
+    the plain work order (the XCD-aware one needs a multiple of 8 pairs)."""
     p = Params("iso", 4, 3)
     check(prefill_case(9, [200, 77], [260, 77], 1, 16, p), "gqa16")
 
