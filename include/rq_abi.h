@@ -127,7 +127,7 @@ int rq_decompress(const uint8_t *packed, const float *norms, int64_t n_rows, int
  * one its compact id in ascending physical order (the order of the sorted
  * unique in the reference), and each is decompressed once.
  *
- * workspace: at least rq_paged_decompress_workspace_bytes(num_blocks) bytes.
+ * workspace: at least rq_paged_decompress_workspace_bytes(num_blocks) bytes, 16-byte aligned.
  * out_k / out_v: capacity_blocks x block_size x num_kv_heads x head_dim of
  * out_dtype.  remapped_block_table: num_seqs x max_blocks int32 (same shape
  * as block_table) receiving the compact ids (entries past a sequence's

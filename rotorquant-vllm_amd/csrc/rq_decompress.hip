@@ -78,14 +78,23 @@ __global__ void mark_kernel(const int32_t *__restrict__ bt, int64_t num_seqs, in
 }
 
 // Single-workgroup exclusive scan of flag[0..n) into compact[], total into *count.
+// Thread t owns a contiguous run of a multiple of 4 entries (16-byte loads and
+// stores; flag and compact are 16-byte aligned), four loads in flight per step.
 __global__ __launch_bounds__(1024) void scan_kernel(const int32_t *__restrict__ flag, int32_t *__restrict__ compact,
                                                      int64_t n, int32_t *count) {
     __shared__ int32_t part[1024];
     const int tid = threadIdx.x;
-    const int64_t per = (n + 1023) / 1024;
-    const int64_t beg = tid * per, end = beg + per < n ? beg + per : n;
+    const int64_t per = (((n + 1023) / 1024) + 3) & ~(int64_t)3;
+    const int64_t beg = tid * per < n ? tid * per : n, end = beg + per < n ? beg + per : n;
+    const int64_t nv = (end - beg) >> 2;  // whole 4-entry groups
+    const int4 *f4 = reinterpret_cast<const int4 *>(flag + beg);
     int32_t s = 0;
-    for (int64_t i = beg; i < end; ++i) s += flag[i];
+#pragma unroll 4
+    for (int64_t k = 0; k < nv; ++k) {
+        const int4 x = f4[k];
+        s += x.x + x.y + x.z + x.w;
+    }
+    for (int64_t i = beg + 4 * nv; i < end; ++i) s += flag[i];
     part[tid] = s;
     __syncthreads();
     // Hillis-Steele inclusive scan over the 1024 partial sums.
@@ -96,7 +105,19 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t *__restrict__ 
         __syncthreads();
     }
     int32_t run = part[tid] - s;
-    for (int64_t i = beg; i < end; ++i) {
+    int4 *c4 = reinterpret_cast<int4 *>(compact + beg);
+#pragma unroll 4
+    for (int64_t k = 0; k < nv; ++k) {
+        const int4 x = f4[k];
+        int4 o;
+        o.x = run;
+        o.y = run + x.x;
+        o.z = o.y + x.y;
+        o.w = o.z + x.z;
+        run = o.w + x.w;
+        c4[k] = o;
+    }
+    for (int64_t i = beg + 4 * nv; i < end; ++i) {
         compact[i] = run;
         run += flag[i];
     }
@@ -123,14 +144,16 @@ __global__ __launch_bounds__(256) void expand_kernel(const uint8_t *__restrict__
     const int64_t c = compact[p];
     if (c >= capacity) return;
     SlotLayout L(H, D);
+    // Rows are (component, token, head); a row has D / 8 packed dwords.  The launch
+    // uses a multiple of D / 8 threads, so each thread keeps one dword position w and
+    // steps over rows: one division (by H) per row instead of three per dword.
     const int words = D / 8;
-    const int per_comp = block_size * H * words;  // dwords per component
-    for (int i = threadIdx.x; i < 2 * per_comp; i += blockDim.x) {
-        int comp = i / per_comp;  // 0 = K, 1 = V
-        int rem = i - comp * per_comp;
-        int tok = rem / (H * words);
-        int hw = rem - tok * H * words;
-        int h = hw / words, w = hw - h * words;
+    const int rows_per_comp = block_size * H;
+    const int w = threadIdx.x % words, rstep = blockDim.x / words;
+    for (int r = threadIdx.x / words; r < 2 * rows_per_comp; r += rstep) {
+        const int comp = r >= rows_per_comp ? 1 : 0;  // 0 = K, 1 = V
+        const int rr = r - comp * rows_per_comp;
+        const int tok = (int)((uint32_t)rr / (uint32_t)H), h = rr - tok * H;
         const uint8_t *slot = cache + p * stride_block + (int64_t)tok * stride_token;
         uint32_t word = reinterpret_cast<const uint32_t *>(slot + (comp ? L.v_idx : L.k_idx) + h * L.half)[w];
         float norm = *reinterpret_cast<const float *>(slot + (comp ? L.v_norm : L.k_norm) + 4 * h);
@@ -203,7 +226,7 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
                                    int32_t n_v_centroids, void *out_k, void *out_v, int32_t out_dtype,
                                    int64_t capacity_blocks, int32_t *remapped_block_table, int32_t *num_unique,
                                    void *workspace, int64_t workspace_bytes, void *stream) {
-    RQ_CHECK_ARG(head_dim % 16 == 0 && head_dim >= 16, "head_dim %d must be a multiple of 16", head_dim);
+    RQ_CHECK_ARG(head_dim % 16 == 0 && head_dim >= 16 && head_dim <= 8192, "head_dim %d must be a multiple of 16 in 16..8192", head_dim);
     RQ_CHECK_ARG(num_kv_heads >= 1 && block_size >= 1 && num_blocks >= 0 && num_seqs >= 0 && max_blocks >= 0,
                  "bad sizes");
     RQ_CHECK_ARG(n_k_centroids >= 1 && n_k_centroids <= 16 && n_v_centroids >= 1 && n_v_centroids <= 16,
@@ -211,12 +234,13 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
     RQ_CHECK_ARG(out_dtype == RQ_DTYPE_F16 || out_dtype == RQ_DTYPE_BF16 || out_dtype == RQ_DTYPE_F32,
                  "bad out_dtype %d", out_dtype);
     RQ_CHECK_ARG(workspace_bytes >= rq_paged_decompress_workspace_bytes(num_blocks), "workspace too small");
+    RQ_CHECK_ARG(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache must be 4-byte aligned");
     RQ_CHECK_ARG(((uintptr_t)out_k % 16) == 0 && ((uintptr_t)out_v % 16) == 0, "outputs must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     int32_t *flag = reinterpret_cast<int32_t *>(workspace);
-    int32_t *compact = flag + num_blocks;
+    int32_t *compact = flag + ((num_blocks + 3) & ~(int64_t)3);  // 16-byte aligned (within the 256-byte slack)
     if (num_blocks > 0) {
         hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(num_blocks, 256)), dim3(256), 0, st, flag, num_blocks);
         if (num_seqs > 0 && max_blocks > 0)
@@ -225,9 +249,11 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
                                flag);
         hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, flag, compact, num_blocks, num_unique);
         if (capacity_blocks > 0) {
+            const int wpr = head_dim / 8;  // packed dwords per row; the block is a multiple of it
+            const int ethreads = wpr >= 256 ? wpr : (256 / wpr) * wpr;
             switch (out_dtype) {
 #define RQ_EXPAND(DT)                                                                                              \
-    hipLaunchKernelGGL(expand_kernel<DT>, dim3((unsigned)num_blocks), dim3(256), 0, st, kv_cache, block_size,      \
+    hipLaunchKernelGGL(expand_kernel<DT>, dim3((unsigned)num_blocks), dim3(ethreads), 0, st, kv_cache, block_size, \
                        stride_block, stride_token, num_kv_heads, head_dim, flag, compact, capacity_blocks,         \
                        k_centroids, n_k_centroids, v_centroids, n_v_centroids, out_k, out_v)
                 case RQ_DTYPE_F16: RQ_EXPAND(RQ_DTYPE_F16); break;
