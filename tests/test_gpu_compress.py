@@ -118,21 +118,23 @@ def test_compress_store_strided_qkv_views():
     assert np.array_equal(cache.cpu().numpy(), ref)
 
 
-def test_paged_decompress_matches_unique_gather():
-    """Paged decompress == sorted-unique gather + per-row decompress + remap (rq_backend.py:763-852)."""
+@pytest.mark.parametrize("H,D", [(8, 128), (3, 80)])
+def test_paged_decompress_matches_unique_gather(H, D):
+    """Paged decompress == sorted-unique gather + per-row decompress + remap (rq_backend.py:763-852).
+    (3, 80): 10 packed dwords per row (a 250-thread expand block) and rows of 3 heads."""
     K = _kernels()
-    p = Params("iso", 3, 3)
-    H, BS = 8, 16
+    p = Params("iso", 3, 3) if D == 128 else Params("planar", 3, 3, head_dim=D)
+    BS = 16
     lens = [37, 1, 160, 64, 0]
     bt, NB, slots = paged_layout(lens, BS, cfg=4)
     bt[2, 3] = bt[0, 1]  # a block shared by two sequences
     slots_all = np.concatenate(slots)
     total = len(slots_all)
-    k, v = kv_config0(total, H, 128, cfg=4)
+    k, v = kv_config0(total, H, D, cfg=4)
     cache = build_cache_oracle(k, v, slots_all, NB, BS, p)
-    kc_ref, vc_ref, bt_ref, U = O.paged_decompress(cache, bt, lens, H, 128, p.kc.numpy(), p.vc.numpy(), "bfloat16")
+    kc_ref, vc_ref, bt_ref, U = O.paged_decompress(cache, bt, lens, H, D, p.kc.numpy(), p.vc.numpy(), "bfloat16")
     ok, ov, remap, count = K.paged_decompress(_dev(torch.from_numpy(cache)), _dev(torch.from_numpy(bt)),
-                                              _dev(torch.tensor(lens, dtype=torch.int32)), H, 128, _dev(p.kc),
+                                              _dev(torch.tensor(lens, dtype=torch.int32)), H, D, _dev(p.kc),
                                               _dev(p.vc), torch.bfloat16)
     assert int(count.item()) == U
     assert np.array_equal(remap.cpu().numpy(), bt_ref)
