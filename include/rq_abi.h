@@ -164,7 +164,7 @@ int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, int32_t blo
  * must be an integer <= 16; n_k_centroids / n_v_centroids 8 or 16; centroids
  * and rotation 16-byte aligned.
  * max_seq_len bounds every seq_lens entry (it sizes the work and workspace).
- * workspace: at least rq_fused_decode_workspace_bytes(...) bytes of device
+ * workspace: at least rq_fused_decode_workspace_bytes(...) bytes (16-byte aligned) of device
  * scratch (split partials, query operands, tile descriptors); no
  * initialisation is needed and every call rewrites what it reads, so one
  * workspace serves any number of calls (calls sharing one workspace must not

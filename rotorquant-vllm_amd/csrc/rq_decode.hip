@@ -1001,6 +1001,7 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
     if (num_seqs == 0) return RQ_OK;
     RQ_CHECK_ARG(workspace_bytes >= rq_fused_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_seq_len),
                  "workspace too small");
+    RQ_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     DecodeArgs a{};
     a.q = q;
