@@ -786,16 +786,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     end_segment();
 }
 
-// Segments per merge pass: lane c < kMergePass loads segment c's (m, l), and every
-// lane loads its two dims of all of them before any is used (one round trip per pass).
-constexpr int kMergePass = 32;
+// Segments per merge pass (PASS = 16 or 32): lane c < PASS loads segment c's (m, l),
+// and every lane loads its two dims of all of them before any is used (one load
+// round per pass).  32 halves the rounds of long sequences; 16 needs ~65 fewer
+// VGPRs, so more merge waves are resident at once.
 
 // Merge the partials of (seq, query head): log-sum-exp over the segments, round
 // to the query dtype (the reference's out_rot, fused_paged_rq_decode.py:201-206),
 // rotate back by R in fp32 and round again (:308).  One wave per query head,
 // two head dims per lane; per pass of kMergePass segments, the (m, l) of each segment
 // and the lane's accumulator entries of all of them are loaded together.
-template <int DT>
+template <int DT, int kMergePass>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1078,7 +1079,16 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
         if (rc) return rc;
     }
     dim3 mgrid((num_q_heads + 3) / 4, (unsigned)num_seqs);
-    if (dtype == RQ_DTYPE_BF16) hipLaunchKernelGGL(decode_merge_kernel<RQ_DTYPE_BF16>, mgrid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(decode_merge_kernel<RQ_DTYPE_F16>, mgrid, dim3(256), 0, st, a);
+    // 32-segment passes when a sequence may span many decode workgroups (very long
+    // contexts), or when all merge waves fit at once at the lower occupancy
+    // (3 per SIMD); otherwise 16 (config 2: 8192 short merges).
+    const bool wide = a.max_len >= 65536 || num_seqs * (int64_t)num_q_heads <= 12LL * device_cus();
+    if (dtype == RQ_DTYPE_BF16) {
+        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 32>), mgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 16>), mgrid, dim3(256), 0, st, a);
+    } else {
+        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 32>), mgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 16>), mgrid, dim3(256), 0, st, a);
+    }
     return check_launch("decode_merge_kernel");
 }

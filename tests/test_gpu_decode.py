@@ -65,6 +65,13 @@ def test_decode_config1_shape_small_batch(dtype):
     check(decode_case(1, 8, 8, 32, lens, dtype=dtype), f"cfg1-small {dtype}")
 
 
+def test_decode_many_short_sequences():
+    """112 sequences x 32 query heads (more merge waves than fit at once at the wide
+    merge's occupancy): the merge runs its 16-segment variant."""
+    lens = lens_uniform(112, 1, 300, cfg=12)
+    check(decode_case(12, len(lens), 8, 32, lens), "many-short")
+
+
 def test_decode_ragged_edges():
     """Lengths 0, 1, 15, 16, 17, 31, 33, 255, 256, 257, 1000 (tile / block / chunk edges)."""
     lens = [0, 1, 15, 16, 17, 31, 33, 255, 256, 257, 1000]
