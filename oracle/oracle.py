@@ -24,9 +24,14 @@ Pins (what each function is checked against, besides the product):
     boundaries but the middle one bit-equal), Max's 1960 table for 3 bits.
   layout: the reference's KAT (tests/test_vllm_integration.py:44-62).
   paged_decompress: closed form (sorted unique + per-row decompress).
-  decode/prefill attention: closed forms (L = 1 -> V row, identical keys ->
-    mean of V, zero context -> zeros) and a float64 softmax written
-    independently in the tests.
+  decode/prefill attention (tests/test_oracle_attention.py): torch's
+    scaled_dot_product_attention in float64 over K/V dequantized by torch
+    (GQA by repeat_interleave, explicit L - T + i causal mask); closed forms
+    (zero context -> zeros, L = 1 -> V row, identical keys -> mean of V, two
+    keys -> logistic weight of sm_scale * (s1 - s0)); prefill rows equal
+    decode over the visible prefix; the q / out roundings against torch's
+    own casts.  Mistakes planted through _kv_head, _visible and _scores
+    (GQA map, mask offset, missing scale) fail these checks.
 """
 from __future__ import annotations
 
@@ -65,6 +70,9 @@ def lib():
                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         L.rqo_row_norm.restype = ctypes.c_float
         L.rqo_row_norm.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.rqo_block_rotate.restype = None
+        L.rqo_block_rotate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -249,70 +257,142 @@ def paged_decompress(cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb,
 def gather_seq(cache, block_table_row, L, num_kv_heads, head_dim, k_cb, v_cb):
     """K, V (L, H, D) fp64 dequantized (centroid * norm in fp32) for one sequence."""
     NB, BS, TB = cache.shape
-    pos = np.arange(L)
-    phys = np.asarray(block_table_row)[pos // BS]
-    slots = cache[phys, pos % BS]  # (L, TB)
-    kp, kn, vp, vn = read_slots(slots.reshape(L, 1, TB), num_kv_heads, head_dim)
+    nblk = (L + BS - 1) // BS
+    pay = slot_layout(num_kv_heads, head_dim)["v_norm_end"]  # payload bytes (the padding is never read)
+    phys = np.asarray(block_table_row)[:nblk]
+    slots = cache[phys, :, :pay].reshape(nblk * BS, pay)[:L]  # whole blocks, then the first L slots
+    kp, kn, vp, vn = read_slots(slots.reshape(L, 1, pay), num_kv_heads, head_dim)
     K = decompress_f32(kp, kn, k_cb).astype(np.float64)
     V = decompress_f32(vp, vn, v_cb).astype(np.float64)
     return K, V
 
 
+def block_width(R: np.ndarray) -> int:
+    """Smallest width in (2, 4, 8, ..., D) for which R is block diagonal."""
+    D = R.shape[0]
+    idx = np.arange(D)
+    blk = 2
+    while blk < D:
+        off = (idx[:, None] // blk) != (idx[None, :] // blk)
+        if not np.any(R[off] != 0):
+            return blk
+        blk *= 2
+    return D
+
+
+def _block_rotate(x: np.ndarray, R: np.ndarray, transpose: bool) -> np.ndarray:
+    """x @ R^T (transpose) or x @ R in fp32 with torch's CPU rounding order (rq_oracle.c)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    Rc = np.ascontiguousarray(R, dtype=np.float32)
+    D = Rc.shape[0]
+    rows = x.size // D
+    out = np.zeros((rows, D), np.float32)
+    sk, sj = (1, D) if transpose else (D, 1)
+    lib().rqo_block_rotate(_ptr(x), rows, D, _ptr(Rc), sk, sj, block_width(Rc), _ptr(out))
+    return out.reshape(x.shape)
+
+
 def rotate_q(q_f32: np.ndarray, R: np.ndarray, dtype: str) -> np.ndarray:
-    """q_rot = (q.float() @ R^T).to(dtype) (fused_paged_rq_decode.py:271)."""
-    return round_to((q_f32.astype(np.float64) @ R.astype(np.float64).T).astype(np.float32), dtype)
+    """q_rot = (q.float() @ R^T).to(dtype) (fused_paged_rq_decode.py:271), fp32 product in
+    torch's CPU order."""
+    return round_to(_block_rotate(q_f32, R, True), dtype)
 
 
 def unrotate_out(out_rot: np.ndarray, R: np.ndarray, dtype: str) -> np.ndarray:
     """out = (out_rot.to(dtype).float() @ R).to(dtype) (fused_paged_rq_decode.py:201-206, :308)."""
-    o = round_to(out_rot.astype(np.float32), dtype).astype(np.float64)
-    return round_to((o @ R.astype(np.float64)).astype(np.float32), dtype)
+    o = round_to(np.asarray(out_rot, np.float64).astype(np.float32), dtype)
+    return round_to(_block_rotate(o, R, False), dtype)
+
+
+def _kv_head(h: int, G: int, H: int) -> int:
+    """KV head read by query head h (fused_paged_rq_decode.py:78: h // (H_Q / H_KV))."""
+    return h // G
+
+
+def _visible(pos_q: np.ndarray, L: int) -> np.ndarray:
+    """(T, L) mask: key j is visible to a query at position p iff j <= p
+    (fused_paged_rq_int8_prefill.py:187-189, with p = L - T + i)."""
+    return np.arange(L)[None, :] <= np.asarray(pos_q)[:, None]
+
+
+def _scores(qr: np.ndarray, K: np.ndarray, sm_scale: float) -> np.ndarray:
+    """Scaled scores q . k * sm_scale (fused_paged_rq_decode.py:150-154 without the log2e
+    change of base, which cancels in the softmax)."""
+    return (qr @ K.T) * sm_scale
+
+
+def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype):
+    """Rotated-space decode output in float64, before the output rounding:
+    (B, HQ, D).  q: (B, HQ, D) fp32 values of the dtype-rounded query."""
+    B, HQ, D = q.shape
+    G = HQ // num_kv_heads
+    out = np.zeros((B, HQ, D))
+    for b in range(B):
+        L = int(seq_lens[b])
+        if L == 0:
+            continue  # empty context -> zeros (the reference: acc 0, l 1)
+        qr = rotate_q(q[b], R, dtype).astype(np.float64)  # (HQ, D)
+        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
+        kv_of = np.array([_kv_head(h, G, num_kv_heads) for h in range(HQ)])
+        for kvh in range(num_kv_heads):
+            heads = np.nonzero(kv_of == kvh)[0]
+            if heads.size == 0:
+                continue
+            S = _scores(qr[heads], np.ascontiguousarray(K[:, kvh, :]), sm_scale)  # (heads, L)
+            P = np.exp(S - S.max(axis=1, keepdims=True))
+            out[b, heads] = (P @ np.ascontiguousarray(V[:, kvh, :])) / P.sum(axis=1, keepdims=True)
+    return out
 
 
 def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype):
     """q: (B, HQ, D) fp32 values of the dtype-rounded query.  Returns (B, HQ, D) fp32 values."""
-    B, HQ, D = q.shape
-    G = HQ // num_kv_heads
-    out = np.zeros((B, HQ, D), np.float32)
-    for b in range(B):
-        L = int(seq_lens[b])
-        qr = rotate_q(q[b], R, dtype).astype(np.float64)  # (HQ, D)
-        if L == 0:
-            o_rot = np.zeros((HQ, D))
-        else:
-            K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
-            o_rot = np.zeros((HQ, D))
-            for h in range(HQ):
-                kvh = h // G
-                s = (K[:, kvh, :] @ qr[h]) * sm_scale
-                p = np.exp(s - s.max())
-                o_rot[h] = (p @ V[:, kvh, :]) / p.sum()
-        out[b] = unrotate_out(o_rot, R, dtype)
-    return out
+    o_rot = decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale,
+                                 dtype)
+    B, HQ, D = o_rot.shape
+    return unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(B, HQ, D)
 
 
-def prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
-                      sm_scale, dtype):
-    """Causal attention; query i of sequence b sits at position seq_lens[b] - q_len_b + i."""
+def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
+                          sm_scale, dtype, rows=None):
+    """Rotated-space causal prefill output in float64, before the output rounding: (T, HQ, D).
+
+    Query i of sequence b sits at position seq_lens[b] - q_len_b + i.  rows
+    (optional, sorted global query rows) restricts the work to those rows;
+    the others stay zero."""
     T, HQ, D = q.shape
     G = HQ // num_kv_heads
-    out = np.zeros((T, HQ, D), np.float32)
+    out = np.zeros((T, HQ, D))
+    want = None if rows is None else np.asarray(rows)
     for b in range(len(seq_lens)):
         s0, s1 = int(cu_seqlens[b]), int(cu_seqlens[b + 1])
         L = int(seq_lens[b])
         T_b = s1 - s0
         if T_b == 0:
             continue
+        local = np.arange(T_b) if want is None else want[(want >= s0) & (want < s1)] - s0
+        if local.size == 0 or L == 0:
+            continue
         K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
-        qr = rotate_q(q[s0:s1].reshape(-1, D), R, dtype).reshape(T_b, HQ, D).astype(np.float64)
-        pos = L - T_b + np.arange(T_b)
-        o_rot = np.zeros((T_b, HQ, D))
+        qr = rotate_q(q[s0 + local].reshape(-1, D), R, dtype).reshape(local.size, HQ, D).astype(np.float64)
+        vis = _visible(L - T_b + local, L)
+        Kc = [np.ascontiguousarray(K[:, j, :]) for j in range(num_kv_heads)]
+        Vc = [np.ascontiguousarray(V[:, j, :]) for j in range(num_kv_heads)]
         for h in range(HQ):
-            kvh = h // G
-            S = (qr[:, h, :] @ K[:, kvh, :].T) * sm_scale  # (T_b, L)
-            S[np.arange(L)[None, :] > pos[:, None]] = -np.inf
-            S -= S.max(axis=1, keepdims=True)
-            P = np.exp(S)
-            o_rot[:, h, :] = (P @ V[:, kvh, :]) / P.sum(axis=1, keepdims=True)
-        out[s0:s1] = unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(T_b, HQ, D)
+            kvh = _kv_head(h, G, num_kv_heads)
+            S = _scores(qr[:, h, :], Kc[kvh], sm_scale)  # (rows, L)
+            S = np.where(vis, S, -np.inf)
+            with np.errstate(invalid="ignore"):  # a row with no visible key (only a wrong mask) gives NaN
+                S -= S.max(axis=1, keepdims=True)
+                P = np.exp(S)
+                out[s0 + local, h, :] = (P @ Vc[kvh]) / P.sum(axis=1, keepdims=True)
     return out
+
+
+def prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
+                      sm_scale, dtype, rows=None):
+    """Causal attention; query i of sequence b sits at position seq_lens[b] - q_len_b + i.
+    Returns (T, HQ, D) fp32 values (rows outside `rows`, when given, are zero)."""
+    o_rot = prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb,
+                                  R, sm_scale, dtype, rows)
+    T, HQ, D = o_rot.shape
+    return unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(T, HQ, D)

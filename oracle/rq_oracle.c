@@ -145,3 +145,25 @@ void rqo_decompress(const uint8_t *packed, const float *norms, int64_t n_rows, i
         }
     }
 }
+
+/*
+ * Block-diagonal fp32 product out[r][j] = sum_k x[r][k] * M(k, j) over the
+ * diagonal block of width blk that holds j, M(k, j) = M[k * sk + j * sj]:
+ * the first product, then an fma chain in increasing k -- the order torch's
+ * CPU fp32 matmul (MKL sgemm, M >= 2 rows) gives a block-diagonal operand
+ * (entries outside the block are exact zeros and leave the sum unchanged).
+ * Used for q_rot = q.float() @ R^T (sk = 1, sj = D; fused_paged_rq_decode.py:271)
+ * and out = out_rot.float() @ R (sk = D, sj = 1; :308).
+ */
+void rqo_block_rotate(const float *x, int64_t rows, int D, const float *M, int64_t sk, int64_t sj, int blk,
+                      float *out) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * D;
+        for (int j = 0; j < D; ++j) {
+            const int k0 = (j / blk) * blk;
+            float acc = xr[k0] * M[k0 * sk + j * sj];
+            for (int i = 1; i < blk; ++i) acc = fmaf(xr[k0 + i], M[(k0 + i) * sk + j * sj], acc);
+            out[r * D + j] = acc;
+        }
+    }
+}

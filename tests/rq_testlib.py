@@ -12,78 +12,9 @@ import numpy as np
 import torch
 
 import oracle as O
-from rotorquant_vllm.quantization import IsoQuantMSE, PlanarQuantMSE
-from rotorquant_vllm.vllm.rq_backend import _build_rotation_matrix, _rq_total_bytes
-
-
-class Params:
-    """Codebooks and rotation of one RQ configuration (CPU, fp32)."""
-
-    def __init__(self, mode="iso", k_bits=3, v_bits=3, iso_mode="fast", head_dim=128):
-        if mode == "iso":
-            kq = IsoQuantMSE(head_dim, k_bits, seed=42, mode=iso_mode)
-            vq = kq if v_bits == k_bits else IsoQuantMSE(head_dim, v_bits, seed=42, mode=iso_mode)
-        else:
-            kq = PlanarQuantMSE(head_dim, k_bits, seed=42)
-            vq = kq if v_bits == k_bits else PlanarQuantMSE(head_dim, v_bits, seed=42)
-        self.mode, self.k_bits, self.v_bits, self.D = mode, k_bits, v_bits, head_dim
-        self.kc, self.kb = kq.centroids.clone(), kq.boundaries.clone()
-        self.vc, self.vb = vq.centroids.clone(), vq.boundaries.clone()
-        self.R = _build_rotation_matrix(kq, head_dim, "cpu")
-        RT = self.R.T.contiguous()
-        self.rte, self.rto = RT[:, 0::2].contiguous(), RT[:, 1::2].contiguous()
-        self.blk = 4 if mode == "iso" else 2
-
-    def np(self):
-        return dict(kc=self.kc.numpy(), vc=self.vc.numpy(), kb=self.kb.numpy(), vb=self.vb.numpy(),
-                    R=self.R.numpy(), rte=self.rte.numpy(), rto=self.rto.numpy())
-
-
-def gen(seed):
-    return torch.Generator().manual_seed(seed)
-
-
-def kv_config0(n_tokens, H, D, cfg=0, dtype=torch.float16):
-    """N(0,1) * (1 + |N(0, 3)|) per (head, channel) for K and V."""
-    out = []
-    for stream in (0, 1):
-        scale = 1 + (torch.randn(H, D, generator=gen(1000 * cfg + 2 + stream)) * 3).abs()
-        out.append((torch.randn(n_tokens, H, D, generator=gen(1000 * cfg + stream)) * scale).to(dtype))
-    return out
-
-
-def kv_outlier_k(n_tokens, H, D, cfg, dtype=torch.float16, n_out=4, factor=10.0):
-    """K N(0,1) with n_out seeded outlier channels per head scaled by `factor`; V N(0,1)."""
-    k = torch.randn(n_tokens, H, D, generator=gen(1000 * cfg))
-    g = gen(1000 * cfg + 2)
-    for h in range(H):
-        ch = torch.randperm(D, generator=g)[:n_out]
-        k[:, h, ch] *= factor
-    v = torch.randn(n_tokens, H, D, generator=gen(1000 * cfg + 1))
-    return k.to(dtype), v.to(dtype)
-
-
-def paged_layout(seq_lens, block_size, cfg, extra_blocks=8):
-    """Seeded random physical block assignment.
-
-    Returns (block_table (B, max_blocks) int32, num_blocks, slot ids per
-    sequence as a list of int64 arrays).  Unused table entries are 0.
-    """
-    seq_lens = [int(x) for x in seq_lens]
-    nblk = [(L + block_size - 1) // block_size for L in seq_lens]
-    total = sum(nblk)
-    num_blocks = total + extra_blocks
-    perm = torch.randperm(num_blocks, generator=gen(1000 * cfg + 5)).numpy().astype(np.int32)
-    max_blocks = max(max(nblk), 1)
-    bt = np.zeros((len(seq_lens), max_blocks), np.int32)
-    slots = []
-    o = 0
-    for b, L in enumerate(seq_lens):
-        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
-        o += nblk[b]
-        pos = np.arange(L)
-        slots.append(bt[b, pos // block_size].astype(np.int64) * block_size + pos % block_size)
-    return bt, num_blocks, slots
+from rotorquant_vllm.vllm.rq_backend import _rq_total_bytes
+from rq_inputs import (Params, gen, gpu_decode_inputs, gpu_prefill_inputs, host_subcache,  # noqa: F401
+                       kv_config0, kv_outlier_k, kv_unit, lens_loguniform, lens_uniform, paged_layout)
 
 
 def build_cache_oracle(k, v, slot_ids, num_blocks, block_size, p: Params):
@@ -98,12 +29,6 @@ def build_cache_oracle(k, v, slot_ids, num_blocks, block_size, p: Params):
     cache = np.zeros((num_blocks, block_size, _rq_total_bytes(D, H)), np.uint8)
     O.compress_store(cache, slot_ids, kp, kn, vp, vn)
     return cache
-
-
-def kv_unit(n_tokens, H, D, cfg, dtype=torch.float16):
-    """K, V ~ N(0, 1) (no channel scaling): attention outputs stay within a few units."""
-    return (torch.randn(n_tokens, H, D, generator=gen(1000 * cfg)).to(dtype),
-            torch.randn(n_tokens, H, D, generator=gen(1000 * cfg + 1)).to(dtype))
 
 
 def decode_case(cfg, B, H, HQ, lens, block_size=16, p: Params | None = None, kv="config0", dtype=torch.bfloat16):
@@ -121,6 +46,19 @@ def decode_case(cfg, B, H, HQ, lens, block_size=16, p: Params | None = None, kv=
     q = torch.randn(B, HQ, p.D, generator=gen(1000 * cfg + 6)).to(dtype)
     return dict(cache=cache, bt=bt, lens=np.asarray(lens, np.int32), q=q, p=p, H=H, HQ=HQ, BS=block_size,
                 sm_scale=1.0 / math.sqrt(p.D))
+
+
+def identical_keys_case(cfg=45, L=333, H=2, HQ=8, p=None):
+    """A one-sequence decode case whose cached keys are all the same vector (per kv head); V varies.
+    Every query head then weighs all keys equally: the output is the mean of V."""
+    p = p or Params("iso", 3, 3)
+    bt, NB, slots = paged_layout([L], 16, cfg)
+    k, v = kv_config0(L, H, 128, cfg)
+    k[:] = k[0:1]
+    cache = build_cache_oracle(k, v, slots[0], NB, 16, p)
+    q = torch.randn(1, HQ, 128, generator=gen(1000 * cfg + 6)).to(torch.bfloat16)
+    return dict(p=p, cache=cache, bt=bt, lens=np.asarray([L], np.int32), q=q, H=H, HQ=HQ, BS=16,
+                sm_scale=1 / math.sqrt(128))
 
 
 def ulp(x: np.ndarray, dtype: str) -> np.ndarray:
@@ -166,11 +104,3 @@ def cos_sim(a: np.ndarray, b: np.ndarray) -> float:
         return 1.0
     return float(a @ b / (na * nb))
 
-
-def lens_uniform(B, lo, hi, cfg):
-    return torch.randint(lo, hi + 1, (B,), generator=gen(1000 * cfg + 4)).tolist()
-
-
-def lens_loguniform(B, lo, hi, cfg):
-    u = torch.rand(B, generator=gen(1000 * cfg + 4), dtype=torch.float64)
-    return [int(math.floor(math.exp(math.log(lo) + x * (math.log(hi) - math.log(lo))))) for x in u.tolist()]

@@ -1,0 +1,128 @@
+"""GPU parity at the benchmark configurations' full sizes.
+
+Each case builds its cache on the device with the library's compress kernel
+(bit-exact against the oracle in test_gpu_compress.py, up to 32768 tokens),
+runs the kernel on the whole configuration, copies back the blocks the checked
+sequences reference and compares with the float64 oracle over those bytes.
+Tolerance as in the other parity tests: cos >= 0.999 and |got - ref| <=
+max(2e-2, ulp(x) + 2 ulp(rotation-block max)) (rq_testlib.check_tolerance);
+each case also prints its max-abs, the number of elements above the flat
+2e-2 and the worst excess in bf16 ulps of the output.
+
+Where the oracle would take minutes, a seeded subset is checked and stated:
+config 2 checks 32 of its 256 sequences, config 4's decode part the
+131072-token sequence and 31 of its 127 companions, config 3 and config 4's
+chunks every 32nd query row plus the last 32 of each sequence.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from rq_testlib import (check_tolerance, gpu_decode_inputs, gpu_prefill_inputs, host_subcache, lens_loguniform,
+                        lens_uniform, ulp)
+
+pytestmark = pytest.mark.gpu
+
+
+def _report(tag, got, ref, dtype, blk):
+    err, excess, cs = check_tolerance(got, ref, dtype, rot_block=blk)
+    over = int((np.abs(got.astype(np.float64) - ref) > 2e-2).sum())
+    ulps = float((np.abs(got.astype(np.float64) - ref) / ulp(np.maximum(np.abs(got), np.abs(ref)), dtype)).max())
+    print(f"{tag}: n={got.size} max_abs={err:.3e} above_2e-2={over} worst={ulps:.1f} ulp "
+          f"excess_over_bound={excess:.3e} cos={cs:.7f}", flush=True)
+    assert np.isfinite(got).all()
+    assert excess <= 0 and cs >= 0.999, tag
+
+
+def _decode_check(tag, inp, check_seqs):
+    from rotorquant_vllm import kernels as K
+    p, dev = inp["p"], inp["q"].device
+    lens = inp["lens_host"]
+    print(f"{tag}: B={len(lens)} sum_L={sum(lens)} checking {len(check_seqs)} sequences", flush=True)
+    out = K.fused_paged_rq_decode(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], p.kc.to(dev), p.vc.to(dev),
+                                  p.R.to(dev), inp["H"], 128, 16, max_seq_len=max(lens))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()[check_seqs]
+    sub, bt, sl = host_subcache(inp["caches"][0], inp["bt_host"], lens, check_seqs)
+    pn = p.np()
+    ref = O.decode_attention(inp["q"].float().cpu().numpy()[check_seqs], sub, bt, sl, inp["H"], 128, pn["kc"],
+                             pn["vc"], pn["R"], 1 / math.sqrt(128), "bfloat16")
+    _report(tag, got, ref, "bfloat16", p.blk)
+
+
+def test_config1_full_batch():
+    """Config 1: 64 sequences, L ~ U[1024, 8192], 32 q / 8 kv heads, iso fast 3-bit; all checked."""
+    lens = lens_uniform(64, 1024, 8192, 1)
+    inp = gpu_decode_inputs(lens, copies=1)
+    _decode_check("config1 B=64", inp, list(range(64)))
+
+
+def test_config2_full_batch_seeded_subset():
+    """Config 2: 256 sequences, L log-uniform [2048, 32768], planar K4/V3, K outlier channels;
+    the whole batch decodes in one call, a seeded 32 of the 256 are checked."""
+    lens = lens_loguniform(256, 2048, 32768, 2)
+    inp = gpu_decode_inputs(lens, cfg=2, mode="planar", k_bits=4, v_bits=3, copies=1, kv="outlier")
+    seqs = sorted(torch.randperm(256, generator=torch.Generator().manual_seed(2007))[:32].tolist())
+    _decode_check("config2 B=256 (32 checked)", inp, seqs)
+    del inp
+    torch.cuda.empty_cache()
+
+
+def test_config4_decode_part():
+    """Config 4's decode part: 1 x 131072 + 127 x U[512, 16384] tokens, 28 q / 4 kv heads
+    (GQA 7), iso full 3-bit, bf16 K/V.  The 131072-token sequence (the only input that
+    takes the widest prep grid and the long-context merge passes) and a seeded 31 of the
+    others are checked."""
+    lens = [131072] + torch.randint(512, 16384 + 1, (127,), generator=torch.Generator().manual_seed(4004)).tolist()
+    inp = gpu_decode_inputs(lens, H=4, HQ=28, cfg=4, mode="iso", iso_mode="full", copies=1, kv="kscale",
+                            kv_dtype="bfloat16")
+    others = sorted(1 + torch.randperm(127, generator=torch.Generator().manual_seed(4008))[:31].numpy())
+    _decode_check("config4 decode B=128 (long + 31 checked)", inp, [0] + [int(x) for x in others])
+    del inp
+    torch.cuda.empty_cache()
+
+
+def _prefill_check(tag, inp, rows_of):
+    from rotorquant_vllm import kernels as K
+    p, dev = inp["p"], inp["q"].device
+    lens, q_lens = inp["lens_host"], inp["q_lens"]
+    print(f"{tag}: seqs={len(lens)} q_tokens={sum(q_lens)} ctx={lens}", flush=True)
+    out = K.fused_paged_rq_int8_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], p.kc.to(dev),
+                                        p.vc.to(dev), p.R.to(dev), inp["H"], 128, 16, cu_seqlens_q=inp["cu"],
+                                        max_q_len=max(q_lens), max_seq_len=max(lens))
+    torch.cuda.synchronize()
+    cu = inp["cu"].cpu().numpy()
+    rows = np.concatenate([cu[b] + rows_of(q_lens[b]) for b in range(len(lens))])
+    sub, bt, sl = host_subcache(inp["caches"][0], inp["bt_host"], lens, list(range(len(lens))))
+    pn = p.np()
+    ref = O.prefill_attention(inp["q"].float().cpu().numpy(), cu, sub, bt, sl, inp["H"], 128, pn["kc"], pn["vc"],
+                              pn["R"], 1 / math.sqrt(128), "bfloat16", rows=rows)
+    _report(tag, out.float().cpu().numpy()[rows], ref[rows], "bfloat16", p.blk)
+
+
+def _sampled_rows(T):
+    return np.unique(np.concatenate([np.arange(0, T, 32), np.arange(max(0, T - 32), T)]))
+
+
+def test_config3_full_size():
+    """Config 3: 8 fresh sequences x 4096 tokens, causal, 32 q / 8 kv, iso fast 4-bit, one launch."""
+    q_lens = [4096] * 8
+    inp = gpu_prefill_inputs(q_lens, q_lens, 8, 32, 3, "iso", 4)
+    _prefill_check("config3 8x4096", inp, _sampled_rows)
+    del inp
+    torch.cuda.empty_cache()
+
+
+def test_config4_chunks_after_prefixes():
+    """Config 4's prefill part: 4 chunks of 2048 tokens after seeded prefixes U{0..14336},
+    28 q / 4 kv heads, iso full 3-bit, one launch."""
+    pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
+    q_lens = [2048] * 4
+    ctx = [x + 2048 for x in pre]
+    inp = gpu_prefill_inputs(q_lens, ctx, 4, 28, 4, "iso", 3, iso_mode="full")
+    _prefill_check(f"config4 chunks prefixes={pre}", inp, _sampled_rows)
+    del inp
+    torch.cuda.empty_cache()

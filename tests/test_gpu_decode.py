@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle as O
-from rq_testlib import Params, check_tolerance, decode_case, lens_loguniform, lens_uniform
+from rq_testlib import Params, check_tolerance, decode_case, identical_keys_case, lens_loguniform, lens_uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -99,7 +99,9 @@ def test_decode_k3_v4_and_block_size_32():
 
 
 def test_decode_closed_forms():
-    """L = 1 -> output = R^T-rotated V row; identical keys -> mean of V (closed forms, no oracle)."""
+    """Closed forms, no attention oracle: L = 1 -> the R-rotated V row; identical keys
+    (every cached key the same vector) -> the R-rotated mean of V, at 8 kv heads x GQA 4
+    and at GQA 7 over 2000 tokens (many tiles, several decode workgroups)."""
     case = decode_case(6, 2, 8, 32, [1, 1])
     got = run_decode(case)
     p = case["p"]
@@ -110,6 +112,18 @@ def test_decode_closed_forms():
             exp = O.unrotate_out(V[0, h // 4][None, :], p.R.numpy(), dt)[0]
             _, excess, cs = check_tolerance(got[b, h], exp, dt, 1e-2, rot_block=p.blk)
             assert excess <= 0 and cs >= 0.9999
+    for L, H, HQ, mode in ((333, 8, 32, "fast"), (2000, 4, 28, "full")):
+        case = identical_keys_case(cfg=45, L=L, H=H, HQ=HQ, p=Params("iso", 3, 3, iso_mode=mode))
+        got = run_decode(case)
+        p = case["p"]
+        K, V = O.gather_seq(case["cache"], case["bt"][0], L, H, 128, p.kc.numpy(), p.vc.numpy())
+        assert np.all(K == K[0:1]), "the case must hold identical keys"
+        mean = V.mean(axis=0)  # (H, D), float64
+        G = HQ // H
+        exp = O.unrotate_out(np.stack([mean[h // G] for h in range(HQ)]), p.R.numpy(), dt)
+        err, excess, cs = check_tolerance(got[0], exp, dt, rot_block=p.blk)
+        print(f"identical keys L={L} H={H} HQ={HQ}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
+        assert excess <= 0 and cs >= 0.9999
 
 
 def test_decode_deterministic_and_batch_consistent():
