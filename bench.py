@@ -46,54 +46,13 @@ def cpu_model() -> str:
     return platform.processor()
 
 
+from rq_inputs import gpu_decode_inputs as build_decode_inputs  # noqa: E402  (seeded device inputs)
+from rq_inputs import gpu_prefill_inputs as prefill_inputs  # noqa: E402
+
+
 def config1_lens(B=64, cfg=1):
     import torch
     return torch.randint(1024, 8192 + 1, (B,), generator=torch.Generator().manual_seed(1000 * cfg + 4)).tolist()
-
-
-def build_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=3, v_bits=3, iso_mode="fast",
-                        copies=3, kv="config0", kv_dtype="float16"):
-    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store.
-
-    kv: "config0" K and V N(0,1) * (1 + |N(0,3)|) per (head, channel); "kscale"
-    only K scaled that way, V N(0,1); "outlier" K N(0,1) with 4 seeded channels
-    per head at 10x, V N(0,1)."""
-    import numpy as np
-    import torch
-
-    from rotorquant_vllm import kernels as K
-    from rq_testlib import Params, paged_layout
-
-    dev = torch.device("cuda")
-    p = Params(mode, k_bits, v_bits, iso_mode=iso_mode, head_dim=D)
-    bt, NB, slots = paged_layout(lens, BS, cfg)
-    total_bytes = 256 * H
-    cache = torch.zeros(NB, BS, total_bytes, dtype=torch.uint8, device=dev)
-    slot_all = torch.from_numpy(np.concatenate(slots)).to(dev)
-    g = torch.Generator(device=dev).manual_seed(1000 * cfg)
-    gs = torch.Generator(device=dev).manual_seed(1000 * cfg + 2)
-    k_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
-    v_scale = 1 + (torch.randn(H, D, generator=gs, device=dev) * 3).abs()
-    if kv != "config0":
-        v_scale = torch.ones(H, D, device=dev)
-    if kv == "outlier":
-        k_scale = torch.ones(H, D, device=dev)
-        go = torch.Generator().manual_seed(1000 * cfg + 2)
-        for h in range(H):
-            k_scale[h, torch.randperm(D, generator=go)[:4].to(dev)] = 10.0
-    kdt = getattr(torch, kv_dtype)
-    rte, rto, kb, vb = (t.to(dev) for t in (p.rte, p.rto, p.kb, p.vb))
-    chunk = 32768
-    for s in range(0, slot_all.numel(), chunk):
-        n = min(chunk, slot_all.numel() - s)
-        k = (torch.randn(n, H, D, generator=g, device=dev) * k_scale).to(kdt)
-        v = (torch.randn(n, H, D, generator=g, device=dev) * v_scale).to(kdt)
-        K.compress_store(k, v, cache, slot_all[s:s + n], rte, rto, kb, vb, rot_block=p.blk)
-    caches = [cache] + [cache.clone() for _ in range(copies - 1)]
-    q = torch.randn(len(lens), HQ, D, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
-                    device=dev).to(torch.bfloat16)
-    return dict(p=p, caches=caches, bt=torch.from_numpy(bt).to(dev), lens=torch.tensor(lens, dtype=torch.int32,
-                device=dev), q=q, H=H, HQ=HQ, D=D, BS=BS, lens_host=list(lens), bt_host=bt, NB=NB)
 
 
 def decode_bytes(lens, H, HQ, D, BS):
@@ -207,7 +166,7 @@ def decode_config(cfg, steps=10):
     or the decode part of config 4 (Qwen2.5-7B layout, iso full 3-bit, 1 x 131072 + 127 x U[512, 16384])."""
     import torch
 
-    from rq_testlib import lens_loguniform
+    from rq_inputs import lens_loguniform
     if cfg == 2:
         lens = lens_loguniform(256, 2048, 32768, 2)
         inp = build_decode_inputs(lens, cfg=2, mode="planar", k_bits=4, v_bits=3, copies=1, kv="outlier")
@@ -225,21 +184,6 @@ def decode_config(cfg, steps=10):
     del inp
     torch.cuda.empty_cache()
     return out
-
-
-def prefill_inputs(q_lens, ctx_lens, H, HQ, cfg, mode, bits, iso_mode="fast"):
-    """Cache holding every sequence's context (new tokens included) and bf16 N(0,1) queries for the new tokens."""
-    import numpy as np
-    import torch
-    inp = build_decode_inputs(ctx_lens, H=H, HQ=HQ, cfg=cfg, mode=mode, k_bits=bits, v_bits=bits, iso_mode=iso_mode,
-                              copies=1, kv="kscale", kv_dtype="bfloat16")
-    dev = inp["q"].device
-    T = int(sum(q_lens))
-    inp["q"] = torch.randn(T, HQ, 128, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
-                           device=dev).to(torch.bfloat16)
-    inp["cu"] = torch.from_numpy(np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)).to(dev)
-    inp["q_lens"] = list(q_lens)
-    return inp
 
 
 def prefill_call(inp):
@@ -288,9 +232,9 @@ def time_prefill_cfg3(steps=5):
 
 def time_mixed_cfg4(steps=5):
     """BASELINE config 4's chunked-prefill part: 4 chunks of 2048 new tokens, each after a seeded
-    prefix of U[0, 16384] cached tokens (Qwen2.5-7B layout, iso full 3-bit)."""
+    prefix of U{0..14336} cached tokens (Qwen2.5-7B layout, iso full 3-bit)."""
     import torch
-    pre = [16 * x for x in torch.randint(0, 1024 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()]
+    pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
     q_lens = [2048] * 4
     ctx = [p + 2048 for p in pre]
     inp = prefill_inputs(q_lens, ctx, 4, 28, 4, "iso", 3, iso_mode="full")
@@ -339,7 +283,7 @@ def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     import torch
 
     from rotorquant_vllm import kernels as K
-    from rq_testlib import Params
+    from rq_inputs import Params
 
     dev = torch.device("cuda")
     p = Params("iso", 3, 3)

@@ -32,6 +32,7 @@ __all__ = [
     "compress_store",
     "paged_decompress",
     "rotation_block",
+    "shared_workspace",
 ]
 
 
@@ -190,12 +191,13 @@ def compress_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tenso
         raise ValueError("slot_mapping shorter than the number of tokens")
     N = min(N, sm.numel())
     NB, BS, TB = kv_cache.shape
+    kb, vb = _f32(k_boundaries, dev), _f32(v_boundaries, dev)
     rc = _lib.load().rq_compress_store(
         key.data_ptr(), value.data_ptr(), _lib.dtype_code(key.dtype), N, key.stride(0), key.stride(1),
         value.stride(0), value.stride(1), H, D, sm.data_ptr(), kv_cache.data_ptr(), NB, BS,
         kv_cache.stride(0), kv_cache.stride(1), TB, _f32(rot_T_even, dev).data_ptr(),
-        _f32(rot_T_odd, dev).data_ptr(), blk, k_boundaries.data_ptr(), k_boundaries.numel(),
-        v_boundaries.data_ptr(), v_boundaries.numel(), _lib.stream_ptr(dev))
+        _f32(rot_T_odd, dev).data_ptr(), blk, kb.data_ptr(), kb.numel(), vb.data_ptr(), vb.numel(),
+        _lib.stream_ptr(dev))
     _lib.check(rc, "rq_compress_store")
 
 
@@ -247,16 +249,23 @@ def paged_decompress(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens
 # ---------------------------------------------------------------------------
 
 _ws_cache: dict = {}
+_ws_retired: list = []
 
 
-def _workspace(dev, nbytes: int, kind: str = "decode") -> torch.Tensor:
-    """Scratch of one kind per device (decode: split-KV partials, query operands,
-    work list; prefill: int8 tile images), grown on demand and reused; every call
-    rewrites what it reads."""
-    buf = _ws_cache.get((dev, kind))
+def shared_workspace(device, kind: str, nbytes: int) -> torch.Tensor:
+    """Device scratch of one kind per device ("decode": split-KV partials, query
+    operands, tile descriptors; "prefill": int8 tile images), shared by every call
+    on the device's stream (calls run one after another; every call rewrites what
+    it reads).  When a call needs more, a larger buffer replaces it and the old one
+    is kept allocated until the process ends, so a HIP graph that captured its
+    address never sees it freed and reused."""
+    key = (str(device), kind)
+    buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        _ws_cache[(dev, kind)] = buf
+        if buf is not None:
+            _ws_retired.append(buf)
+        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _ws_cache[key] = buf
     return buf
 
 
@@ -284,7 +293,7 @@ def _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroid
     blk = rotation_block(rotation)
     L = _lib.load()
     need = L.rq_fused_decode_workspace_bytes(num_seqs, H_Q, head_dim, max_seq_len)
-    ws = workspace if workspace is not None and workspace.numel() >= need else _workspace(dev, need)
+    ws = workspace if workspace is not None and workspace.numel() >= need else shared_workspace(dev, "decode", need)
     R = _f32(rotation, dev)
     kc, vc = _f32(centroids_k, dev), _f32(centroids_v, dev)
     sl = seq_lens.contiguous()
@@ -394,7 +403,7 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
         max_seq_len = bt.shape[1] * block_size
     L = _lib.load()
     need = L.rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len)
-    ws = workspace if workspace is not None and workspace.numel() >= need else _workspace(dev, need, "prefill")
+    ws = workspace if workspace is not None and workspace.numel() >= need else shared_workspace(dev, "prefill", need)
     rc = L.rq_int8_prefill(
         q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
         num_seqs, max_q_len, kv_cache.data_ptr(), kv_cache.shape[0], block_size, kv_cache.stride(0),

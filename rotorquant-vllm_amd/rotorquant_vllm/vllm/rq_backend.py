@@ -22,6 +22,8 @@ classes then derive from small local stand-ins), which is how the tests run.
 from __future__ import annotations
 
 import enum
+import functools
+import inspect
 import logging
 import os
 from dataclasses import dataclass
@@ -95,18 +97,62 @@ _fused_paged_rq_decode_fn = None
 _fused_paged_rq_int8_prefill_fn = None
 _compress_store_fn = None
 _paged_decompress_fn = None
+_shared_workspace = None
 try:
     from rotorquant_vllm import _lib as _rq_lib
     from rotorquant_vllm.kernels import compress_store as _compress_store_fn
     from rotorquant_vllm.kernels import fused_paged_rq_decode as _fused_paged_rq_decode_fn
     from rotorquant_vllm.kernels import fused_paged_rq_int8_prefill as _fused_paged_rq_int8_prefill_fn
     from rotorquant_vllm.kernels import paged_decompress as _paged_decompress_fn
+    from rotorquant_vllm.kernels import shared_workspace as _shared_workspace
 
     _rq_lib.load()
     _fused_paged_kernel_available = True
     _fused_prefill_kernel_available = True
 except (ImportError, OSError, RuntimeError) as exc:
     logger.info("RotorQuant HIP kernels unavailable: %s", exc)
+
+# Shapes the fused kernels take (checked again by the C ABI): head_dim 128, a
+# GQA group of at most 16 query heads, at most 64 kv heads.
+RQ_FUSED_HEAD_DIM = 128
+RQ_FUSED_MAX_GQA = 16
+RQ_FUSED_MAX_KV_HEADS = 64
+
+
+def _fused_shape_ok(num_heads: int, num_kv_heads: int, head_size: int) -> str | None:
+    """None if the fused kernels take this attention shape, else the reason they do not."""
+    if head_size != RQ_FUSED_HEAD_DIM:
+        return f"head_size {head_size} (the fused kernels take {RQ_FUSED_HEAD_DIM})"
+    if num_kv_heads < 1 or num_kv_heads > RQ_FUSED_MAX_KV_HEADS:
+        return f"{num_kv_heads} kv heads (at most {RQ_FUSED_MAX_KV_HEADS})"
+    if num_heads % num_kv_heads or num_heads // num_kv_heads > RQ_FUSED_MAX_GQA:
+        return f"{num_heads} query heads over {num_kv_heads} kv heads (GQA group must be an integer <= 16)"
+    return None
+
+
+@functools.lru_cache(maxsize=64)
+def _accepted_keywords(fn) -> frozenset | None:
+    """Keyword names fn accepts (None: any).  The module-level kernel hooks below are
+    monkey-patchable, and a replacement may have the reference's narrower signature
+    (fused_paged_rq_decode.py:214-227, fused_paged_rq_int8_prefill.py:247-260)."""
+    try:
+        params = inspect.signature(fn).parameters
+    except (TypeError, ValueError):
+        return frozenset()
+    if any(p.kind is inspect.Parameter.VAR_KEYWORD for p in params.values()):
+        return None
+    return frozenset(params)
+
+
+def _call_hook(fn, *args, **kwargs):
+    """fn(*args, **kwargs) with the keyword arguments fn does not accept left out; only
+    the optional extras of this build (workspace, max_seq_len, cu_seqlens_q, max_q_len)
+    are ever dropped: the reference's own keywords are accepted by every hook."""
+    names = _accepted_keywords(fn)
+    if names is not None:
+        kwargs = {k: v for k, v in kwargs.items() if k in names}
+    return fn(*args, **kwargs)
+
 
 # ---------------------------------------------------------------------------
 # Cache size helpers (reference: rq_backend.py:155-188)
@@ -290,13 +336,40 @@ class RQFullAttentionSpec(FullAttentionSpec):
 
 
 class RQMetadataBuilder(_BuilderBase):
-    """Builder of the parent backend; CUDA/HIP-graph support only with the fused kernels."""
+    """Builder of the parent backend; CUDA/HIP-graph support only with the fused kernels.
+
+    Two additions to the parent's metadata, both for mixed batches:
+    * reorder_batch_threshold = 1 asks vLLM's model runner to put single-token
+      (decode) requests first, so a mixed batch is [decodes | prefill chunks]
+      and each part is a contiguous range of sequences;
+    * the host copies of query_start_loc and seq_lens that vLLM already holds
+      (CommonAttentionMetadata.query_start_loc_cpu / seq_lens_cpu) are attached
+      as rq_query_start_loc_cpu / rq_seq_lens_cpu, so forward() splits and
+      groups a mixed batch without reading device memory.
+    """
+
+    reorder_batch_threshold = 1
 
     @classmethod
     def get_cudagraph_support(cls, vllm_config: object, kv_cache_spec: object):
-        if _fused_paged_kernel_available and _parse_rq_fused_paged_env():
-            return AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE
-        return AttentionCGSupport.NEVER
+        if not (_fused_paged_kernel_available and _parse_rq_fused_paged_env()):
+            return AttentionCGSupport.NEVER
+        head_size = getattr(kv_cache_spec, "head_size", RQ_FUSED_HEAD_DIM)
+        if head_size != RQ_FUSED_HEAD_DIM:
+            return AttentionCGSupport.NEVER
+        return AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE
+
+    def build(self, *args, **kwargs):  # noqa: D102
+        md = super().build(*args, **kwargs)
+        common = kwargs.get("common_attn_metadata", args[1] if len(args) > 1 else None)
+        for name in ("query_start_loc_cpu", "seq_lens_cpu"):
+            val = getattr(common, name, None)
+            if val is not None:
+                try:
+                    setattr(md, "rq_" + name, val)
+                except (AttributeError, TypeError):  # frozen / slotted metadata: forward reads device copies
+                    pass
+        return md
 
 
 # ---------------------------------------------------------------------------
@@ -391,8 +464,14 @@ class RQAttentionImpl(_ImplBase):
         self._max_model_len = vllm_config.model_config.max_model_len if vllm_config is not None else 8192
         self._max_prefill_len = (vllm_config.scheduler_config.max_num_batched_tokens
                                  if vllm_config is not None else 2048)
-        self._fused_paged_available = _parse_rq_fused_paged_env() and _fused_paged_kernel_available
-        self._fused_prefill_available = _parse_rq_fused_paged_env() and _fused_prefill_kernel_available
+        self._max_num_seqs = (getattr(vllm_config.scheduler_config, "max_num_seqs", 256)
+                              if vllm_config is not None else 256)
+        env_on = _parse_rq_fused_paged_env()
+        why_not = _fused_shape_ok(self.num_heads, num_kv_heads, head_size)
+        if env_on and why_not is not None:
+            logger.info("RotorQuant fused kernels off for this layer: %s", why_not)
+        self._fused_paged_available = env_on and _fused_paged_kernel_available and why_not is None
+        self._fused_prefill_available = env_on and _fused_prefill_kernel_available and why_not is None
 
         fp16_total = 2 * num_kv_heads * head_size * 2
         logger.info("RQAttentionImpl: %s mode, %d KV heads, head_size=%d, k_bits=%d, v_bits=%d, "
@@ -405,17 +484,37 @@ class RQAttentionImpl(_ImplBase):
     # -- scratch -----------------------------------------------------------
 
     def _init_cg_buffers(self, kv_cache, compute_dtype):
-        """Device-side tensors used by every launch (codebooks, rotation splits, scratch)."""
+        """Device tensors every launch reads (codebooks, R and its R^T splits), and the
+        shared workspaces sized for the largest call this configuration allows
+        (max_num_seqs sequences of max_model_len for decode, one max_model_len
+        sequence of tile images for prefill).  This runs at the first forward --
+        vLLM's profiling run -- so later calls find their scratch allocated; the
+        workspaces are shared by all layers of the process on this device and are
+        never freed (rotorquant_vllm.kernels.shared_workspace)."""
         dev = kv_cache.device
         self._dev_kc = self._k_quantizer.centroids.to(dev, torch.float32).contiguous()
         self._dev_vc = self._v_quantizer.centroids.to(dev, torch.float32).contiguous()
         self._dev_kb = self._k_quantizer.boundaries.to(dev, torch.float32).contiguous()
         self._dev_vb = self._v_quantizer.boundaries.to(dev, torch.float32).contiguous()
         self._dev_R = self._rq_rot.to(dev, torch.float32).contiguous()
-        self._dev_rte = self._rq_rot_T_even.to(dev).contiguous()
-        self._dev_rto = self._rq_rot_T_odd.to(dev).contiguous()
-        self._decode_ws = None
+        self._dev_rte = self._rq_rot_T_even.to(dev, torch.float32).contiguous()
+        self._dev_rto = self._rq_rot_T_odd.to(dev, torch.float32).contiguous()
+        if dev.type == "cuda" and _shared_workspace is not None:
+            lib = _rq_lib.load()
+            cap = -(-self._max_model_len // kv_cache.shape[1]) * kv_cache.shape[1]
+            if self._fused_paged_available:
+                _shared_workspace(dev, "decode", lib.rq_fused_decode_workspace_bytes(
+                    self._max_num_seqs, self.num_heads, self.head_size, cap))
+            if self._fused_prefill_available:
+                _shared_workspace(dev, "prefill", lib.rq_int8_prefill_workspace_bytes(1, self.num_kv_heads, cap))
         self._cg_buffers_ready = True
+
+    def _launch_operands(self):
+        """(K centroids, V centroids, R) for the kernel hooks: the device copies once
+        _init_cg_buffers ran, else the quantizers' own tensors."""
+        if hasattr(self, "_dev_kc"):
+            return self._dev_kc, self._dev_vc, self._dev_R
+        return self._k_quantizer.centroids, self._v_quantizer.centroids, self._rq_rot
 
     # -- compress + store ----------------------------------------------------
 
@@ -427,39 +526,120 @@ class RQAttentionImpl(_ImplBase):
         _compress_store_fn(key[:n], value[:n], kv_cache, slot_mapping, self._dev_rte, self._dev_rto,
                            self._dev_kb, self._dev_vb, rot_block=self._rq_rot_block)
 
+    # -- fused paths -----------------------------------------------------------
+
+    def _fused_decode(self, query, kv_cache, block_table, seq_lens, output, n):
+        """Fused decode of sequences [0, n) (one query token each) into output[:n].
+
+        max_seq_len is the block table's capacity, not the batch's longest
+        sequence: a captured HIP graph replays with longer sequences than it was
+        captured with, so the launch must not depend on the lengths."""
+        kc, vc, R = self._launch_operands()
+        BS = kv_cache.shape[1]
+        cap = block_table.shape[1] * BS
+        ws = None
+        if _shared_workspace is not None and query.device.type == "cuda":
+            ws = _shared_workspace(query.device, "decode", _rq_lib.load().rq_fused_decode_workspace_bytes(
+                n, query.shape[1], self.head_size, cap))
+        _call_hook(_fused_paged_rq_decode_fn, query[:n], kv_cache, block_table, seq_lens, kc, vc, R,
+                   self.num_kv_heads, self.head_size, BS, sm_scale=self.scale, out=output[:n], max_seq_len=cap,
+                   workspace=ws)
+
+    def _prefill_groups(self, lens: list, q_lens: list, b0: int, BS: int, max_blocks: int, device):
+        """Split sequences [b0, B) into contiguous groups whose tile images fit the
+        prefill workspace (sized at init for one max_model_len sequence):
+        [(b_start, b_end, max_seq_len, max_q_len)]."""
+        lib = _rq_lib.load()
+        budget = _shared_workspace(device, "prefill", 0).numel()
+        cap = max_blocks * BS
+        groups, start, mx, mq = [], b0, 0, 0
+        for b in range(b0, len(lens)):
+            L = min(max(lens[b], 1), cap)
+            n_mx, n_mq = max(mx, L), max(mq, q_lens[b])
+            if b > start and lib.rq_int8_prefill_workspace_bytes(b + 1 - start, self.num_kv_heads, n_mx) > budget:
+                groups.append((start, b, mx, mq))
+                start, n_mx, n_mq = b, L, q_lens[b]
+            mx, mq = n_mx, n_mq
+        if start < len(lens):
+            groups.append((start, len(lens), mx, mq))
+        return groups
+
+    def _fused_batch(self, query, kv_cache, md, output, num_actual_tokens):
+        """A batch with multi-token sequences through the fused kernels: the leading
+        single-token sequences (vLLM orders decodes first) go to the fused decode,
+        the rest to the int8 prefill in groups that fit its workspace."""
+        qsl_cpu = getattr(md, "rq_query_start_loc_cpu", None)
+        sl_cpu = getattr(md, "rq_seq_lens_cpu", None)
+        qsl_cpu = (qsl_cpu if qsl_cpu is not None else md.query_start_loc.cpu()).tolist()
+        lens = (sl_cpu if sl_cpu is not None else md.seq_lens.cpu()).tolist()
+        B = len(lens)
+        q_lens = [qsl_cpu[b + 1] - qsl_cpu[b] for b in range(B)]
+        nd = 0
+        if self._fused_paged_available:
+            while nd < B and q_lens[nd] == 1:
+                nd += 1
+        if nd:
+            self._fused_decode(query, kv_cache, md.block_table[:nd], md.seq_lens[:nd], output, nd)
+        if nd == B:
+            return output
+        kc, vc, R = self._launch_operands()
+        BS = kv_cache.shape[1]
+        bt = md.block_table
+        for g0, g1, mx, mq in self._prefill_groups(lens, q_lens, nd, BS, bt.shape[1], query.device):
+            _call_hook(_fused_paged_rq_int8_prefill_fn, query[:num_actual_tokens], kv_cache, bt[g0:g1],
+                       md.seq_lens[g0:g1], kc, vc, R, self.num_kv_heads, self.head_size, BS, sm_scale=self.scale,
+                       out=output[:num_actual_tokens], cu_seqlens_q=md.query_start_loc[g0:g1 + 1], max_q_len=mq,
+                       max_seq_len=mx)
+        return output
+
     # -- non-fused path -----------------------------------------------------------
 
     def _forward_unfused(self, query, kv_cache, md, output, num_actual_tokens):
-        """Paged decompress + fp32 attention in rotated space (replaces the FA call, :937-1036)."""
+        """Paged decompress + fp32 attention in rotated space (replaces the FA call, :937-1036).
+
+        K/V of the referenced blocks are decompressed once (rq_paged_decompress) to
+        fp32; each sequence attends over its blocks, one kv head (its GQA group of
+        query heads) and at most ~32 M scores at a time.  Host lengths come from the
+        metadata's host copies when present (one device read otherwise)."""
         BS = kv_cache.shape[1]
         H, D = self.num_kv_heads, self.head_size
         q = query[:num_actual_tokens]
+        HQ = q.shape[1]
+        G = HQ // H
         q_rot = (q.float() @ self._dev_R.T).to(q.dtype).float()
+        qsl = getattr(md, "rq_query_start_loc_cpu", None)
+        if qsl is None:
+            qsl = getattr(md, "query_start_loc", None)
+            qsl = qsl.cpu() if qsl is not None else torch.tensor([0, num_actual_tokens])
+        sl = getattr(md, "rq_seq_lens_cpu", None)
+        lens = (sl if sl is not None else md.seq_lens.cpu()).tolist()
+        starts = qsl.tolist()
+        # capacity: every referenced block once (fewer when sequences share blocks)
+        cap = max(1, sum((L + BS - 1) // BS for L in lens))
+        out_k = torch.empty(cap, BS, H, D, dtype=torch.float32, device=q.device)
         k_cache, v_cache, bt, _ = _paged_decompress_fn(kv_cache, md.block_table, md.seq_lens, H, D, self._dev_kc,
-                                                       self._dev_vc, torch.float32)
-        qsl = getattr(md, "query_start_loc", None)
-        seq_lens = md.seq_lens.tolist()
-        starts = qsl.tolist() if qsl is not None else [0, num_actual_tokens]
-        bt_host = bt.cpu()
-        G = self.num_heads // H if hasattr(self, "num_heads") else q.shape[1] // H
-        out_rot = torch.zeros(num_actual_tokens, q.shape[1], D, dtype=torch.float32, device=q.device)
-        for b, L in enumerate(seq_lens):
+                                                       self._dev_vc, torch.float32, out_k=out_k,
+                                                       out_v=torch.empty_like(out_k))
+        out_rot = torch.zeros(num_actual_tokens, HQ, D, dtype=torch.float32, device=q.device)
+        for b, L in enumerate(lens):
             s0, s1 = starts[b], starts[b + 1]
-            if s1 <= s0 or L == 0:
+            T = s1 - s0
+            if T <= 0 or L == 0:
                 continue
-            nblk = (L + BS - 1) // BS
-            ids = bt_host[b, :nblk].to(q.device).long()
+            ids = bt[b, :(L + BS - 1) // BS].long()
             K = k_cache[ids].reshape(-1, H, D)[:L]
             V = v_cache[ids].reshape(-1, H, D)[:L]
-            K = K.repeat_interleave(G, dim=1).transpose(0, 1).contiguous()  # (HQ, L, D)
-            V = V.repeat_interleave(G, dim=1).transpose(0, 1).contiguous()
-            Q = q_rot[s0:s1].transpose(0, 1).contiguous()  # (HQ, T, D)
-            S = torch.matmul(Q, K.transpose(1, 2).contiguous()) * self.scale
-            T = s1 - s0
-            pos = L - T + torch.arange(T, device=q.device)
-            S = S.masked_fill(torch.arange(L, device=q.device)[None, None, :] > pos[None, :, None], float("-inf"))
-            P = torch.softmax(S, dim=-1)
-            out_rot[s0:s1] = torch.matmul(P, V).transpose(0, 1)
+            rows = max(1, min(T, (32 << 20) // max(1, G * L)))
+            for r0 in range(0, T, rows):
+                r1 = min(T, r0 + rows)
+                pos = (L - T + r0) + torch.arange(r1 - r0, device=q.device)
+                masked = torch.arange(L, device=q.device)[None, :] > pos[:, None]  # (rows, L)
+                for h in range(H):
+                    Qh = q_rot[s0 + r0:s0 + r1, h * G:(h + 1) * G, :].reshape(-1, D)  # (rows*G, D)
+                    S = (Qh @ K[:, h, :].T) * self.scale  # (rows*G, L)
+                    S = S.view(r1 - r0, G, L).masked_fill_(masked[:, None, :], float("-inf"))
+                    P = torch.softmax(S, dim=-1).view(-1, L)
+                    out_rot[s0 + r0:s0 + r1, h * G:(h + 1) * G, :] = (P @ V[:, h, :]).view(r1 - r0, G, D)
         out_rot = out_rot.to(q.dtype).float()
         output[:num_actual_tokens] = (out_rot @ self._dev_R).to(output.dtype)
         return output
@@ -468,7 +648,14 @@ class RQAttentionImpl(_ImplBase):
 
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
                 output_block_scale=None):
-        """compress/store new K/V, then attention from the packed cache."""
+        """compress/store new K/V, then attention from the packed cache (reference :858-1036).
+
+        Dispatch: a batch of single-token decodes -> fused decode (graph-capturable);
+        one multi-token sequence -> the int8 prefill with the reference's arguments;
+        a batch with several sequences and multi-token ones -> leading decodes to
+        the fused decode, the rest to the int8 prefill; without RQ_USE_FUSED_PAGED
+        (or for shapes the fused kernels do not take) -> paged decompress + fp32
+        attention."""
         assert output is not None, "Output tensor must be provided."
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("Fused output quantization is not supported with RotorQuant backend")
@@ -488,34 +675,23 @@ class RQAttentionImpl(_ImplBase):
             self._compress_and_store(key, value, kv_cache, attn_metadata.slot_mapping)
 
         if is_decode and self._fused_paged_available:
-            n = num_actual_tokens
-            _fused_paged_rq_decode_fn(query[:n], kv_cache, attn_metadata.block_table, attn_metadata.seq_lens,
-                                      self._k_quantizer.centroids, self._v_quantizer.centroids, self._rq_rot,
-                                      self.num_kv_heads, self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                      out=output[:n])
+            self._fused_decode(query, kv_cache, attn_metadata.block_table, attn_metadata.seq_lens, output,
+                               num_actual_tokens)
             return output
 
-        if (not is_decode and self._fused_prefill_available
-                and not getattr(attn_metadata, "use_cascade", False)):
+        use_cascade = getattr(attn_metadata, "use_cascade", False)
+        if not is_decode and self._fused_prefill_available and not use_cascade:
             if attn_metadata.seq_lens.numel() == 1:
-                _fused_paged_rq_int8_prefill_fn(query[:num_actual_tokens], kv_cache, attn_metadata.block_table,
-                                                attn_metadata.seq_lens, self._k_quantizer.centroids,
-                                                self._v_quantizer.centroids, self._rq_rot, self.num_kv_heads,
-                                                self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                                out=output[:num_actual_tokens],
-                                                max_seq_len=getattr(attn_metadata, "max_seq_len", None))
-            else:
-                _fused_paged_rq_int8_prefill_fn(query[:num_actual_tokens], kv_cache, attn_metadata.block_table,
-                                                attn_metadata.seq_lens, self._k_quantizer.centroids,
-                                                self._v_quantizer.centroids, self._rq_rot, self.num_kv_heads,
-                                                self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                                out=output[:num_actual_tokens],
-                                                cu_seqlens_q=attn_metadata.query_start_loc,
-                                                max_q_len=max_query_len,
-                                                max_seq_len=getattr(attn_metadata, "max_seq_len", None))
-            return output
+                # the reference's call (fused_paged_rq_int8_prefill.py:247-260), plus this
+                # build's workspace when the hook takes it
+                kc, vc, R = self._launch_operands()
+                _call_hook(_fused_paged_rq_int8_prefill_fn, query[:num_actual_tokens], kv_cache,
+                           attn_metadata.block_table, attn_metadata.seq_lens, kc, vc, R, self.num_kv_heads,
+                           self.head_size, kv_cache.shape[1], sm_scale=self.scale, out=output[:num_actual_tokens])
+                return output
+            return self._fused_batch(query, kv_cache, attn_metadata, output, num_actual_tokens)
 
-        if getattr(attn_metadata, "use_cascade", False):
+        if use_cascade:
             raise NotImplementedError("RQ does not yet support cascade attention")
         return self._forward_unfused(query, kv_cache, attn_metadata, output, num_actual_tokens)
 

@@ -101,3 +101,117 @@ def test_backend_prefill_then_decode(monkeypatch, fused, mode, bits):
     err, excess, cs = check_tolerance(outd.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
     print(f"decode {mode}{bits} fused={fused}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
     assert excess <= 0 and cs >= 0.999
+
+
+def _mixed_setup(monkeypatch, H, HQ, mode, bits, iso_mode, ctx, q_lens, cfg):
+    """Impl + a cache holding every sequence's first ctx - q_len tokens (oracle store);
+    the last q_len tokens of each sequence arrive in the forward call."""
+    monkeypatch.setenv("RQ_MODE", mode)
+    monkeypatch.setenv("RQ_BITS", str(bits))
+    monkeypatch.setenv("RQ_ISO_MODE", iso_mode)
+    monkeypatch.delenv("RQ_K_BITS", raising=False)
+    monkeypatch.delenv("RQ_V_BITS", raising=False)
+    monkeypatch.setenv("RQ_USE_FUSED_PAGED", "1")
+    from rotorquant_vllm.vllm.rq_backend import RQAttentionImpl
+    impl = RQAttentionImpl(HQ, D, 1.0 / math.sqrt(D), num_kv_heads=H)
+    p = Params(mode, bits, bits, iso_mode=iso_mode)
+    bt, NB, slots = paged_layout(ctx, BS, cfg)
+    k_all, v_all = kv_config0(sum(ctx), H, D, cfg, dtype=torch.bfloat16)
+    offs = np.concatenate([[0], np.cumsum(ctx)])
+    old_idx = np.concatenate([np.arange(offs[b], offs[b + 1] - q_lens[b]) for b in range(len(ctx))])
+    new_idx = np.concatenate([np.arange(offs[b + 1] - q_lens[b], offs[b + 1]) for b in range(len(ctx))])
+    old_slots = np.concatenate([slots[b][:ctx[b] - q_lens[b]] for b in range(len(ctx))])
+    new_slots = np.concatenate([slots[b][ctx[b] - q_lens[b]:] for b in range(len(ctx))])
+    cache0 = build_cache_oracle(k_all[old_idx], v_all[old_idx], old_slots, NB, BS, p)
+    full_cache = build_cache_oracle(k_all, v_all, np.concatenate(slots), NB, BS, p)
+    T = int(sum(q_lens))
+    q = torch.randn(T, HQ, D, generator=gen(1000 * cfg + 6)).to(torch.bfloat16)
+    md = _metadata(T, max(q_lens), new_slots, bt, ctx, q_lens)
+    md.rq_query_start_loc_cpu = md.query_start_loc.cpu()
+    md.rq_seq_lens_cpu = md.seq_lens.cpu()
+    return impl, p, dict(bt=bt, NB=NB, k_new=k_all[new_idx], v_new=v_all[new_idx], cache0=cache0,
+                         full_cache=full_cache, q=q, md=md)
+
+
+def test_backend_mixed_batch_one_forward(monkeypatch):
+    """vLLM's chunked-prefill batch shape in ONE forward: five decodes with long contexts
+    first, then two prefill chunks (one after a 600-token prefix, one fresh), at the
+    Qwen2.5-7B head layout (28 q / 4 kv, iso full 3-bit).  The decodes go to the fused
+    decode and the chunks to the int8 prefill; the cache bytes equal the oracle's store
+    and every output row meets the attention tolerance against the oracle.  The prefill
+    workspace is the one sized at init (no growth)."""
+    from rotorquant_vllm import kernels as K
+    ctx = [9000, 3000, 1500, 700, 5, 800, 64]
+    q_lens = [1, 1, 1, 1, 1, 200, 64]
+    impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 71)
+    dev = torch.device("cuda")
+    kv_cache = torch.from_numpy(c["cache0"]).to(dev)
+    out = torch.empty(c["q"].shape, dtype=torch.bfloat16, device=dev)
+    n_retired = len(K._ws_retired)
+    impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
+    torch.cuda.synchronize()
+    assert len(K._ws_retired) == n_retired, "the forward grew a workspace"
+    got_cache = kv_cache.cpu().numpy()
+    assert np.array_equal(got_cache, c["full_cache"]), f"{int((got_cache != c['full_cache']).sum())} bytes differ"
+    pn = p.np()
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    ref = O.prefill_attention(c["q"].float().numpy(), cu, c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 4, D,
+                              pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+    got = out.float().cpu().numpy()
+    for name, rows in (("decodes", slice(0, 5)), ("chunks", slice(5, None))):
+        err, excess, cs = check_tolerance(got[rows], ref[rows], "bfloat16", rot_block=p.blk)
+        print(f"mixed {name}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
+        assert excess <= 0 and cs >= 0.999, name
+
+
+def test_backend_decode_step_graph_replay(monkeypatch):
+    """One decode step through RQAttentionImpl.forward (compress + store of the new token,
+    fused decode) captured in a HIP graph, as vLLM captures UNIFORM_SINGLE_TOKEN_DECODE
+    batches.  Replays, with eager forwards in between -- one of them with a block table
+    twice as wide, which grows the shared decode workspace past the captured buffer --
+    reproduce the eager output bit for bit."""
+    from rotorquant_vllm import kernels as K
+    ctx = [700, 4000, 33, 2500]
+    impl, p, c = _mixed_setup(monkeypatch, 8, 32, "iso", 3, "fast", ctx, [1, 1, 1, 1], 72)
+    dev = torch.device("cuda")
+    kv_cache = torch.from_numpy(c["cache0"]).to(dev)
+    q, kn, vn = c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev)
+    md = c["md"]
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        impl.forward(None, q, kn, vn, kv_cache, md, output=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    # an eager batch whose block table is wider than any the workspace was sized for
+    # (2.24 M tokens of capacity per sequence: its tile descriptors alone, 4 x 70 000 x
+    # 272 bytes, outgrow the ~72 MB sized at init for 256 sequences x 8192 tokens)
+    wide_bt = torch.zeros(4, 140000, dtype=torch.int32, device=dev)
+    wide_bt[:, :md.block_table.shape[1]] = md.block_table
+    md_wide = _metadata(4, 1, md.slot_mapping.cpu().numpy(), wide_bt.cpu().numpy(), ctx, [1, 1, 1, 1])
+    out_wide = torch.empty_like(out)
+    n_retired = len(K._ws_retired)
+    for i in range(3):
+        out.zero_()
+        impl.forward(None, q, kn, vn, kv_cache, md_wide, output=out_wide)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        assert torch.equal(out_wide, eager)
+    assert len(K._ws_retired) > n_retired, "the wide batch should have grown the decode workspace"
+    pn = p.np()
+    ref = O.decode_attention(c["q"].float().numpy(), c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 8, D,
+                             pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+    _, excess, cs = check_tolerance(eager.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
+    assert excess <= 0 and cs >= 0.999
