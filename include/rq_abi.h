@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 2  /* 2: rq_int8_prefill takes max_seq_len and a workspace */
+#define RQ_ABI_VERSION 3  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc */
 
 enum rq_status {
     RQ_OK = 0,
@@ -184,6 +184,38 @@ int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_
                     const float *rotation, int32_t rot_block, float sm_scale,
                     void *out, int64_t out_stride_seq, int64_t out_stride_head,
                     void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * rq_fused_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture that may not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference, whose Triton launch allocates its scratch
+ * through torch.
+ *
+ * The split partials, query operands and tile descriptors live in a static
+ * device array of RQ_DECODE_SCRATCH_BYTES inside the library, one per GPU,
+ * held until the process ends.  A call whose rq_fused_decode_workspace_bytes(
+ * num_seqs, num_q_heads, head_dim, max_seq_len) exceeds it returns RQ_ENOSPACE
+ * and launches nothing.  The call allocates nothing (no hipMalloc, no library
+ * allocation); its first call on a device looks up that device's array.  All
+ * calls on one GPU share the array: calls that overlap in time on one GPU (two
+ * streams, two threads) race and must be serialised by the caller.  Nothing in
+ * the array needs clearing between calls (every call rewrites what it reads).
+ * Arguments and results are those of rq_fused_decode.
+ */
+#define RQ_DECODE_SCRATCH_BYTES (256LL << 20)
+int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                            int64_t q_stride_seq, int64_t q_stride_head,
+                            const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
+                            int64_t stride_block, int64_t stride_token,
+                            int32_t num_kv_heads, int32_t head_dim,
+                            const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                            const int32_t *seq_lens, int64_t max_seq_len,
+                            const float *k_centroids, int32_t n_k_centroids,
+                            const float *v_centroids, int32_t n_v_centroids,
+                            const float *rotation, int32_t rot_block, float sm_scale,
+                            void *out, int64_t out_stride_seq, int64_t out_stride_head,
+                            void *stream);
 
 /*
  * Causal prefill attention over the packed cache on int8 MFMA (Q K^T and P V),

@@ -31,6 +31,7 @@
 // exactly the k-group order used for O^T = V^T P^T (A = V^T: row = a head dim,
 // k = those 8 tokens; B = P^T: col = query head): no cross-lane movement of P.
 #include <algorithm>
+#include <mutex>
 
 #include "rq_common.h"
 
@@ -973,6 +974,16 @@ extern "C" int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num
     return DecodeWorkspace(num_seqs, num_q_heads, std::max<int64_t>(max_seq_len, 1)).total;
 }
 
+static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                             int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
+                             int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
+                             int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                             int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
+                             const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
+                             int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
+                             void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+
 extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
                                int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
                                int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
@@ -982,6 +993,87 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
                                int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
                                void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
                                int64_t workspace_bytes, void *stream) {
+    return fused_decode_impl(q, dtype, num_seqs, num_q_heads, q_stride_seq, q_stride_head, kv_cache, num_blocks,
+                             block_size, stride_block, stride_token, num_kv_heads, head_dim, block_table, max_blocks,
+                             bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids, v_centroids,
+                             n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq, out_stride_head,
+                             workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the workspace is a file-scope device array.
+// ---------------------------------------------------------------------------
+
+namespace rq {
+// Each GPU the library runs on holds its own copy of this array (its code
+// object's global segment) until the process ends.  Host code never passes the
+// array's name to a kernel or a copy: in host code the name is only a stand-in,
+// and its device address, found once per device by hipGetSymbolAddress, is the
+// one kept in g_scratch_ptr and used.
+static __device__ __align__(256) uint8_t scratch[RQ_DECODE_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mutex;
+
+// Device address of this device's scratch array (looked up on the first call on
+// each device, with that device current).  nullptr with the error text set on failure.
+static void *device_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("rq_fused_decode_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            set_error("rq_fused_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace rq
+
+extern "C" int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                                       int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
+                                       int64_t num_blocks, int32_t block_size, int64_t stride_block,
+                                       int64_t stride_token, int32_t num_kv_heads, int32_t head_dim,
+                                       const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                                       const int32_t *seq_lens, int64_t max_seq_len, const float *k_centroids,
+                                       int32_t n_k_centroids, const float *v_centroids, int32_t n_v_centroids,
+                                       const float *rotation, int32_t rot_block, float sm_scale, void *out,
+                                       int64_t out_stride_seq, int64_t out_stride_head, void *stream) {
+    const int64_t need = rq_fused_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_seq_len);
+    if (need > RQ_DECODE_SCRATCH_BYTES) {
+        set_error("rq_fused_decode_noalloc: %lld sequences x %d query heads up to %lld tokens need %lld bytes of "
+                  "scratch, more than the library's static %lld (use rq_fused_decode with a workspace)",
+                  (long long)num_seqs, num_q_heads, (long long)max_seq_len, (long long)need,
+                  (long long)RQ_DECODE_SCRATCH_BYTES);
+        return RQ_ENOSPACE;
+    }
+    void *ws = device_scratch();
+    if (ws == nullptr) return RQ_ELAUNCH;
+    return fused_decode_impl(q, dtype, num_seqs, num_q_heads, q_stride_seq, q_stride_head, kv_cache, num_blocks,
+                             block_size, stride_block, stride_token, num_kv_heads, head_dim, block_table, max_blocks,
+                             bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids, v_centroids,
+                             n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq, out_stride_head, ws,
+                             RQ_DECODE_SCRATCH_BYTES, stream);
+}
+
+// Shared body of the two entry points (workspace given or the static scratch).
+static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                             int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
+                             int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
+                             int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                             int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
+                             const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
+                             int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
+                             void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
+                             int64_t workspace_bytes, void *stream) {
     RQ_CHECK_ARG(dtype == RQ_DTYPE_BF16 || dtype == RQ_DTYPE_F16, "decode dtype must be f16 or bf16");
     RQ_CHECK_ARG(head_dim == kD, "head_dim %d unsupported (only %d)", head_dim, kD);
     RQ_CHECK_ARG(num_kv_heads >= 1 && num_kv_heads <= kMaxKvHeads, "num_kv_heads %d must be 1..%d", num_kv_heads,

@@ -36,6 +36,9 @@ _SIGNATURES = {
     "rq_fused_decode": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64,
                                  _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i32, _c_p,
                                  _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
+    "rq_fused_decode_noalloc": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32,
+                                         _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
+                                         _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p]),
     "rq_int8_prefill_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i64]),
     "rq_int8_prefill": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p,
                                  _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p,
