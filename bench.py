@@ -274,12 +274,16 @@ def time_paged_decompress(inp, steps=10):
     return dict(blocks=n_blocks, us=round(ms * 1e3, 1), GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
 
 
+COMPRESS_BYTES_PER_TOKEN_H8 = 5192  # 2*H*D*2 read + 136*H payload written + 8 slot id, H = 8 (pad not counted)
+
+
 def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     """rq_compress_store of n_tokens K+V (fp16) into random slots.
 
-    Bytes per token: K and V rows read (2*H*D*2), the slot id (8) and the whole
-    256*H-byte slot written (payload plus the zeroed padding the cache format
-    requires)."""
+    Algorithmic bytes per token (the roofline numerator): K and V rows read
+    (2*H*D*2), the payload written (136*H) and the slot id (8) = 5192 at H = 8.
+    The kernel also writes each slot's 960-byte zero padding (the format requires
+    it: 6152 bytes per token with it), reported beside as GBps_with_pad."""
     import torch
 
     from rotorquant_vllm import kernels as K
@@ -295,54 +299,190 @@ def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     k = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
     v = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
     args = (k, v, cache, slots, p.rte.to(dev), p.rto.to(dev), p.kb.to(dev), p.vb.to(dev))
-    for _ in range(3):
-        K.compress_store(*args, rot_block=4)
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(steps):
-        K.compress_store(*args, rot_block=4)
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / steps
-    nbytes = n_tokens * (2 * H * D * 2 + 8 + 256 * H)
-    return dict(tokens=n_tokens, us=ms * 1e3, GBps=nbytes / (ms * 1e-3) / 1e9)
+    ms = time_events(lambda: K.compress_store(*args, rot_block=4), steps, warmup=3)
+    alg = n_tokens * (2 * H * D * 2 + 136 * H + 8)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return dict(tokens=n_tokens, us=round(ms * 1e3, 1), GBps=round(gbs, 1),
+                GBps_with_pad=round(n_tokens * (2 * H * D * 2 + 8 + 256 * H) / (ms * 1e-3) / 1e9, 1),
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_token": 2 * H * D * 2 + 136 * H + 8,
+                          "traffic": None})
 
 
-def cpu_baseline(inp, budget_s=15.0):
-    """CPU path on a bounded sample: oracle decompress of each sequence's blocks + torch fp32 attention."""
+def config0_roundtrip(budget_s=10.0):
+    """2048 tokens x 8 kv heads x 128 of fp16 K and V, N(0,1) * (1 + |N(0,3)|)
+    per (head, channel), iso fast 3-bit, one sequence of 128 blocks in a pool of 256
+    (seeded permutation).  GPU: rq_compress_store into the cache, rq_paged_decompress back
+    to fp16.  CPU baseline (reported, on the host cores): the reference's CPU fallback op
+    sequence (torch: norm, divide, matmul, bucketize, pack; then lookup x norm), repeated on
+    the same sample for about budget_s seconds.  The cache bytes are compared with the C
+    oracle's store, and the Lloyd-Max boundary ties (a rotated coordinate exactly equal to
+    a boundary: the place where the reference's CPU and Triton paths round differently)
+    are counted."""
     import numpy as np
     import torch
 
     import oracle as O
+    from rotorquant_vllm import kernels as K
+    from rq_inputs import Params, kv_config0, paged_layout
+
+    dev = torch.device("cuda")
+    H, D, BS, N = 8, 128, 16, 2048
+    p = Params("iso", 3, 3)
+    k, v = kv_config0(N, H, D, cfg=0)
+    bt, NB, slots = paged_layout([N], BS, 0, extra_blocks=128)
+    cache = torch.zeros(NB, BS, 256 * H, dtype=torch.uint8, device=dev)
+    kd, vd, sd = k.to(dev), v.to(dev), torch.from_numpy(slots[0]).to(dev)
+    rte, rto, kb, vb = (t.to(dev) for t in (p.rte, p.rto, p.kb, p.vb))
+    comp_ms = time_events(lambda: K.compress_store(kd, vd, cache, sd, rte, rto, kb, vb, rot_block=4), 20, 3)
+    btd = torch.from_numpy(bt).to(dev)
+    sl = torch.tensor([N], dtype=torch.int32, device=dev)
+    kc, vc = p.kc.to(dev), p.vc.to(dev)
+    out_k = torch.empty(N // BS, BS, H, D, dtype=torch.float16, device=dev)
+    out_v = torch.empty_like(out_k)
+    dec_ms = time_events(lambda: K.paged_decompress(cache, btd, sl, H, D, kc, vc, torch.float16, out_k=out_k,
+                                                    out_v=out_v), 20, 3)
+    torch.cuda.synchronize()
+    # --- CPU side (the checker and the measured CPU baseline) ---
+    pn = p.np()
+    kbits, vbits = O.to_bits(k)[0], O.to_bits(v)[0]
+    kp, kn, _, k_ties = O.compress(kbits, "float16", pn["rte"], pn["rto"], pn["kb"], 4, want_ties=True)
+    vp, vn, _, v_ties = O.compress(vbits, "float16", pn["rte"], pn["rto"], pn["vb"], 4, want_ties=True)
+    ref = np.zeros((NB, BS, 256 * H), np.uint8)
+    O.compress_store(ref, slots[0], kp, kn, vp, vn)
+    exact = bool(np.array_equal(cache.cpu().numpy(), ref))
+    _, _, remap, _ = K.paged_decompress(cache, btd, sl, H, D, kc, vc, torch.float16, out_k=out_k, out_v=out_v)
+    logical_k = out_k[remap[0].long()].reshape(N, H, D).cpu()  # compact blocks back in sequence order
+    dec_exact = bool(np.array_equal(logical_k.view(torch.int16).numpy().view(np.uint16),
+                                    O.round_to(O.decompress_f32(kp, kn, pn["kc"]), "float16").astype(np.float16)
+                                    .view(np.uint16)))
+    torch.set_num_threads(os.cpu_count() or 1)
+    rte_c, rto_c, kb_c, vb_c, kc_c, vc_c = p.rte, p.rto, p.kb, p.vb, p.kc, p.vc
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        pk, nk = O.reference_cpu_compress(k, rte_c, rto_c, kb_c)
+        pv, nv = O.reference_cpu_compress(v, rte_c, rto_c, vb_c)
+        O.reference_cpu_decompress(pk, nk, kc_c, torch.float16)
+        O.reference_cpu_decompress(pv, nv, vc_c, torch.float16)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    cpu_exact = bool(np.array_equal(pk.numpy(), kp) and np.array_equal(pv.numpy(), vp))
+    rt_bytes = N * (2 * H * D * 2 + 136 * H + 8) + N * (136 * H + 2 * H * D * 2)  # compress + decompress
+    return dict(tokens=N, compress_store_us=round(comp_ms * 1e3, 1), paged_decompress_us=round(dec_ms * 1e3, 1),
+                roundtrip_GBps=round(rt_bytes / ((comp_ms + dec_ms) * 1e-3) / 1e9, 1),
+                cache_bit_exact_vs_oracle=exact, decompress_bit_exact_vs_oracle=dec_exact,
+                boundary_ties={"k": k_ties, "v": v_ties, "elements": 2 * N * H * D},
+                cpu_baseline={"value": round(rt_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                              "kind": "port", "us_per_roundtrip": round(cpu_s * 1e6, 1),
+                              "bytes_equal_to_gpu": cpu_exact,
+                              "sample": f"config 0 (2048 tokens x 8 heads, K and V) compress + decompress with the "
+                                        f"reference's CPU op sequence in torch, {reps} repetitions"})
+
+
+def cpu_baseline(inp, gpu_out, budget_s=15.0):
+    """CPU path on a bounded sample: oracle decompress of each sequence's blocks + torch fp32
+    attention (the reference has no CPU decode path).  Its outputs, rounded as the reference
+    rounds (bf16 out_rot, back-rotation, bf16), are also compared with the GPU's output."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    from rq_testlib import check_tolerance
 
     torch.set_num_threads(os.cpu_count() or 1)
     p = inp["p"]
     cache = inp["caches"][0].cpu().numpy()
     q = inp["q"].float().cpu()
-    R = p.R.numpy().astype(np.float64)
+    R = p.R.numpy()
     lens = inp["lens_host"]
     H, HQ, D = inp["H"], inp["HQ"], inp["D"]
     G = HQ // H
     done_bytes = 0
     n_seq = 0
+    outs = []
     t0 = time.perf_counter()
     for b, L in enumerate(lens):
         K_, V_ = O.gather_seq(cache, inp["bt_host"][b], L, H, D, p.kc.numpy(), p.vc.numpy())
         Kt = torch.from_numpy(K_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
         Vt = torch.from_numpy(V_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
-        qr = torch.from_numpy((q[b].numpy().astype(np.float64) @ R.T).astype(np.float32))
+        qr = torch.from_numpy(O.rotate_q(q[b].numpy(), R, "bfloat16"))
         s = torch.einsum("hd,hld->hl", qr, Kt) / math.sqrt(D)
         o = torch.einsum("hl,hld->hd", torch.softmax(s, -1), Vt)
-        _ = o.numpy() @ R.astype(np.float32)
-        done_bytes += decode_bytes([L], H, HQ, D, inp["BS"]) - 0
+        outs.append(O.unrotate_out(o.numpy(), R, "bfloat16"))
+        done_bytes += decode_bytes([L], H, HQ, D, inp["BS"])
         n_seq += 1
         if time.perf_counter() - t0 > budget_s:
             break
     el = time.perf_counter() - t0
+    got = gpu_out.float().cpu().numpy()[:n_seq]
+    ref = np.stack(outs)
+    err, excess, cs = check_tolerance(got, ref, "bfloat16", rot_block=p.blk)
     return dict(value=done_bytes / el / 1e9, unit="GB/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"{n_seq} of {len(lens)} config-1 sequences ({sum(lens[:n_seq])} tokens): oracle C "
-                       f"decompress + torch fp32 attention, {el:.1f} s", cpu=cpu_model(), os_cpu_count=os.cpu_count())
+                       f"decompress + torch fp32 attention, {el:.1f} s", cpu=cpu_model(), os_cpu_count=os.cpu_count(),
+                gpu_vs_cpu={"max_abs": err, "cos": round(cs, 7), "within_tolerance": bool(excess <= 0 and cs >= 0.999),
+                            "tolerance": "cos >= 0.999, |d| <= max(2e-2, ulp(x) + 2 ulp(rotation-block max))"})
+
+
+def time_config4_one_forward(steps=5):
+    """BASELINE config 4 as ONE RQAttentionImpl.forward (RQ_USE_FUSED_PAGED=1): 128 decodes
+    (1 x 131072 + 127 x U[512, 16384] context) then 4 chunks of 2048 tokens after prefixes
+    U{0..14336}, Qwen2.5-7B layout (28 q / 4 kv), iso full 3-bit, bf16.  The call stores the
+    132 + 8192 new tokens' K/V, runs the fused decode on the decodes and the int8 prefill on
+    the chunks.  Reported: wall time per forward (HIP events), with the decode part and the
+    chunk part also timed alone through the same forward."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from rq_inputs import gpu_decode_inputs
+
+    os.environ.update(RQ_MODE="iso", RQ_BITS="3", RQ_ISO_MODE="full", RQ_USE_FUSED_PAGED="1")
+    for var in ("RQ_K_BITS", "RQ_V_BITS"):
+        os.environ.pop(var, None)
+    from rotorquant_vllm.vllm.rq_backend import RQAttentionImpl
+
+    dec = [131072] + torch.randint(512, 16384 + 1, (127,), generator=torch.Generator().manual_seed(4004)).tolist()
+    pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
+    ctx = dec + [x + 2048 for x in pre]
+    q_lens = [1] * len(dec) + [2048] * 4
+    inp = gpu_decode_inputs(ctx, H=4, HQ=28, cfg=4, mode="iso", iso_mode="full", copies=1, kv="kscale",
+                            kv_dtype="bfloat16")
+    dev = inp["q"].device
+    impl = RQAttentionImpl(28, 128, 128 ** -0.5, num_kv_heads=4)
+    impl._max_model_len = 131072
+    T = int(sum(q_lens))
+    g = torch.Generator(device=dev).manual_seed(4006)
+    q = torch.randn(T, 28, 128, generator=g, device=dev).to(torch.bfloat16)
+    k_new = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    v_new = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    bt_host = inp["bt_host"]
+    slots = np.concatenate([bt_host[b, (np.arange(L - ql, L)) // 16].astype(np.int64) * 16 + np.arange(L - ql, L) % 16
+                            for b, (L, ql) in enumerate(zip(ctx, q_lens))])
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32)
+
+    def md_of(b0, b1):
+        c = cu[b0:b1 + 1] - cu[b0]
+        md = types.SimpleNamespace(num_actual_tokens=int(c[-1]), max_query_len=max(q_lens[b0:b1]), use_cascade=False,
+                                   slot_mapping=torch.from_numpy(slots[int(cu[b0]):int(cu[b1])]).to(dev),
+                                   block_table=inp["bt"][b0:b1], seq_lens=inp["lens"][b0:b1],
+                                   query_start_loc=c.to(dev), max_seq_len=max(ctx[b0:b1]))
+        md.rq_query_start_loc_cpu, md.rq_seq_lens_cpu = c, torch.tensor(ctx[b0:b1], dtype=torch.int32)
+        return md, int(cu[b0]), int(cu[b1])
+
+    out = torch.empty_like(q)
+    res = {}
+    for name, (b0, b1) in (("whole_batch", (0, 132)), ("decode_part", (0, 128)), ("chunk_part", (128, 132))):
+        md, r0, r1 = md_of(b0, b1)
+        fn = lambda: impl.forward(None, q[r0:r1], k_new[r0:r1], v_new[r0:r1], inp["caches"][0], md,  # noqa: E731
+                                  output=out[r0:r1])
+        res[name + "_us"] = round(time_events(fn, steps, warmup=2) * 1e3, 1)
+    del inp
+    torch.cuda.empty_cache()
+    return dict(decodes=128, decode_ctx_tokens=int(sum(dec)), chunks=4, chunk_prefixes=pre, **res)
 
 
 def measured_traffic():
@@ -363,7 +503,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
-    ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress"],
+    ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
+                                       "config0", "config4_forward"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -379,7 +520,8 @@ def main():
     if args.only:
         fn = {"compress": time_compress, "prefill3": time_prefill_cfg3, "decode2": lambda: decode_config(2),
               "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4,
-              "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1))}[args.only]
+              "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
+              "config0": config0_roundtrip, "config4_forward": time_config4_one_forward}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -391,10 +533,10 @@ def main():
     lens = config1_lens()
     inp = build_decode_inputs(lens)
     torch.cuda.synchronize()
-    t, _ = time_decode(inp, args.steps, args.warmup, graphs=args.graphs)
+    t, gpu_out = time_decode(inp, args.steps, args.warmup, graphs=args.graphs)
     if t["graphs"] and not t["replay_matches_eager"]:
         print("bench.py: graph replay differs from eager results; timing eager launches", file=sys.stderr)
-        t, _ = time_decode(inp, args.steps, args.warmup, graphs=False)
+        t, gpu_out = time_decode(inp, args.steps, args.warmup, graphs=False)
     nbytes = decode_bytes(lens, 8, 32, 128, 16)
     step_s = t["avg_ms"] * 1e-3
     gbs = nbytes / step_s / 1e9
@@ -434,8 +576,10 @@ def main():
         result["decode_config2"] = decode_config(2)
         result["decode_config4"] = decode_config(4)
         result["prefill_config4_chunks"] = time_mixed_cfg4()
+        result["config4_one_forward"] = time_config4_one_forward()
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(inp)
+        result["config0_roundtrip"] = config0_roundtrip()
+        result["cpu_baseline"] = cpu_baseline(inp, gpu_out)
     print(json.dumps(result), flush=True)
 
 

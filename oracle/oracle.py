@@ -6,7 +6,9 @@ calls it.
 
 Restates the reference (tpurtell/rotorquant-vllm) on the CPU:
 
-  compress / decompress ........ rq_oracle.c (bit-exact restatement, see there)
+  compress / decompress ........ rq_oracle.c (bit-exact restatement, see there);
+                                 reference_cpu_compress / _decompress: the same
+                                 torch CPU op sequence, timed as bench.py's CPU baseline
   lloyd_max_closed_form ........ src/rotorquant_vllm/quantization/lloyd_max.py:32-86
                                  (same schedule, exact Gaussian integrals)
   slot layout .................. src/rotorquant_vllm/vllm/rq_backend.py:155-188, :482-490
@@ -145,6 +147,38 @@ def decompress_f32(packed: np.ndarray, norms: np.ndarray, centroids: np.ndarray)
     out = np.zeros((N * H, D), np.float32)
     lib().rqo_decompress(_ptr(p), _ptr(n), N * H, D, _ptr(c), c.size, _ptr(out))
     return out.reshape(N, H, D)
+
+
+def reference_cpu_compress(x, rot_T_even, rot_T_odd, boundaries):
+    """The reference's CPU fallback compress as torch CPU ops, in its order
+    (triton/isoquant_compress.py:161-190; planarquant_compress.py:157-186 is the
+    same): norm, divide by norm + 1e-10, dense matmul with R^T, bucketize, clamp,
+    nibble pack.  Used as the measured CPU baseline of compress (its bytes equal
+    compress() above: the golden vectors pin both)."""
+    import torch
+    N, H, D = x.shape
+    flat = x.reshape(N * H, D).float()
+    raw_norms = torch.norm(flat, dim=-1, keepdim=True)
+    normalized = flat / (raw_norms + 1e-10)
+    rotation_T = torch.empty(D, D, dtype=torch.float32)
+    rotation_T[:, 0::2] = rot_T_even
+    rotation_T[:, 1::2] = rot_T_odd
+    idx = torch.bucketize(normalized @ rotation_T, boundaries).clamp(0, 15).to(torch.uint8)
+    packed = (idx[:, 0::2] << 4) | idx[:, 1::2]
+    return packed.reshape(N, H, D // 2), raw_norms.reshape(N, H, 1)
+
+
+def reference_cpu_decompress(packed, norms, centroids, dtype):
+    """The reference's CPU fallback decompress as torch CPU ops
+    (triton/isoquant_decompress.py:103-133): centroid lookup times norm, cast."""
+    import torch
+    N, H, half = packed.shape
+    pf = packed.reshape(N * H, half)
+    nf = norms.reshape(N * H, 1).float()
+    out = torch.empty(N * H, 2 * half, dtype=torch.float32)
+    out[:, 0::2] = centroids[(pf >> 4).long()] * nf
+    out[:, 1::2] = centroids[(pf & 15).long()] * nf
+    return out.reshape(N, H, 2 * half).to(dtype)
 
 
 def decompress(packed, norms, centroids, dtype: str) -> np.ndarray:

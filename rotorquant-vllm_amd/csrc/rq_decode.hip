@@ -561,7 +561,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     float sc;
     f32x4 acc[8];
     float m_run, l_run;
-    int e_run;
+    int e_run;      // every V norm of the segment so far is < 2^e_run
+    float lim;      // 2^e_run
     auto begin_segment = [&]() {
         const uint32_t ln = lane_now(), lc = ln & 15;  // rebuilt here, not kept live across the loop
         const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + lc * 256 + (ln >> 4) * 64);
@@ -574,8 +575,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     #pragma unroll
         for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;  // running max (log2 domain) for query head `col`
-        l_run = 0.f;        // this lane's partial sum of p
-        e_run = -126;       // P operand = p * v_norm * 2^-e_run <= 2^8 (fp16); acc carries the same scale
+        l_run = 0.f;        // this lane's partial sum of p' = p * 2^-e_run
+        // P operand = p' * v_norm = p * v_norm * 2^-e_run <= 2^8 (fp16).  acc and l_run
+        // carry the factor 2^-e_run, so the partial is (m_run + e_run, l_run, acc).
+        // Starting at 2^-64 keeps p' <= 2^72 and l_run finite for tiny norms.
+        e_run = -64;
+        lim = 0x1p-64f;
     };
     // Partial of the current segment -> slot w + seq.  Addresses are a uniform
     // 64-bit base plus a 32-bit lane offset computed here (a hoisted 64-bit per-lane
@@ -588,17 +593,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             uint8_t *pm = reinterpret_cast<uint8_t *>(a.part_ml + slot * 2);
             const uint32_t ln = lane_now();
             const uint32_t lo_off = ((ln & 15) * kD + 32 * (ln >> 4)) * 4;
-            // acc[m][i] * 2^e_run = O[col][8 * (4g + i) + m]
-            const float es = ldexpf(1.f, e_run);
+            // acc[m][i] = O[col][8 * (4g + i) + m] relative to 2^(m_run + e_run)
     #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float4 lo = make_float4(acc[0][i] * es, acc[1][i] * es, acc[2][i] * es, acc[3][i] * es);
-                float4 hi = make_float4(acc[4][i] * es, acc[5][i] * es, acc[6][i] * es, acc[7][i] * es);
+                float4 lo = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
+                float4 hi = make_float4(acc[4][i], acc[5][i], acc[6][i], acc[7][i]);
                 float4 *dst = reinterpret_cast<float4 *>(pa + lo_off + 32 * i);
                 dst[0] = lo;
                 dst[1] = hi;
             }
-            if (g == 0) *reinterpret_cast<float2 *>(pm + 8u * (lane_now() & 15)) = make_float2(m_run, lsum);
+            if (g == 0) *reinterpret_cast<float2 *>(pm + 8u * (lane_now() & 15)) = make_float2(m_run + (float)e_run, lsum);
         }
     };
     // The query slot holds the operand of the segment starting at local tile q_upto;
@@ -701,15 +705,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                 vw[i] = tt < valid ? vw[i] : 0u;
             }
         }
-        // largest V norm of the tile -> power-of-two scale of P
-        float nvm = fmaxf(fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3])), fmaxf(fmaxf(nv[4], nv[5]), fmaxf(nv[6], nv[7])));
-        nvm = rows_max(nvm);
-        const int e_tile = (int)((__float_as_uint(nvm) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
-        if (e_tile > e_run) {
-            const float f = ldexpf(1.f, e_run - e_tile);
+        // A V norm at or above 2^e_run (rare after the first tile): raise e_run to the
+        // tile's largest norm (over all 32 tokens: the four row groups of the wave)
+        // and rescale what carries 2^-e_run.
+        const float nvl = fmaxf(fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3])), fmaxf(fmaxf(nv[4], nv[5]), fmaxf(nv[6], nv[7])));
+        if (__any(nvl >= lim)) {
+            const float nvm = rows_max(nvl);
+            const int e_tile = (int)((__float_as_uint(nvm) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
+            if (e_tile > e_run) {
+                const float f = ldexpf(1.f, e_run - e_tile);
     #pragma unroll
-            for (int m = 0; m < 8; ++m) acc[m] *= f;
-            e_run = e_tile;
+                for (int m = 0; m < 8; ++m) acc[m] *= f;
+                l_run *= f;
+                e_run = e_tile;
+                lim = ldexpf(1.f, e_run);
+            }
         }
 
         // ---- S^T = K Q^T ----------------------------------------------------
@@ -741,7 +751,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         // than 8 (log2 units).  In between, p = 2^(score - m_run) <= 2^8, so the
         // fp16 P operand (p * v_norm * 2^-e_run <= 2^8) stays in range; acc and l_run
         // are relative to the same m_run, so the result does not depend on when the
-        // rescale happens.
+        // rescale happens.  The exponent's fma also applies 2^-e_run.
         if (__any(tmax > m_run + 8.f)) {
             const float m_new = fmaxf(m_run, tmax);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
@@ -750,13 +760,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             l_run *= alpha;
             m_run = m_new;
         }
-        const float pf = ldexpf(1.f, -e_run);
+        const float mb = -(m_run + (float)e_run);
         float p[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sc, -m_run));
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sc, mb));  // p * 2^-e_run
             l_run += p[i];
-            nv[i] *= pf;
         }
         u32x4 pop;
         pop.x = pack2<RQ_DTYPE_F16>(p[0] * nv[0], p[1] * nv[1]);

@@ -2,25 +2,28 @@
 
 Init-time part of the reference's IsoQuantMSE (src/rotorquant_vllm/quantization/isoquant.py:46-102):
 the codebook and the quaternions q_L (seed) and, in 'full' mode, q_R (seed +
-10000), drawn as normalised Gaussians from a torch generator of the target
-device type -- the same draws, so the same rotation, as the reference.
+10000), drawn as normalised Gaussians in the reference's order.  The generator
+is the CPU's unless RQ_PARAM_DEVICE=device asks for the target device's, as the
+reference uses (lloyd_max.param_draw_device).
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
-from .lloyd_max import LloydMaxCodebook
+from .lloyd_max import LloydMaxCodebook, param_draw_device
 
 
 def make_random_unit_quaternion(shape, device="cpu", seed: int | None = None) -> torch.Tensor:
-    """(..., 4) unit quaternions [w, x, y, z] (reference: isoquant.py:46-55)."""
+    """(..., 4) unit quaternions [w, x, y, z] (reference: isoquant.py:46-55), drawn on
+    param_draw_device(device) and returned on `device`."""
     dev = torch.device(device)
-    gen = torch.Generator(device=dev.type)
+    draw = param_draw_device(dev)
+    gen = torch.Generator(device=draw.type)
     if seed is not None:
         gen.manual_seed(seed)
-    q = torch.randn(*shape, 4, generator=gen, device=dev)
-    return q / q.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+    q = torch.randn(*shape, 4, generator=gen, device=draw)
+    return (q / q.norm(dim=-1, keepdim=True).clamp(min=1e-8)).to(dev)
 
 
 class IsoQuantMSE(nn.Module):

@@ -11,15 +11,33 @@ bit for bit but not the sign of the tiny middle boundary (-3.5e-17 for 3 bits,
 exactly 0 for 4 bits), which decides where exact zeros land.
 
 Unlike the reference, results are memoised per (d, bits, use_exact): every
-attention layer of a model shares one solve.
+attention layer of a model shares one solve; and the head_dim-128 codebooks come
+from a table of their fp32 bits, so startup needs no solve at all.
 """
 from __future__ import annotations
 
 import functools
 import math
+import os
 
 import torch
 from scipy import integrate
+
+
+def param_draw_device(device) -> torch.device:
+    """Device whose torch generator draws the seeded rotation parameters.
+
+    RQ_PARAM_DEVICE=cpu (the default): the CPU generator, whatever the target
+    device, so the rotations -- and every cache byte -- are the same on any
+    machine (they equal the reference's draws on a CPU device).
+    RQ_PARAM_DEVICE=device: the target device's own generator, as the reference
+    draws them (quantization/isoquant.py:46-55, planarquant.py:26-37 with vLLM's
+    device); those values depend on the device's RNG implementation.
+    Any other value raises ValueError."""
+    mode = os.environ.get("RQ_PARAM_DEVICE", "cpu").lower()
+    if mode not in ("cpu", "device"):
+        raise ValueError(f"RQ_PARAM_DEVICE must be 'cpu' or 'device', got '{mode}'")
+    return torch.device("cpu") if mode == "cpu" else torch.device(device)
 
 
 def beta_pdf(x: float, d: int) -> float:
@@ -74,8 +92,30 @@ def _solve(d: int, bits: int, use_exact: bool, max_iter: int, tol: float) -> tup
     return tuple(cents), tuple(bounds), iters
 
 
+# fp32 bit patterns of the Gaussian-model codebooks at head_dim 128 (the case
+# every supported model uses), as the solve above produces them with the
+# reference's schedule (max_iter 200, tol 1e-10): startup then needs no scipy
+# solve.  A CPU test re-solves both and compares bit for bit.
+_FP32_TABLE = {
+    (128, 3): ((0xbe42c59b, 0xbdf34608, 0xbd88da01, 0xbcb17797, 0x3cb17797, 0x3d88da01, 0x3df34608, 0x3e42c59b),
+               (0xbe1e344f, 0xbdbe1005, 0xbd3537e6, 0xa4200000, 0x3d3537e6, 0x3dbe1005, 0x3e1e344f)),
+    (128, 4): ((0xbe775eb8, 0xbe3b50e6, 0xbe127ff3, 0xbde37f89, 0xbdaaaa39, 0xbd6de67f, 0xbd0c91c0, 0xbc3a0bdd,
+                0x3c3a0bdd, 0x3d0c91c0, 0x3d6de67f, 0x3daaaa39, 0x3de37f89, 0x3e127ff3, 0x3e3b50e6, 0x3e775eb8),
+               (0xbe5957cf, 0xbe26e86d, 0xbe021fdc, 0xbdc714e1, 0xbd90cebc, 0xbd3d3c1f, 0xbcbb14b7, 0x00000000,
+                0x3cbb14b7, 0x3d3d3c1f, 0x3d90cebc, 0x3dc714e1, 0x3e021fdc, 0x3e26e86d, 0x3e5957cf)),
+}
+
+
+def _from_bits(words) -> torch.Tensor:
+    return torch.tensor(list(words), dtype=torch.int64).to(torch.int32).view(torch.float32).clone()
+
+
 def solve_lloyd_max(d: int, bits: int, use_exact: bool = False, max_iter: int = 200, tol: float = 1e-10):
     """Return (centroids fp32 [2^bits], boundaries fp32 [2^bits - 1])."""
+    key = (int(d), int(bits))
+    if not use_exact and max_iter == 200 and tol == 1e-10 and key in _FP32_TABLE:
+        c, b = _FP32_TABLE[key]
+        return _from_bits(c), _from_bits(b)
     cents, bounds, _ = _solve(int(d), int(bits), bool(use_exact), int(max_iter), float(tol))
     return torch.tensor(cents, dtype=torch.float32), torch.tensor(bounds, dtype=torch.float32)
 

@@ -193,10 +193,14 @@ def test_backend_decode_step_graph_replay(monkeypatch):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         step()
-    # an eager batch whose block table is wider than any the workspace was sized for
-    # (2.24 M tokens of capacity per sequence: its tile descriptors alone, 4 x 70 000 x
-    # 272 bytes, outgrow the ~72 MB sized at init for 256 sequences x 8192 tokens)
-    wide_bt = torch.zeros(4, 140000, dtype=torch.int32, device=dev)
+    # an eager batch whose block table is wide enough that its tile descriptors outgrow
+    # the decode workspace in use (sized at init, or grown by earlier calls)
+    from rotorquant_vllm import _lib
+    cur = K._ws_cache[(str(q.device), "decode")].numel()
+    width = 1024
+    while _lib.load().rq_fused_decode_workspace_bytes(4, 32, D, width * BS) <= cur:
+        width *= 2
+    wide_bt = torch.zeros(4, width, dtype=torch.int32, device=dev)
     wide_bt[:, :md.block_table.shape[1]] = md.block_table
     md_wide = _metadata(4, 1, md.slot_mapping.cpu().numpy(), wide_bt.cpu().numpy(), ctx, [1, 1, 1, 1])
     out_wide = torch.empty_like(out)

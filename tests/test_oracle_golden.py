@@ -151,3 +151,51 @@ def test_rotation_orthogonal_block_diagonal(mode, blk):
     idx = np.arange(128)
     off = (idx[:, None] // blk) != (idx[None, :] // blk)
     assert (R[off] == 0).all()
+
+
+def test_reference_cpu_ops_match_golden_and_c_oracle():
+    """oracle.reference_cpu_compress / _decompress (the torch op sequence bench.py times
+    as the compress CPU baseline) reproduce the golden vectors and the C restatement."""
+    g = G
+    for mode in ("iso_fast", "planar"):
+        R = torch.from_numpy(g[f"R_{mode}"])
+        RT = R.T.contiguous()
+        rte, rto = RT[:, 0::2].contiguous(), RT[:, 1::2].contiguous()
+        for bits in (3, 4):
+            b = torch.from_numpy(g[f"boundaries_b{bits}"])
+            c = torch.from_numpy(g[f"centroids_b{bits}"])
+            x = torch.from_numpy(g["x_f16"].view(np.int16)).view(torch.float16)
+            p_c, n_c = O.compress(g["x_f16"], "float16", rte.numpy(), rto.numpy(), b.numpy(), 4 if mode != "planar" else 2)
+            packed, norms = O.reference_cpu_compress(x, rte, rto, b)
+            key = f"{mode}_b{bits}_f16"
+            assert np.array_equal(packed.numpy(), g[f"packed_{key}"]), key
+            assert np.array_equal(packed.numpy(), p_c) and np.array_equal(norms.numpy(), n_c), key
+            assert np.array_equal(norms.numpy().view(np.uint32), g[f"norms_{key}"].view(np.uint32)), key
+            dec = O.reference_cpu_decompress(packed, norms, c, torch.float16)
+            assert np.array_equal(dec.view(torch.int16).numpy().view(np.uint16), g[f"dec_{key}"]), key
+
+
+def test_codebook_table_equals_the_solve():
+    """The head_dim-128 codebooks returned from the fp32 table are bit-equal to the
+    scipy solve on the reference's schedule and to the golden fixture."""
+    from rotorquant_vllm.quantization import lloyd_max as LM
+    for bits in (3, 4):
+        c, b = LM.solve_lloyd_max(128, bits)
+        cs, bs, _ = LM._solve(128, bits, False, 200, 1e-10)
+        assert np.array_equal(c.numpy().view(np.uint32), np.asarray(cs, np.float32).view(np.uint32))
+        assert np.array_equal(b.numpy().view(np.uint32), np.asarray(bs, np.float32).view(np.uint32))
+        assert np.array_equal(c.numpy().view(np.uint32), G[f"centroids_b{bits}"].view(np.uint32))
+        assert np.array_equal(b.numpy().view(np.uint32), G[f"boundaries_b{bits}"].view(np.uint32))
+
+
+def test_param_device_env(monkeypatch):
+    """RQ_PARAM_DEVICE: 'cpu' (default) draws on the CPU generator; bad values raise."""
+    from rotorquant_vllm.quantization import IsoQuantMSE
+    from rotorquant_vllm.quantization.lloyd_max import param_draw_device
+    monkeypatch.delenv("RQ_PARAM_DEVICE", raising=False)
+    assert param_draw_device("cuda").type == "cpu"
+    monkeypatch.setenv("RQ_PARAM_DEVICE", "device")
+    assert param_draw_device("cuda").type == "cuda"
+    monkeypatch.setenv("RQ_PARAM_DEVICE", "gpu")
+    with pytest.raises(ValueError, match="RQ_PARAM_DEVICE must be"):
+        IsoQuantMSE(128, 3)
