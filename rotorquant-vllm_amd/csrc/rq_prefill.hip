@@ -8,20 +8,23 @@
 //     sequence sits at position seq_len - q_len + i (chunked prefill with a
 //     cached prefix is causal-correct; the reference places it at i);
 //   * key tiles entirely above the causal diagonal are skipped;
-//   * int8 operands are rounded to nearest and carry a second int8 "low" part
-//     where one int8 is too coarse for the 2e-2 output tolerance:
-//       Q K^T = s_q s_k [q_hi.k_hi + (q_hi.k_lo + q_lo.k_hi) / 128]   (3 MFMAs)
-//       P V   = s_w s_v [w_hi.v_hi + (w_hi.v_lo + w_lo.v_hi) / 128]   (3 MFMAs)
-//     q per query row (absmax / 127); k, v from per-codebook index -> int8
-//     byte tables (centroid * 127 / max|centroid| and the residual * 128)
-//     with the per-token scale norm * max|centroid| / 127; w = p * v_norm
-//     per 64-key tile scaled by the tile's largest v norm.
+//   * int8 operands are rounded to nearest and carry a second int8 "low" part,
+//     one int8 being too coarse for the 2e-2 output tolerance:
+//       Q K^T = s_q s_k [q_hi.k_hi + (q_hi.k_lo + q_lo.k_hi) / 128]   (3 int8 MFMAs)
+//     q per query row (absmax / 127); k from a per-codebook index -> int8 byte
+//     table (centroid * 127 / max|centroid| and the residual * 128) with the
+//     per-token scale norm / (largest k norm of the 64-key tile).
+//   P V runs on the fp16 MFMA, as the reference's 16-bit product (:217-227) but
+//   with 11-bit operands on both sides: V' = (centroid * norm) * 2^-e_tile in
+//   fp16, with 2^e_tile above the 64-key tile's largest v norm, and
+//   P' = p * 2^(e_tile - e_run) in fp16, e_run the largest e_tile so far (acc
+//   is rescaled when it grows); the row sum is a 17th MFMA row of 2^-e_tile.
 //
 // Two kernels per call:
 //   * prefill_pack_kernel decodes every 64-key tile of every (sequence, kv head)
-//     once into an int8 "tile image" in the caller's workspace: K hi/lo rows (key
-//     norms included), V^T hi/lo rows, the tile's score unit and per-key V
-//     weights, laid out exactly as the attention kernel keeps them in LDS;
+//     once into a "tile image" in the caller's workspace: K hi/lo int8 rows (key
+//     norms included), fp16 V'^T rows, the tile's score unit and V exponent,
+//     laid out exactly as the attention kernel keeps them in LDS;
 //   * prefill_attn_kernel: one workgroup per (query block of QB positions, kv
 //     head, sequence); its waves are (query head of the GQA group, 16-position
 //     group).  It streams the tile images of its sequence and kv head into a
@@ -32,9 +35,12 @@
 //   A (16 x 64): lane holds row l % 16, k = 16g .. 16g+15 (16 bytes)
 //   B (64 x 16): lane holds col l % 16, k = 16g .. 16g+15
 //   C (16 x 16): lane holds col l % 16, rows 4g .. 4g+3 (4 int32)
-// S^T = K Q^T: rows = 16 keys of a key block, cols = 16 query positions.
-// O^T = V^T P^T: rows = 16 head dims, k = the 16 keys lane g holds scores
-// for (keys 16b + 4g + i, b = 0..3, i = 0..3), so P needs no transpose.
+// S^T = K Q^T: rows = 16 keys of a key block, cols = 16 query positions; lane
+// (g, col) then holds the scores of keys 16b + 4g + i (b, i = 0..3).
+// O^T = V^T P^T on v_mfma_f32_16x16x32_f16 (A 16 x 32: lane holds row
+// l % 16, k = 8g .. 8g+7), two k-steps per tile: k-step s, element j of lane
+// group g is key 32s + 4g + j (j < 4) or 32s + 16 + 4g + j - 4 (j >= 4) --
+// exactly the scores the lane holds, so P needs no transpose.
 #include <algorithm>
 
 #include "rq_common.h"
@@ -49,13 +55,27 @@ constexpr int kKT = 64;    // keys per tile
 constexpr int kPQ = 16;    // query positions per wave
 constexpr float kLog2eP = 1.4426950408889634f;
 
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+
+// fp16 MFMA of the P V product (fp32 accumulation).
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+}
+
+// Two fp32 values rounded to fp16, packed low | high << 16 (one v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+    const f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ i32x4 mfma_i8(u32x4 a, u32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
                                                  0);
 }
 
-// Two 16-bit lanes in one dword (P packing shifts both with one v_pk_lshrrev_b16).
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int sat_i8(float x) { return (int)fminf(127.f, fmaxf(-127.f, rintf(x))); }
 
@@ -90,21 +110,17 @@ struct PrefillArgs {
 // conflicts.  Padded pitches of 144 / 80 bytes measured two-way conflicts on
 // gfx950; these swizzles measured conflict-free (same speed as contiguous reads).
 //   K row r, piece c (0..7):   r * 128 + 16 * (c ^ (r & 7))
-//   V^T row d, piece c (0..3): d * 64 + 16 * (c ^ ((d >> 1) & 3))
+//   V^T row d, piece c (0..7): the same (8 keys of 16 bits per piece)
 constexpr int kKP = kPD;                            // K row pitch
-constexpr int kVP = kKT;                            // V^T row pitch
 constexpr int kImKhi = 0;                           // [64 keys][kKP] int8, dims permuted per 8
 constexpr int kImKlo = kImKhi + kKT * kKP;          // same, low parts
-constexpr int kImVthi = kImKlo + kKT * kKP;         // [128 dims][kVP] int8, keys in MFMA k order
-constexpr int kImVtlo = kImVthi + kPD * kVP;        // same, low parts
+constexpr int kImVt = kImKlo + kKT * kKP;          // [128 dims][64 keys] fp16 V', keys in MFMA k order
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
-__host__ __device__ constexpr int vt_piece(int d, int c) { return d * kVP + 16 * (c ^ ((d >> 1) & 3)); }
-constexpr int kImSk = kImVtlo + kPD * kVP;          // float: score unit = tile k scale * kmax/127 * score_scale / 128
-constexpr int kImUnit = kImSk + 4;                  // float: output unit = tile v scale * vmax / (127 * 127 * 128)
-constexpr int kImBytes = (kImUnit + 4 + 1023) / 1024 * 1024;  // whole 1 KB copies
+// V^T row d (128 bytes: 8 pieces of 8 keys) uses the K row swizzle: piece c at k_piece(d, c).
+constexpr int kImSk = kImVt + kPD * kKT * 2;        // float: score unit = tile k scale * kmax/127 * score_scale / 128
+constexpr int kImVe = kImSk + 4;                    // int: e_tile, 2^e_tile > the tile's largest v norm
+constexpr int kImBytes = (kImVe + 4 + 1023) / 1024 * 1024;  // whole 1 KB copies
 constexpr int kImChunks = kImBytes / 1024;
-constexpr int kWaveBytes = kPQ * kPD * 2;           // per wave q / out staging: 16 x 128 16-bit values
-static_assert(2 * kImBytes >= 16 * kWaveBytes, "staging must fit in the tile buffers");
 
 // Largest |centroid| of a codebook (1 when all are zero): int8 unit = this / 127.
 __device__ __forceinline__ float codebook_max(const float *c, int n) {
@@ -121,6 +137,7 @@ __device__ __forceinline__ int visible_keys(const PrefillArgs &a, int64_t seq) {
 }
 
 // ---- pack: one workgroup (256 threads) per (tile, kv head, sequence) --------
+template <int DT>
 __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     const int tile = blockIdx.x, h = blockIdx.y;
     const int64_t seq = blockIdx.z;
@@ -132,16 +149,17 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     uint8_t *img = a.ws + (((int64_t)seq * a.H + h) * a.max_tiles + tile) * kImBytes;
     const SlotLayout SL(a.H, kPD);
     __shared__ uint64_t toff[kKT];
-    const float kmax = codebook_max(a.kc, a.nkc), vmax = codebook_max(a.vc, a.nvc);
+    const float kmax = codebook_max(a.kc, a.nkc);
 
     // K codebook in int8 units; each K element is c * 127 / kmax * (k norm / tile k scale),
     // so the key norms are part of the K operand and the score unit is one per tile.
     // Likewise V: c * 127 / vmax * (v norm / tile v scale).
     __shared__ float ktab[16], vtab[16];
-    __shared__ float krho[kKT], vrho[kKT];
+    __shared__ float krho[kKT], vnorm[kKT];
+    __shared__ float vscale;  // 2^-e_v
     if (tid < 16) {
         ktab[tid] = tid < a.nkc ? a.kc[tid] * (127.f / kmax) : 0.f;
-        vtab[tid] = tid < a.nvc ? a.vc[tid] * (127.f / vmax) : 0.f;
+        vtab[tid] = tid < a.nvc ? a.vc[tid] : 0.f;
     }
     if (tid < kKT) {
         // token offset (keys past the tile's end read slot 0 and get zero norms)
@@ -164,20 +182,25 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
             nvv = *reinterpret_cast<const float *>(a.cache + off + SL.v_norm + 4 * h);
         }
         toff[tid] = off;
-        // tile scales: the largest v norm and the largest k norm
-        float mx = fmaxf(nvv, 0.f), kx = fmaxf(nkv, 0.f);
+        // tile scales: the largest k norm; the power of two above the largest v norm
+        float kx = fmaxf(nkv, 0.f), vx = fmaxf(nvv, 0.f);
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) {
-            mx = fmaxf(mx, __shfl_xor(mx, o));
             kx = fmaxf(kx, __shfl_xor(kx, o));
+            vx = fmaxf(vx, __shfl_xor(vx, o));
         }
-        const float s_v = mx > 0.f ? mx : 1.f;
         const float s_k = kx > 0.f ? kx : 1.f;
+        // 2^e_v > vx, clamped to [-14, 24] so that 2^-e_v is an fp16 (normal or denormal)
+        // value: the attention kernel's row-sum MFMA reads it.  Norms above 2^24 would
+        // overflow v' in fp16.
+        const int e_v = min(24, max(-14, (int)((__float_as_uint(vx) >> 23) & 0xffu) - 126));
         krho[tid] = nkv / s_k;
-        vrho[tid] = nvv / s_v;
-        if (tid == 0) *reinterpret_cast<float *>(img + kImSk) = s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f));
-        // P V = sum_k (w_k / 127) V_k with w = 127 p: one unit per tile
-        if (tid == 0) *reinterpret_cast<float *>(img + kImUnit) = s_v * (vmax / (127.f * 127.f * 128.f));
+        vnorm[tid] = nvv;
+        if (tid == 0) {
+            *reinterpret_cast<float *>(img + kImSk) = s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f));
+            *reinterpret_cast<int *>(img + kImVe) = e_v;
+            vscale = ldexpf(1.f, -e_v);
+        }
     }
     __syncthreads();
     // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
@@ -204,42 +227,39 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         *reinterpret_cast<uint2 *>(img + kImKhi + ko) = make_uint2(hw[0], hw[1]);
         *reinterpret_cast<uint2 *>(img + kImKlo + ko) = make_uint2(lw[0], lw[1]);
     }
-    // V^T rows: Vt[dim][kk], kk = MFMA k index of key t: key t = 16b + 4g + i -> kk = 16g + 4b + i
+    // V'^T rows: v' = (centroid * norm, rounded to fp32) * 2^-e_v (exact), rounded to
+    // fp16 (|v'| < max|centroid|).  Key t = 16b + 4gg + i sits in piece
+    // 4 (b >> 1) + gg of its dim row, element 4 (b & 1) + i: thread (key quad,
+    // dword) writes 4 consecutive keys = 8 bytes.
     {
         const int tq = tid & 15, dw = tid >> 4;  // key quad (4 consecutive keys), dword position
         uint32_t x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             x[i] = *reinterpret_cast<const uint32_t *>(a.cache + toff[4 * tq + i] + SL.v_idx + h * 64 + 4 * dw);
-        const uint32_t A01 = perm(x[1], x[0], 0x05010400u), B01 = perm(x[1], x[0], 0x07030602u);
-        const uint32_t A23 = perm(x[3], x[2], 0x05010400u), B23 = perm(x[3], x[2], 0x07030602u);
-        const uint32_t G4[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u),
-                                perm(B23, B01, 0x05040100u), perm(B23, B01, 0x07060302u)};
-        const int t0 = 4 * tq;  // = 16b + 4gg
-        const int kk = 16 * ((t0 >> 2) & 3) + 4 * (t0 >> 4);
-        float rv[4];  // byte i of a transposed word is key t0 + i
+        const int t0 = 4 * tq;
+        const int b = t0 >> 4, gg = (t0 >> 2) & 3;
+        const int piece = 4 * (b >> 1) + gg, elem_off = 8 * (b & 1);
+        float nv[4];
+        const float vs = vscale;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rv[i] = vrho[t0 + i];
+        for (int i = 0; i < 4; ++i) nv[i] = vnorm[t0 + i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int d = 8 * dw + 2 * j;
+        for (int j = 0; j < 4; ++j) {  // byte j of the dword: dims 8 dw + 2j (high nibble), + 1 (low)
 #pragma unroll
-            for (int par = 0; par < 2; ++par) {  // dim d: high nibbles, dim d + 1: low nibbles
-                const uint32_t sel = par ? (G4[j] & 0x0f0f0f0fu) : ((G4[j] >> 4) & 0x0f0f0f0fu);
-                uint32_t hv = 0, lv = 0;
+            for (int par = 0; par < 2; ++par) {
+                const int d = 8 * dw + 2 * j + par;
+                uint32_t e[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float t = vtab[(sel >> (8 * i)) & 15u] * rv[i];  // |t| <= 127
-                    const int hi = sat_i8(t);
-                    const int lo = sat_i8((t - (float)hi) * 128.f);
-                    hv |= (uint32_t)(hi & 0xff) << (8 * i);
-                    lv |= (uint32_t)(lo & 0xff) << (8 * i);
+                    const uint32_t idx = (x[i] >> (8 * j + (par ? 0 : 4))) & 15u;
+                    e[i] = f32_to_f16_bits(opaque(vtab[idx] * nv[i]) * vs);
                 }
-                const int o = vt_piece(d + par, kk >> 4) + (kk & 15);
-                *reinterpret_cast<uint32_t *>(img + kImVthi + o) = hv;
-                *reinterpret_cast<uint32_t *>(img + kImVtlo + o) = lv;
+                *reinterpret_cast<uint2 *>(img + kImVt + k_piece(d, piece) + elem_off) =
+                    make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
             }
-        }    }
+        }
+    }
 }
 
 template <int DT>
@@ -273,7 +293,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int nwaves = nthr >> 6;
     const int g = lane >> 4, col = lane & 15;
     // this lane's operand pieces in a tile image: key col, pieces g and 4 + g; dim col, piece g
-    const int koff0 = k_piece(col, g), koff1 = k_piece(col, 4 + g), voff = vt_piece(col, g);
+    const int koff0 = k_piece(col, g), koff1 = k_piece(col, 4 + g);
     const int gh = wave / a.npg;            // query head inside the GQA group
     const int pg = wave - gh * a.npg;       // 16-position group
     const int hq = h * a.G + gh;
@@ -282,10 +302,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int my_i = i0 + col;              // query index of this lane's column
     const int my_pos = pos_base + my_i;
 
-    // LDS: two tile-image buffers; the per-wave output staging aliases them after
-    // the key loop.
+    // LDS: two tile-image buffers.
     extern __shared__ __align__(16) uint8_t lds[];
-    uint16_t *wbuf = reinterpret_cast<uint16_t *>(lds + wave * kWaveBytes);
 
     // ---- key range: causal bound of the whole workgroup --------------------------
     const int last_i = min(T, (qblk + 1) * a.qb) - 1;
@@ -377,9 +395,10 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
                 uint32_t h2[2] = {0, 0}, l2[2] = {0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
+                    // |x| <= 127 (inv = 127 / absmax) and |x - xh| <= 1/2: both parts fit int8
                     const float x = qr[16 * s_ + 8 * half + order[e]] * inv;
-                    const int xh = sat_i8(x);
-                    const int xl = sat_i8((x - (float)xh) * 128.f);
+                    const int xh = (int)rintf(x);
+                    const int xl = (int)rintf((x - (float)xh) * 128.f);
                     h2[e >> 2] |= (uint32_t)(xh & 0xff) << (8 * (e & 3));
                     l2[e >> 2] |= (uint32_t)(xl & 0xff) << (8 * (e & 3));
                 }
@@ -394,12 +413,12 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     }
 
 
-    float acc[8][4];
+    f32x4 acc[8];
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[m][i] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+    int e_run = -14;  // acc = sum P' V' and lsum = sum P' 2^-e_v carry the same 2^-e_run: out = acc / l
+    f32x4 lsum = f32x4{0.f, 0.f, 0.f, 0.f};  // row 0 (lanes g = 0, element 0): the row sum of the weights
 
     // The first two tile images landed while the query operand was built.
     if (n_tiles > 0) {
@@ -447,92 +466,103 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
         tmax = rows_max(tmax) * s_unit;
-        const float m_new = fmaxf(m_run, tmax);
-        if (__any(m_new > m_run)) {
+        // Lazy running max: rescale only when a position's max exceeds m_run by more
+        // than 8 in log2 units, so p <= 2^8 in between (P' = p 2^(e_v - e_run) <= 2^8
+        // stays in fp16); acc and l_run are relative to the same m_run either way.
+        if (__any((tmax - m_run) * sq > 8.f)) {
+            const float m_new = fmaxf(m_run, tmax);
             const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sq);
 #pragma unroll
             for (int m = 0; m < 8; ++m)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[m][i] *= alpha;
-            l_run *= alpha;
+            lsum *= alpha;
             m_run = m_new;
         }
-        // w = 127 p in [0, 127] (p <= 1): hi / lo int8 in MFMA k order (16b + 4g + i -> 4b + i).
-        // z = trunc(128 w + 1/2) = round(128 w) in [0, 16256], so hi = z >> 7 and lo = z & 127
-        // are both in [0, 127] and hi + lo / 128 = z / 128.  Four z go to 16-bit pairs (one
-        // perm per pair), are shifted as pairs, and their bytes are gathered by perms.  The
-        // row sum comes from the same bytes (z = 128 hi + lo, one v_dot4 per word), so the
-        // numerator and the denominator use the same quantised weights.
-        const float msq = m_run == -INFINITY ? 0.f : m_run * sq;
-        const float usq = s_unit * sq;
-        uint32_t wh[4], wl[4];
-        uint32_t zsum = 0;
+        // V exponent of the tile: acc carries 2^-e_run, and P' = p 2^(e_v - e_run) <= 2^8
+        // in fp16 (the exponent's fma adds e_v - e_run).  The row sum is one more MFMA
+        // row: sum P' 2^-e_v = 2^-e_run sum p, with the same rounded weights as the
+        // numerator (the reference sums p in fp32 and rounds it for P V, :214-229).
+        // k-step s takes the scores of key blocks 2s and 2s + 1, in the lane's order.
+        const int e_v = *reinterpret_cast<const int *>(tb + kImVe);
+        if (e_v > e_run) {  // uniform: one tile per workgroup
+            const float f = ldexpf(1.f, e_run - e_v);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            uint32_t z[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * b + i], usq, -msq));
-                z[i] = (uint32_t)__builtin_fmaf(p, 128.f * 127.f, 0.5f);
-            }
-            const uint32_t z01 = perm(z[1], z[0], 0x05040100u), z23 = perm(z[3], z[2], 0x05040100u);
-            const u16x2 seven = {7, 7};
-            const uint32_t h01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, z01) >> seven);
-            const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, z23) >> seven);
-            wh[b] = perm(h23, h01, 0x06040200u);
-            wl[b] = perm(z23, z01, 0x06040200u) & 0x7f7f7f7fu;
-            zsum = __builtin_amdgcn_udot4(wh[b], 0x80808080u, zsum, false);
-            zsum = __builtin_amdgcn_udot4(wl[b], 0x01010101u, zsum, false);
+            for (int m = 0; m < 8; ++m) acc[m] *= f;
+            lsum *= f;
+            e_run = e_v;
         }
-        l_run = __builtin_fmaf((float)zsum, 1.f / (128.f * 127.f), l_run);  // zsum < 2^24: exact
-        const u32x4 ph = u32x4{wh[0], wh[1], wh[2], wh[3]}, pl = u32x4{wl[0], wl[1], wl[2], wl[3]};
-        // ---- O^T += V^T P^T: 8 blocks of 16 head dims ----
-        const float o_unit = *reinterpret_cast<const float *>(tb + kImUnit);
+        const float bias = (m_run == -INFINITY ? 0.f : -m_run * sq) + (float)(e_v - e_run);
+        const float usq = s_unit * sq;
+        u32x4 pop[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            float p[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * st + e], usq, bias));
+            pop[st] = u32x4{pack_f16(p[0], p[1]), pack_f16(p[2], p[3]), pack_f16(p[4], p[5]), pack_f16(p[6], p[7])};
+        }
+        {
+            const uint32_t w = col == 0 ? pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v)) : 0u;  // 2^-e_v: fp16 normal or denormal
+            const u32x4 ones = u32x4{w, w, w, w};
+            lsum = mfma_f16(ones, pop[0], lsum);
+            lsum = mfma_f16(ones, pop[1], lsum);
+        }
+        // ---- O^T += V^T P^T: 8 blocks of 16 head dims, two k-steps of 32 keys ----
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            // dim 16m + col, piece g (the swizzle term of dim 16m + col is (col >> 1) & 3)
-            const u32x4 vah = *reinterpret_cast<const u32x4 *>(tb + kImVthi + 16 * m * kVP + voff);
-            const u32x4 val = *reinterpret_cast<const u32x4 *>(tb + kImVtlo + 16 * m * kVP + voff);
-            const i32x4 zero = i32x4{0, 0, 0, 0};
-            const i32x4 oh = mfma_i8(vah, ph, zero);
-            i32x4 ol = mfma_i8(vah, pl, zero);
-            ol = mfma_i8(val, ph, ol);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[m][i] = __builtin_fmaf((float)((oh[i] << 7) + ol[i]), o_unit, acc[m][i]);
+            // dim 16m + col, piece 4st + g (the swizzle term of dim 16m + col is col & 7)
+            const u32x4 v0 = *reinterpret_cast<const u32x4 *>(tb + kImVt + 16 * m * kKP + koff0);
+            const u32x4 v1 = *reinterpret_cast<const u32x4 *>(tb + kImVt + 16 * m * kKP + koff1);
+            acc[m] = mfma_f16(v0, pop[0], acc[m]);
+            acc[m] = mfma_f16(v1, pop[1], acc[m]);
         }
         }
         wait_copies<0>();  // the next tile's image has landed
         __syncthreads();   // ... for every wave; this buffer is refilled next
     }
-    __syncthreads();  // the staging buffers below alias the tile area
     if (!wave_active) return;
 
     // ---- epilogue: normalise, round to the q dtype, rotate back by R, round ----
-    l_run = rows_sum(l_run);
-    const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
-    // acc[m][i] = O[position col][dim 16m + 4g + i]
-    __builtin_amdgcn_wave_barrier();
+    // Lane (g, col) holds position col's dims 16m + 4g + i (i = 0..3): a whole 4-dim
+    // block of R (or two 2-dim ones, whose off-block entries are exact zeros), so the
+    // back-rotation runs in registers: out[d] = fma chain over the block in
+    // increasing k of round(o[k]) * R[k][d] (fused_paged_rq_decode.py:308 order).
+    const float l_run = rows_sum(lsum[0]);  // rows 4g: only g = 0 holds row 0
+    const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;  // acc and l carry the same 2^-e_run
+    if (i0 + col >= T) return;
+    uint16_t *orow = reinterpret_cast<uint16_t *>(a.out) + (int64_t)(q0 + i0 + col) * a.o_st + (int64_t)hq * a.o_sh;
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < 8; ++m) {
+        const int d0 = 16 * m + 4 * g;
+        float o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            wbuf[col * kPD + 16 * m + 4 * g + i] = (uint16_t)Elem<DT>::from_f32(acc[m][i] * inv_l);
-    __builtin_amdgcn_wave_barrier();
-    for (int idx = lane; idx < kPQ * kPD; idx += 64) {
-        const int r = idx / kPD, d = idx - r * kPD;
-        if (i0 + r >= T) continue;
-        const int kb0 = (d / a.rot_block) * a.rot_block;
-        float o = 0.f;
-        for (int i = 0; i < a.rot_block; ++i)
-            o = __builtin_fmaf(Elem<DT>::to_f32(wbuf[r * kPD + kb0 + i]), a.R[(kb0 + i) * kPD + d], o);
-        uint16_t *dst = reinterpret_cast<uint16_t *>(a.out) + (int64_t)(q0 + i0 + r) * a.o_st + (int64_t)hq * a.o_sh;
-        dst[d] = (uint16_t)Elem<DT>::from_f32(o);
+        for (int i = 0; i < 4; ++i) o[i] = Elem<DT>::to_f32(Elem<DT>::from_f32(acc[m][i] * inv_l));
+        float4 r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const float4 *>(a.R + (int64_t)(d0 + i) * kPD + d0);
+        const float rc[4][4] = {{r[0].x, r[0].y, r[0].z, r[0].w}, {r[1].x, r[1].y, r[1].z, r[1].w},
+                                {r[2].x, r[2].y, r[2].z, r[2].w}, {r[3].x, r[3].y, r[3].z, r[3].w}};
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k0 = a.rot_block == 4 ? 0 : (j & 2);  // first row of d0 + j's block
+            float v = o[k0] * rc[k0][j];
+            v = __builtin_fmaf(o[k0 + 1], rc[k0 + 1][j], v);
+            if (a.rot_block == 4) {
+                v = __builtin_fmaf(o[2], rc[2][j], v);
+                v = __builtin_fmaf(o[3], rc[3][j], v);
+            }
+            w[j] = Elem<DT>::from_f32(v);
+        }
+        *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
     }
 }
 
+template <int DT>
 static void launch_pack(const PrefillArgs &a, int64_t num_seqs, hipStream_t st) {
     dim3 grid((unsigned)a.max_tiles, (unsigned)a.H, (unsigned)num_seqs);
-    hipLaunchKernelGGL(prefill_pack_kernel, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((prefill_pack_kernel<DT>), grid, dim3(256), 0, st, a);
 }
 
 template <int DT>
@@ -617,7 +647,8 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.o_sh = out_stride_head;
     const int nwaves = a.G * a.npg;
     hipStream_t st = (hipStream_t)stream;
-    launch_pack(a, num_seqs, st);
+    if (dtype == RQ_DTYPE_BF16) launch_pack<RQ_DTYPE_BF16>(a, num_seqs, st);
+    else launch_pack<RQ_DTYPE_F16>(a, num_seqs, st);
     int rc = check_launch("prefill_pack_kernel");
     if (rc) return rc;
     if (dtype == RQ_DTYPE_BF16) launch_attn<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, st);
