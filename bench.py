@@ -33,6 +33,7 @@ for _p in (os.path.join(ROOT, "rotorquant-vllm_amd"), os.path.join(ROOT, "oracle
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA
 
 
 def cpu_model() -> str:
@@ -242,6 +243,48 @@ def time_mixed_cfg4(steps=5):
     ops = 2 * causal_macs(q_lens, ctx, 28)
     out = dict(chunks=4, prefix_tokens=pre, us=round(ms * 1e3, 1),
                algorithmic_TOPS=round(ops / (ms * 1e-3) / 1e12, 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
+def unfused_call(inp, q, cu, max_q):
+    """One rq_paged_attention call (the backend's non-fused path) over a prepared cache."""
+    import torch
+
+    from rotorquant_vllm import kernels as K
+    p, dev = inp["p"], q.device
+    kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
+    out = torch.empty_like(q)
+
+    def fn():
+        K.paged_attention(q, inp["caches"][0], inp["bt"], inp["lens"], cu, max_q, kc, vc, R, inp["H"], 128, inp["BS"],
+                          out=out)
+    return fn
+
+
+def time_unfused(cfg, steps=5):
+    """The non-fused path (rq_paged_attention: K/V dequantized to bf16 in LDS, 16-bit MFMA)
+    on config 1's decode batch (bytes as the fused decode's roofline) or config 3's
+    causal prefill (algorithmic bf16 flops = 2 x the causal Q K^T + P V multiply-adds)."""
+    import torch
+    if cfg == 1:
+        lens = config1_lens()
+        inp = build_decode_inputs(lens, copies=1)
+        B = len(lens)
+        cu = torch.arange(B + 1, dtype=torch.int32, device="cuda")
+        ms = time_events(unfused_call(inp, inp["q"], cu, 1), steps)
+        nb = decode_bytes(lens, 8, 32, 128, 16)
+        gbs = nb / (ms * 1e-3) / 1e9
+        out = dict(batch=B, us=round(ms * 1e3, 1), GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+    else:
+        q_lens = [4096] * 8
+        inp = prefill_inputs(q_lens, q_lens, 8, 32, 3, "iso", 4)
+        ms = time_events(unfused_call(inp, inp["q"], inp["cu"], max(q_lens)), steps)
+        flops = 2 * causal_macs(q_lens, q_lens, 32)
+        tf = flops / (ms * 1e-3) / 1e12
+        out = dict(tokens=sum(q_lens), us=round(ms * 1e3, 1), bf16_TFLOPS=round(tf, 1),
+                   frac_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
     del inp
     torch.cuda.empty_cache()
     return out
@@ -504,7 +547,7 @@ def main():
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
-                                       "config0", "config4_forward"],
+                                       "config0", "config4_forward", "unfused1", "unfused3"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -521,7 +564,8 @@ def main():
         fn = {"compress": time_compress, "prefill3": time_prefill_cfg3, "decode2": lambda: decode_config(2),
               "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4,
               "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
-              "config0": config0_roundtrip, "config4_forward": time_config4_one_forward}[args.only]
+              "config0": config0_roundtrip, "config4_forward": time_config4_one_forward,
+              "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3)}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -577,6 +621,8 @@ def main():
         result["decode_config4"] = decode_config(4)
         result["prefill_config4_chunks"] = time_mixed_cfg4()
         result["config4_one_forward"] = time_config4_one_forward()
+        result["unfused_config1_decode"] = time_unfused(1)
+        result["unfused_config3_prefill"] = time_unfused(3)
     if not args.no_cpu_baseline:
         result["config0_roundtrip"] = config0_roundtrip()
         result["cpu_baseline"] = cpu_baseline(inp, gpu_out)

@@ -34,7 +34,8 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 3  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc */
+#define RQ_ABI_VERSION 4  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
+                              4: rq_paged_attention */
 
 enum rq_status {
     RQ_OK = 0,
@@ -254,6 +255,44 @@ int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q
  * per 64 keys of max_seq_len, per sequence and kv head.  No counterpart in the
  * reference, which decodes K/V inside its attention kernel. */
 int64_t rq_int8_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len);
+
+/*
+ * Attention of new query tokens over the packed cache with K and V dequantized
+ * to the q dtype inside the kernel: the backend's non-fused path in one launch,
+ * with no workspace and no decompressed copy of the cache.
+ *
+ * Replaces, in RQAttentionImpl.forward's non-fused path
+ *   src/rotorquant_vllm/vllm/rq_backend.py:937-1036:
+ *   q pre-rotation (:939-941, :981), _decompress_cache_paged (:737-852) to the
+ *   q dtype, vLLM's flash_attn_varlen_func over those pages (:996-1030) and the
+ *   back-rotation out = out_rot R (:1032-1034).
+ * K, V = dtype(centroid * norm) (the values rq_decompress writes); S = q_rot K^T
+ * with exact 16-bit products and fp32 sums; softmax in fp32; out_rot rounded to
+ * the q dtype before the back-rotation.  Query i of sequence b sits at position
+ * seq_lens[b] - q_len_b + i; causal != 0: it attends to cache positions <= its
+ * own (flash attention's bottom-right aligned causal mask with seqused_k),
+ * causal == 0: to all seq_lens[b] positions.  Keys past the block table's
+ * capacity (max_blocks * block_size) are not read.
+ *
+ * q: total_q x num_q_heads x head_dim (16-byte aligned rows), out likewise
+ * (8-byte aligned rows); head_dim 128; num_q_heads / num_kv_heads <= 16;
+ * 1..16 centroids per codebook; rot_block 2 or 4.  Other arguments as for
+ * rq_int8_prefill.  Every launch size depends only on num_seqs, max_q_len and
+ * num_kv_heads, so the call can be captured in a HIP graph.
+ */
+int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                       int64_t q_stride_tok, int64_t q_stride_head,
+                       const int32_t *cu_seqlens_q, int64_t num_seqs, int64_t max_q_len, int32_t causal,
+                       const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
+                       int64_t stride_block, int64_t stride_token,
+                       int32_t num_kv_heads, int32_t head_dim,
+                       const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                       const int32_t *seq_lens,
+                       const float *k_centroids, int32_t n_k_centroids,
+                       const float *v_centroids, int32_t n_v_centroids,
+                       const float *rotation, int32_t rot_block, float sm_scale,
+                       void *out, int64_t out_stride_tok, int64_t out_stride_head,
+                       void *stream);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,9 @@ Restates the reference (tpurtell/rotorquant-vllm) on the CPU:
                                  (math of the kernel :76-206 in fp64)
   prefill_attention ............ src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:296-363
                                  (math in fp64; causal position offset L - T + i)
+  unfused_attention ............ src/rotorquant_vllm/vllm/rq_backend.py:937-1036 (the
+                                 non-fused path: K/V decompressed to the q dtype,
+                                 flash attention's math in fp64, causal or not)
 
 Pins (what each function is checked against, besides the product):
   compress/decompress: golden vectors produced by executing the reference's
@@ -34,6 +37,9 @@ Pins (what each function is checked against, besides the product):
     decode over the visible prefix; the q / out roundings against torch's
     own casts.  Mistakes planted through _kv_head, _visible and _scores
     (GQA map, mask offset, missing scale) fail these checks.
+  unfused_attention: K/V equal to torch's decompress-then-cast; a non-causal
+    row equals the decode oracle over the whole context (two code paths);
+    causal rows with fp32 K/V equal prefill_attention.
 """
 from __future__ import annotations
 
@@ -288,17 +294,20 @@ def paged_decompress(cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb,
 # Attention references (float64 over the exact dequantized K/V)
 # ---------------------------------------------------------------------------
 
-def gather_seq(cache, block_table_row, L, num_kv_heads, head_dim, k_cb, v_cb):
-    """K, V (L, H, D) fp64 dequantized (centroid * norm in fp32) for one sequence."""
+def gather_seq(cache, block_table_row, L, num_kv_heads, head_dim, k_cb, v_cb, kv_dtype=None):
+    """K, V (L, H, D) fp64 dequantized (centroid * norm in fp32) for one sequence;
+    with kv_dtype, rounded to that dtype as decompress() writes them (the pages
+    _decompress_cache_paged hands to flash attention, rq_backend.py:737-852)."""
     NB, BS, TB = cache.shape
     nblk = (L + BS - 1) // BS
     pay = slot_layout(num_kv_heads, head_dim)["v_norm_end"]  # payload bytes (the padding is never read)
     phys = np.asarray(block_table_row)[:nblk]
     slots = cache[phys, :, :pay].reshape(nblk * BS, pay)[:L]  # whole blocks, then the first L slots
     kp, kn, vp, vn = read_slots(slots.reshape(L, 1, pay), num_kv_heads, head_dim)
-    K = decompress_f32(kp, kn, k_cb).astype(np.float64)
-    V = decompress_f32(vp, vn, v_cb).astype(np.float64)
-    return K, V
+    if kv_dtype is None:
+        return decompress_f32(kp, kn, k_cb).astype(np.float64), decompress_f32(vp, vn, v_cb).astype(np.float64)
+    return (decompress(kp, kn, k_cb, kv_dtype).astype(np.float64),
+            decompress(vp, vn, v_cb, kv_dtype).astype(np.float64))
 
 
 def block_width(R: np.ndarray) -> int:
@@ -355,9 +364,11 @@ def _scores(qr: np.ndarray, K: np.ndarray, sm_scale: float) -> np.ndarray:
     return (qr @ K.T) * sm_scale
 
 
-def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype):
+def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype,
+                         kv_dtype=None):
     """Rotated-space decode output in float64, before the output rounding:
-    (B, HQ, D).  q: (B, HQ, D) fp32 values of the dtype-rounded query."""
+    (B, HQ, D).  q: (B, HQ, D) fp32 values of the dtype-rounded query; kv_dtype as
+    for gather_seq."""
     B, HQ, D = q.shape
     G = HQ // num_kv_heads
     out = np.zeros((B, HQ, D))
@@ -366,7 +377,7 @@ def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim
         if L == 0:
             continue  # empty context -> zeros (the reference: acc 0, l 1)
         qr = rotate_q(q[b], R, dtype).astype(np.float64)  # (HQ, D)
-        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
+        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb, kv_dtype)
         kv_of = np.array([_kv_head(h, G, num_kv_heads) for h in range(HQ)])
         for kvh in range(num_kv_heads):
             heads = np.nonzero(kv_of == kvh)[0]
@@ -378,21 +389,23 @@ def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim
     return out
 
 
-def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype):
+def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype,
+                     kv_dtype=None):
     """q: (B, HQ, D) fp32 values of the dtype-rounded query.  Returns (B, HQ, D) fp32 values."""
     o_rot = decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale,
-                                 dtype)
+                                 dtype, kv_dtype)
     B, HQ, D = o_rot.shape
     return unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(B, HQ, D)
 
 
 def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
-                          sm_scale, dtype, rows=None):
-    """Rotated-space causal prefill output in float64, before the output rounding: (T, HQ, D).
+                          sm_scale, dtype, rows=None, causal=True, kv_dtype=None):
+    """Rotated-space prefill output in float64, before the output rounding: (T, HQ, D).
 
-    Query i of sequence b sits at position seq_lens[b] - q_len_b + i.  rows
+    Query i of sequence b sits at position seq_lens[b] - q_len_b + i; causal: it
+    sees the keys at positions <= its own, else all seq_lens[b] keys.  rows
     (optional, sorted global query rows) restricts the work to those rows;
-    the others stay zero."""
+    the others stay zero.  kv_dtype as for gather_seq."""
     T, HQ, D = q.shape
     G = HQ // num_kv_heads
     out = np.zeros((T, HQ, D))
@@ -406,9 +419,9 @@ def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_he
         local = np.arange(T_b) if want is None else want[(want >= s0) & (want < s1)] - s0
         if local.size == 0 or L == 0:
             continue
-        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb)
+        K, V = gather_seq(cache, block_table[b], L, num_kv_heads, head_dim, k_cb, v_cb, kv_dtype)
         qr = rotate_q(q[s0 + local].reshape(-1, D), R, dtype).reshape(local.size, HQ, D).astype(np.float64)
-        vis = _visible(L - T_b + local, L)
+        vis = _visible(L - T_b + local if causal else np.full(local.size, L - 1), L)
         Kc = [np.ascontiguousarray(K[:, j, :]) for j in range(num_kv_heads)]
         Vc = [np.ascontiguousarray(V[:, j, :]) for j in range(num_kv_heads)]
         for h in range(HQ):
@@ -423,10 +436,21 @@ def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_he
 
 
 def prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
-                      sm_scale, dtype, rows=None):
-    """Causal attention; query i of sequence b sits at position seq_lens[b] - q_len_b + i.
+                      sm_scale, dtype, rows=None, causal=True, kv_dtype=None):
+    """Attention of new tokens; query i of sequence b sits at position seq_lens[b] - q_len_b + i.
     Returns (T, HQ, D) fp32 values (rows outside `rows`, when given, are zero)."""
     o_rot = prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb,
-                                  R, sm_scale, dtype, rows)
+                                  R, sm_scale, dtype, rows, causal, kv_dtype)
     T, HQ, D = o_rot.shape
     return unrotate_out(o_rot.reshape(-1, D), R, dtype).reshape(T, HQ, D)
+
+
+def unfused_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale,
+                      dtype, rows=None, causal=True):
+    """The reference's non-fused path (rq_backend.py:937-1036): q_rot = q R^T rounded
+    to the q dtype (:939-941, :981), K/V paged-decompressed to the q dtype
+    (:737-852), flash_attn_varlen_func's attention with the bottom-right causal
+    mask over seqused_k (:996-1030; here exact, in fp64), out_rot rounded to the
+    q dtype, then out_rot R rounded (:1032-1034)."""
+    return prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
+                             sm_scale, dtype, rows, causal, kv_dtype=dtype)

@@ -43,33 +43,14 @@
 // exactly the scores the lane holds, so P needs no transpose.
 #include <algorithm>
 
-#include "rq_common.h"
+#include "rq_attn_tile.h"
 
 namespace rq {
 
-typedef __attribute__((ext_vector_type(4))) int i32x4;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-
-constexpr int kPD = 128;   // head_dim
-constexpr int kKT = 64;    // keys per tile
-constexpr int kPQ = 16;    // query positions per wave
-constexpr float kLog2eP = 1.4426950408889634f;
-
-typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-
-// fp16 MFMA of the P V product (fp32 accumulation).
-__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                  0);
-}
-
-// Two fp32 values rounded to fp16, packed low | high << 16 (one v_cvt_pk_f16_f32).
-__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
-    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
-    const f16x2 v = {(_Float16)lo, (_Float16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-}
+constexpr int kPD = kAttnD;   // head_dim
+constexpr int kKT = kAttnKT;  // keys per tile
+constexpr int kPQ = kAttnPQ;  // query positions per wave
+constexpr float kLog2eP = kAttnLog2e;
 
 __device__ __forceinline__ i32x4 mfma_i8(u32x4 a, u32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
@@ -264,23 +245,9 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
 
 template <int DT>
 __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
-    // Work order.  Workgroups are dispatched round-robin over the 8 XCDs, each with
-    // its own L2.  When the (sequence, kv head) pairs divide into 8, XCD j takes
-    // pairs j, j + 8, ... one after another, so all query blocks that stream one
-    // pair's tile images share one L2; within a pair the last (heaviest) query
-    // blocks go first.  Any other grid keeps the plain order.  Both are bijections
-    // of the grid onto (query block, kv head, sequence).
-    const uint32_t nx = gridDim.x, ny = gridDim.y;
-    const uint32_t lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
-    uint32_t pair = blockIdx.y + ny * blockIdx.z, xo = blockIdx.x;
-    if ((ny * gridDim.z) % 8u == 0) {
-        const uint32_t k = lin >> 3;  // rank of this workgroup on its XCD
-        pair = (lin & 7u) + 8u * (k / nx);
-        xo = k % nx;
-    }
-    const int qblk = (int)(nx - 1 - xo);
-    const int h = (int)(pair % ny);
-    const int64_t seq = pair / ny;
+    int qblk, h;
+    int64_t seq;
+    attn_work_item(qblk, h, seq);
     const int q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
     const int T = q1 - q0;
     const int L = a.seq_lens[seq];
@@ -358,24 +325,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
             for (int k = 0; k < 16; ++k) xin[k] = Elem<DT>::to_f32((w16[k >> 1] >> (16 * (k & 1))) & 0xffffu);
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int j = base + k;
-                float acc;
-                if (rb == 4) {  // R[j][4 (j / 4) + i], i < 4
-                    const float4 r = *reinterpret_cast<const float4 *>(a.R + (int64_t)j * kPD + (j & ~3));
-                    const int b0 = k & ~3;
-                    acc = __builtin_fmaf(xin[b0], r.x, 0.f);
-                    acc = __builtin_fmaf(xin[b0 + 1], r.y, acc);
-                    acc = __builtin_fmaf(xin[b0 + 2], r.z, acc);
-                    acc = __builtin_fmaf(xin[b0 + 3], r.w, acc);
-                } else {  // R[j][2 (j / 2) + i], i < 2
-                    const float2 r = *reinterpret_cast<const float2 *>(a.R + (int64_t)j * kPD + (j & ~1));
-                    const int b0 = k & ~1;
-                    acc = __builtin_fmaf(xin[b0], r.x, 0.f);
-                    acc = __builtin_fmaf(xin[b0 + 1], r.y, acc);
-                }
-                qr[16 * s_ + k] = Elem<DT>::to_f32(Elem<DT>::from_f32(acc));
-            }
+            for (int hf = 0; hf < 2; ++hf) rotate_q8<DT>(xin + 8 * hf, base + 8 * hf, a.R, rb, qr + 16 * s_ + 8 * hf);
         }
         // per-position absmax over 128 dims: this lane's 32, then the other three lane groups
         float amax = 0.f;
@@ -413,12 +363,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     }
 
 
-    f32x4 acc[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;
-    int e_run = -14;  // acc = sum P' V' and lsum = sum P' 2^-e_v carry the same 2^-e_run: out = acc / l
-    f32x4 lsum = f32x4{0.f, 0.f, 0.f, 0.f};  // row 0 (lanes g = 0, element 0): the row sum of the weights
+    AttnState st;
+    st.init();
 
     // The first two tile images landed while the query operand was built.
     if (n_tiles > 0) {
@@ -444,14 +390,14 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         for (int b = 0; b < 4; ++b) {
             i32x4 chh = i32x4{0, 0, 0, 0}, cx = chh;
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                // key 16b + col, piece 4st + g (the swizzle term of key 16b + col is col & 7)
-                const int ko = 16 * b * kKP + (st ? koff1 : koff0);
+            for (int ks = 0; ks < 2; ++ks) {
+                // key 16b + col, piece 4ks + g (the swizzle term of key 16b + col is col & 7)
+                const int ko = 16 * b * kKP + (ks ? koff1 : koff0);
                 const u32x4 kh = *reinterpret_cast<const u32x4 *>(tb + kImKhi + ko);
                 const u32x4 kl = *reinterpret_cast<const u32x4 *>(tb + kImKlo + ko);
-                chh = mfma_i8(kh, qh[st], chh);
-                cx = mfma_i8(kh, ql[st], cx);
-                cx = mfma_i8(kl, qh[st], cx);
+                chh = mfma_i8(kh, qh[ks], chh);
+                cx = mfma_i8(kh, ql[ks], cx);
+                cx = mfma_i8(kl, qh[ks], cx);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[4 * b + i] = (float)((chh[i] << 7) + cx[i]);
@@ -461,62 +407,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) s[j] = (16 * (j >> 2) + (j & 3)) < lim ? s[j] : -INFINITY;
         }
-        // ---- online softmax over this lane's 16 keys + the other 3 key groups ----
-        float tmax = s[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-        tmax = rows_max(tmax) * s_unit;
-        // Lazy running max: rescale only when a position's max exceeds m_run by more
-        // than 8 in log2 units, so p <= 2^8 in between (P' = p 2^(e_v - e_run) <= 2^8
-        // stays in fp16); acc and l_run are relative to the same m_run either way.
-        if (__any((tmax - m_run) * sq > 8.f)) {
-            const float m_new = fmaxf(m_run, tmax);
-            const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sq);
-#pragma unroll
-            for (int m = 0; m < 8; ++m)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[m][i] *= alpha;
-            lsum *= alpha;
-            m_run = m_new;
-        }
-        // V exponent of the tile: acc carries 2^-e_run, and P' = p 2^(e_v - e_run) <= 2^8
-        // in fp16 (the exponent's fma adds e_v - e_run).  The row sum is one more MFMA
-        // row: sum P' 2^-e_v = 2^-e_run sum p, with the same rounded weights as the
-        // numerator (the reference sums p in fp32 and rounds it for P V, :214-229).
-        // k-step s takes the scores of key blocks 2s and 2s + 1, in the lane's order.
-        const int e_v = *reinterpret_cast<const int *>(tb + kImVe);
-        if (e_v > e_run) {  // uniform: one tile per workgroup
-            const float f = ldexpf(1.f, e_run - e_v);
-#pragma unroll
-            for (int m = 0; m < 8; ++m) acc[m] *= f;
-            lsum *= f;
-            e_run = e_v;
-        }
-        const float bias = (m_run == -INFINITY ? 0.f : -m_run * sq) + (float)(e_v - e_run);
-        const float usq = s_unit * sq;
-        u32x4 pop[2];
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            float p[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * st + e], usq, bias));
-            pop[st] = u32x4{pack_f16(p[0], p[1]), pack_f16(p[2], p[3]), pack_f16(p[4], p[5]), pack_f16(p[6], p[7])};
-        }
-        {
-            const uint32_t w = col == 0 ? pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v)) : 0u;  // 2^-e_v: fp16 normal or denormal
-            const u32x4 ones = u32x4{w, w, w, w};
-            lsum = mfma_f16(ones, pop[0], lsum);
-            lsum = mfma_f16(ones, pop[1], lsum);
-        }
-        // ---- O^T += V^T P^T: 8 blocks of 16 head dims, two k-steps of 32 keys ----
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            // dim 16m + col, piece 4st + g (the swizzle term of dim 16m + col is col & 7)
-            const u32x4 v0 = *reinterpret_cast<const u32x4 *>(tb + kImVt + 16 * m * kKP + koff0);
-            const u32x4 v1 = *reinterpret_cast<const u32x4 *>(tb + kImVt + 16 * m * kKP + koff1);
-            acc[m] = mfma_f16(v0, pop[0], acc[m]);
-            acc[m] = mfma_f16(v1, pop[1], acc[m]);
-        }
+        // ---- online softmax and O^T += V'^T P'^T ----
+        softmax_pv(st, s, s_unit, sq, *reinterpret_cast<const int *>(tb + kImVe), tb + kImVt, koff0, koff1, col);
         }
         wait_copies<0>();  // the next tile's image has landed
         __syncthreads();   // ... for every wave; this buffer is refilled next
@@ -524,39 +416,10 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     if (!wave_active) return;
 
     // ---- epilogue: normalise, round to the q dtype, rotate back by R, round ----
-    // Lane (g, col) holds position col's dims 16m + 4g + i (i = 0..3): a whole 4-dim
-    // block of R (or two 2-dim ones, whose off-block entries are exact zeros), so the
-    // back-rotation runs in registers: out[d] = fma chain over the block in
-    // increasing k of round(o[k]) * R[k][d] (fused_paged_rq_decode.py:308 order).
-    const float l_run = rows_sum(lsum[0]);  // rows 4g: only g = 0 holds row 0
-    const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;  // acc and l carry the same 2^-e_run
+    const float inv_l = attn_inv_l(st);
     if (i0 + col >= T) return;
     uint16_t *orow = reinterpret_cast<uint16_t *>(a.out) + (int64_t)(q0 + i0 + col) * a.o_st + (int64_t)hq * a.o_sh;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const int d0 = 16 * m + 4 * g;
-        float o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = Elem<DT>::to_f32(Elem<DT>::from_f32(acc[m][i] * inv_l));
-        float4 r[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const float4 *>(a.R + (int64_t)(d0 + i) * kPD + d0);
-        const float rc[4][4] = {{r[0].x, r[0].y, r[0].z, r[0].w}, {r[1].x, r[1].y, r[1].z, r[1].w},
-                                {r[2].x, r[2].y, r[2].z, r[2].w}, {r[3].x, r[3].y, r[3].z, r[3].w}};
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k0 = a.rot_block == 4 ? 0 : (j & 2);  // first row of d0 + j's block
-            float v = o[k0] * rc[k0][j];
-            v = __builtin_fmaf(o[k0 + 1], rc[k0 + 1][j], v);
-            if (a.rot_block == 4) {
-                v = __builtin_fmaf(o[2], rc[2][j], v);
-                v = __builtin_fmaf(o[3], rc[3][j], v);
-            }
-            w[j] = Elem<DT>::from_f32(v);
-        }
-        *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
-    }
+    store_rotated<DT>(st, inv_l, orow, a.R, a.rot_block, g);
 }
 
 template <int DT>

@@ -44,6 +44,10 @@ _SIGNATURES = {
                                  _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p,
                                  _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64,
                                  _c_p, _c_i64, _c_p]),
+    "rq_paged_attention": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32,
+                                    _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
+                                    _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64,
+                                    _c_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -13,6 +13,9 @@ the C ABI (include/rq_abi.h).  Differences, all deliberate:
   raises ValueError for more than one, fused_paged_rq_int8_prefill.py:305-309)
   through the keyword `cu_seqlens_q`; with one sequence and no keyword it
   behaves as the reference: all q tokens are the sequence's last q_len tokens.
+* paged_attention has no op-level counterpart: it is the backend's non-fused
+  path (paged decompress + flash_attn_varlen_func + the two rotations,
+  rq_backend.py:937-1036) as one launch.
 """
 from __future__ import annotations
 
@@ -31,6 +34,7 @@ __all__ = [
     "fused_paged_rq_decode",
     "compress_store",
     "paged_decompress",
+    "paged_attention",
     "rotation_block",
     "shared_workspace",
 ]
@@ -412,4 +416,52 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
         R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
         _lib.stream_ptr(dev))
     _lib.check(rc, "rq_int8_prefill")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Non-fused path: attention over K/V dequantized to the q dtype in-kernel
+# ---------------------------------------------------------------------------
+
+def paged_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    cu_seqlens_q: torch.Tensor, max_q_len: int, k_centroids: torch.Tensor,
+                    v_centroids: torch.Tensor, rotation: torch.Tensor, num_kv_heads: int, head_dim: int,
+                    block_size: int, sm_scale: float | None = None, causal: bool = True,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention of the new query tokens over the packed cache, q and output in original space.
+
+    The reference's non-fused path (rq_backend.py:937-1036: q_rot = q R^T cast to
+    q's dtype, paged decompress to q's dtype, flash_attn_varlen_func, out_rot R)
+    as one kernel that dequantizes K/V tiles into LDS (rq_paged_attention).
+    q: (num_tokens, H_Q, D); cu_seqlens_q (num_seqs + 1,) int32; seq_lens
+    (num_seqs,) int32 context lengths including the new tokens; max_q_len: a host
+    int bounding every q_len (it sizes the grid).  Query i of sequence b sits at
+    position seq_lens[b] - q_len_b + i.
+    """
+    num_tokens, H_Q, D = q.shape
+    assert D == head_dim
+    assert H_Q % num_kv_heads == 0
+    assert kv_cache.dtype == torch.uint8
+    assert block_table.dtype == torch.int32 and seq_lens.dtype == torch.int32
+    assert cu_seqlens_q.dtype == torch.int32
+    dev = _require_device(q, kv_cache, block_table, seq_lens, cu_seqlens_q)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    bt = block_table if block_table.stride(-1) == 1 else block_table.contiguous()
+    blk = rotation_block(rotation)
+    R = _f32(rotation, dev)
+    kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
+    cu, sl = cu_seqlens_q.contiguous(), seq_lens.contiguous()
+    L = _lib.load()
+    rc = L.rq_paged_attention(
+        q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
+        sl.numel(), int(max_q_len), 1 if causal else 0, kv_cache.data_ptr(), kv_cache.shape[0], block_size,
+        kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim, bt.data_ptr(), bt.shape[1], bt.stride(0),
+        sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale),
+        out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_paged_attention")
     return out

@@ -14,7 +14,9 @@ librq_hip.so (include/rq_abi.h):
     compress + store  -> rq_compress_store   (one fused K+V launch, writes slots)
     decode            -> rq_fused_decode     (Q and output rotation inside)
     prefill           -> rq_int8_prefill     (int8 MFMA, multi-sequence)
-    non-fused path    -> rq_paged_decompress + fp32 attention
+    non-fused path    -> rq_paged_attention  (K/V dequantized to the q dtype in
+                         LDS, 16-bit MFMA; head_size 128), other head sizes
+                         rq_paged_decompress + device attention in fp32
 
 vLLM itself is imported lazily: without vLLM the module still imports (the
 classes then derive from small local stand-ins), which is how the tests run.
@@ -97,12 +99,14 @@ _fused_paged_rq_decode_fn = None
 _fused_paged_rq_int8_prefill_fn = None
 _compress_store_fn = None
 _paged_decompress_fn = None
+_paged_attention_fn = None
 _shared_workspace = None
 try:
     from rotorquant_vllm import _lib as _rq_lib
     from rotorquant_vllm.kernels import compress_store as _compress_store_fn
     from rotorquant_vllm.kernels import fused_paged_rq_decode as _fused_paged_rq_decode_fn
     from rotorquant_vllm.kernels import fused_paged_rq_int8_prefill as _fused_paged_rq_int8_prefill_fn
+    from rotorquant_vllm.kernels import paged_attention as _paged_attention_fn
     from rotorquant_vllm.kernels import paged_decompress as _paged_decompress_fn
     from rotorquant_vllm.kernels import shared_workspace as _shared_workspace
 
@@ -336,7 +340,9 @@ class RQFullAttentionSpec(FullAttentionSpec):
 
 
 class RQMetadataBuilder(_BuilderBase):
-    """Builder of the parent backend; CUDA/HIP-graph support only with the fused kernels.
+    """Builder of the parent backend; HIP-graph capture of uniform single-token decode
+    batches whenever the kernels take the shape (the fused decode and the non-fused
+    rq_paged_attention both launch with sizes independent of the context lengths).
 
     Two additions to the parent's metadata, both for mixed batches:
     * reorder_batch_threshold = 1 asks vLLM's model runner to put single-token
@@ -352,7 +358,7 @@ class RQMetadataBuilder(_BuilderBase):
 
     @classmethod
     def get_cudagraph_support(cls, vllm_config: object, kv_cache_spec: object):
-        if not (_fused_paged_kernel_available and _parse_rq_fused_paged_env()):
+        if not _fused_paged_kernel_available:
             return AttentionCGSupport.NEVER
         head_size = getattr(kv_cache_spec, "head_size", RQ_FUSED_HEAD_DIM)
         if head_size != RQ_FUSED_HEAD_DIM:
@@ -595,7 +601,31 @@ class RQAttentionImpl(_ImplBase):
     # -- non-fused path -----------------------------------------------------------
 
     def _forward_unfused(self, query, kv_cache, md, output, num_actual_tokens):
-        """Paged decompress + fp32 attention in rotated space (replaces the FA call, :937-1036).
+        """Non-fused path (replaces :937-1036: q pre-rotation, paged decompress to the q
+        dtype, flash_attn_varlen_func, back-rotation).
+
+        head_size 128, f16/bf16: one rq_paged_attention launch over the whole batch
+        (K/V tiles dequantized to the q dtype in LDS; no workspace, no host read of
+        the metadata, capturable in a HIP graph).  Other shapes: the device path
+        _forward_unfused_torch."""
+        q = query[:num_actual_tokens]
+        if (_paged_attention_fn is not None and q.dtype in (torch.float16, torch.bfloat16)
+                and _fused_shape_ok(q.shape[1], self.num_kv_heads, self.head_size) is None):
+            max_q = getattr(md, "max_query_len", None)
+            if max_q is None:
+                qsl = getattr(md, "rq_query_start_loc_cpu", None)
+                qsl = qsl if qsl is not None else md.query_start_loc.cpu()
+                max_q = int((qsl[1:] - qsl[:-1]).max()) if qsl.numel() > 1 else 0
+            kc, vc, R = self._launch_operands()
+            _paged_attention_fn(q, kv_cache, md.block_table, md.seq_lens, md.query_start_loc, int(max_q), kc, vc, R,
+                                self.num_kv_heads, self.head_size, kv_cache.shape[1], sm_scale=self.scale,
+                                causal=bool(getattr(md, "causal", True)), out=output[:num_actual_tokens])
+            return output
+        return self._forward_unfused_torch(query, kv_cache, md, output, num_actual_tokens)
+
+    def _forward_unfused_torch(self, query, kv_cache, md, output, num_actual_tokens):
+        """Paged decompress + fp32 attention on the device, for shapes rq_paged_attention
+        does not take (head sizes other than 128, GQA groups above 16, fp32 models).
 
         K/V of the referenced blocks are decompressed once (rq_paged_decompress) to
         fp32; each sequence attends over its blocks, one kv head (its GQA group of
@@ -606,6 +636,7 @@ class RQAttentionImpl(_ImplBase):
         q = query[:num_actual_tokens]
         HQ = q.shape[1]
         G = HQ // H
+        causal = bool(getattr(md, "causal", True))
         q_rot = (q.float() @ self._dev_R.T).to(q.dtype).float()
         qsl = getattr(md, "rq_query_start_loc_cpu", None)
         if qsl is None:
@@ -633,6 +664,8 @@ class RQAttentionImpl(_ImplBase):
             for r0 in range(0, T, rows):
                 r1 = min(T, r0 + rows)
                 pos = (L - T + r0) + torch.arange(r1 - r0, device=q.device)
+                if not causal:
+                    pos = torch.full_like(pos, L - 1)
                 masked = torch.arange(L, device=q.device)[None, :] > pos[:, None]  # (rows, L)
                 for h in range(H):
                     Qh = q_rot[s0 + r0:s0 + r1, h * G:(h + 1) * G, :].reshape(-1, D)  # (rows*G, D)
@@ -654,8 +687,8 @@ class RQAttentionImpl(_ImplBase):
         one multi-token sequence -> the int8 prefill with the reference's arguments;
         a batch with several sequences and multi-token ones -> leading decodes to
         the fused decode, the rest to the int8 prefill; without RQ_USE_FUSED_PAGED
-        (or for shapes the fused kernels do not take) -> paged decompress + fp32
-        attention."""
+        (or for shapes the fused kernels do not take) -> the non-fused path
+        (_forward_unfused)."""
         assert output is not None, "Output tensor must be provided."
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("Fused output quantization is not supported with RotorQuant backend")

@@ -208,3 +208,29 @@ def test_workspace_growth_keeps_captured_buffers_alive(monkeypatch):
     assert big is not small and big.numel() >= 5000
     assert any(t.data_ptr() == ptr for t in K._ws_retired)        # the old one is still held
     assert K.shared_workspace("cpu", "decode", 4000) is big
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_unfused_path_is_one_paged_attention_call(monkeypatch, causal):
+    """Without RQ_USE_FUSED_PAGED a mixed batch is one rq_paged_attention call over the
+    whole batch, with vLLM's device metadata as is (no host copies read) and
+    max_query_len / causal from the metadata."""
+    impl = _bare_impl(False, False)
+    calls = []
+
+    def fake(q, kv_cache, block_table, seq_lens, cu_seqlens_q, max_q_len, kc, vc, R, num_kv_heads, head_dim,
+             block_size, sm_scale=None, causal=True, out=None):
+        calls.append((tuple(q.shape), block_table is md.block_table, seq_lens is md.seq_lens,
+                      cu_seqlens_q is md.query_start_loc, max_q_len, causal, num_kv_heads, head_dim, block_size,
+                      sm_scale))
+        out.fill_(2.0)
+        return out
+
+    monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", fake)
+    md = _mixed_metadata([1, 1, 40, 7], [500, 30, 300, 107], host_copies=False)
+    md.causal = causal
+    query = torch.randn(md.num_actual_tokens + 3, 32, 128, dtype=torch.bfloat16)  # 3 padding rows
+    output = torch.zeros_like(query)
+    impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
+    assert calls == [((49, 32, 128), True, True, True, 40, causal, 8, 128, 16, 0.125)]
+    assert torch.all(output[:49] == 2.0) and torch.all(output[49:] == 0.0)

@@ -4,10 +4,13 @@ One prefill step (three ragged prompts) and one decode step through
 RQAttentionImpl.forward, as vLLM drives it (rq_backend.py:858-1036 in the
 reference): new K/V are compressed into the packed cache, then attention runs
 from the cache, fused (RQ_USE_FUSED_PAGED=1: rq_fused_decode / rq_int8_prefill)
-or unfused (paged decompress + fp32 attention).  After each step every cache
+or unfused (rq_paged_attention; or paged decompress + fp32 attention on the
+device, the path kept for other head sizes).  After each step every cache
 byte must equal the oracle's store of the same K/V, and the output must match
 the oracle's attention within the parity tolerance (cos >= 0.999,
-|got - ref| <= max(2e-2, ulp(x) + 2 ulp(rotation-block max))).
+|got - ref| <= max(2e-2, ulp(x) + 2 ulp(rotation-block max))); the
+rq_paged_attention path against the oracle of the reference's non-fused path
+(K/V decompressed to the q dtype).
 """
 import math
 import types
@@ -51,10 +54,16 @@ def _metadata(n_tokens, max_query_len, slots, bt, seq_lens, q_lens):
         query_start_loc=torch.from_numpy(cu).to(d), max_seq_len=int(max(seq_lens)))
 
 
-@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+@pytest.mark.parametrize("path", ["fused", "unfused", "unfused_torch"])
 @pytest.mark.parametrize("mode,bits", [("iso", 3), ("planar", 4)])
-def test_backend_prefill_then_decode(monkeypatch, fused, mode, bits):
+def test_backend_prefill_then_decode(monkeypatch, path, mode, bits):
+    """fused: RQ_USE_FUSED_PAGED=1; unfused: rq_paged_attention; unfused_torch: the
+    device path kept for shapes rq_paged_attention does not take, forced here."""
+    fused = path == "fused"
     impl = _impl(monkeypatch, fused, mode, bits)
+    if path == "unfused_torch":
+        import rotorquant_vllm.vllm.rq_backend as rq_backend_module
+        monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", None)
     p = Params(mode, bits, bits)
     pn = p.np()
     dev = torch.device("cuda")
@@ -78,10 +87,12 @@ def test_backend_prefill_then_decode(monkeypatch, fused, mode, bits):
     got_cache = kv_cache.cpu().numpy()
     assert np.array_equal(got_cache, ref_cache), f"prefill store: {int((got_cache != ref_cache).sum())} bytes differ"
     cu = np.concatenate([[0], np.cumsum(prompts)]).astype(np.int32)
+    # rq_paged_attention follows the reference's non-fused path: K/V decompressed to the q dtype
+    kv_dtype = "bfloat16" if path == "unfused" else None
     ref = O.prefill_attention(q.float().numpy(), cu, ref_cache, bt, np.asarray(prompts, np.int32), H, D, pn["kc"],
-                              pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+                              pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16", kv_dtype=kv_dtype)
     err, excess, cs = check_tolerance(out.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
-    print(f"prefill {mode}{bits} fused={fused}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
+    print(f"prefill {mode}{bits} {path}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
     assert excess <= 0 and cs >= 0.999
 
     # ---- decode: one new token per sequence ---------------------------------------
@@ -97,13 +108,13 @@ def test_backend_prefill_then_decode(monkeypatch, fused, mode, bits):
     got_cache = kv_cache.cpu().numpy()
     assert np.array_equal(got_cache, ref_cache), f"decode store: {int((got_cache != ref_cache).sum())} bytes differ"
     ref = O.decode_attention(qd.float().numpy(), ref_cache, bt, np.asarray(full, np.int32), H, D, pn["kc"], pn["vc"],
-                             pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+                             pn["R"], 1.0 / math.sqrt(D), "bfloat16", kv_dtype=kv_dtype)
     err, excess, cs = check_tolerance(outd.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
-    print(f"decode {mode}{bits} fused={fused}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
+    print(f"decode {mode}{bits} {path}: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
     assert excess <= 0 and cs >= 0.999
 
 
-def _mixed_setup(monkeypatch, H, HQ, mode, bits, iso_mode, ctx, q_lens, cfg):
+def _mixed_setup(monkeypatch, H, HQ, mode, bits, iso_mode, ctx, q_lens, cfg, fused=True):
     """Impl + a cache holding every sequence's first ctx - q_len tokens (oracle store);
     the last q_len tokens of each sequence arrive in the forward call."""
     monkeypatch.setenv("RQ_MODE", mode)
@@ -111,7 +122,10 @@ def _mixed_setup(monkeypatch, H, HQ, mode, bits, iso_mode, ctx, q_lens, cfg):
     monkeypatch.setenv("RQ_ISO_MODE", iso_mode)
     monkeypatch.delenv("RQ_K_BITS", raising=False)
     monkeypatch.delenv("RQ_V_BITS", raising=False)
-    monkeypatch.setenv("RQ_USE_FUSED_PAGED", "1")
+    if fused:
+        monkeypatch.setenv("RQ_USE_FUSED_PAGED", "1")
+    else:
+        monkeypatch.delenv("RQ_USE_FUSED_PAGED", raising=False)
     from rotorquant_vllm.vllm.rq_backend import RQAttentionImpl
     impl = RQAttentionImpl(HQ, D, 1.0 / math.sqrt(D), num_kv_heads=H)
     p = Params(mode, bits, bits, iso_mode=iso_mode)
@@ -219,3 +233,60 @@ def test_backend_decode_step_graph_replay(monkeypatch):
                              pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
     _, excess, cs = check_tolerance(eager.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
     assert excess <= 0 and cs >= 0.999
+
+
+def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
+    """The default (non-fused) path: a mixed batch of decodes and chunks in one forward
+    is one rq_paged_attention launch, checked against the oracle of the reference's
+    non-fused path; then a decode step on the same path captured in a HIP graph
+    replays the eager output bit for bit (no host read of the metadata, no
+    workspace)."""
+    ctx = [3000, 700, 5, 800, 64]
+    q_lens = [1, 1, 1, 200, 64]
+    impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 73, fused=False)
+    assert not impl._fused_paged_available and not impl._fused_prefill_available
+    dev = torch.device("cuda")
+    kv_cache = torch.from_numpy(c["cache0"]).to(dev)
+    out = torch.empty(c["q"].shape, dtype=torch.bfloat16, device=dev)
+    impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
+    torch.cuda.synchronize()
+    got_cache = kv_cache.cpu().numpy()
+    assert np.array_equal(got_cache, c["full_cache"]), f"{int((got_cache != c['full_cache']).sum())} bytes differ"
+    pn = p.np()
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    ref = O.unfused_attention(c["q"].float().numpy(), cu, c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 4, D,
+                              pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+    err, excess, cs = check_tolerance(out.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)
+    print(f"unfused mixed: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}")
+    assert excess <= 0 and cs >= 0.999
+
+    # decode step (one new token for each of the first three sequences), captured
+    dctx = [3001, 701, 6]
+    bt = c["bt"][:3]
+    slots = [int(bt[b][(L - 1) // BS]) * BS + (L - 1) % BS for b, L in enumerate(dctx)]
+    md = _metadata(3, 1, slots, np.ascontiguousarray(bt), dctx, [1, 1, 1])
+    qd = torch.randn(3, 28, D, generator=gen(7306)).to(torch.bfloat16).to(dev)
+    kn = torch.randn(3, 4, D, generator=gen(7307)).to(torch.bfloat16).to(dev)
+    vn = torch.randn(3, 4, D, generator=gen(7308)).to(torch.bfloat16).to(dev)
+    outd = torch.empty_like(qd)
+
+    def step():
+        impl.forward(None, qd, kn, vn, kv_cache, md, output=outd)
+
+    step()
+    torch.cuda.synchronize()
+    eager = outd.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(3):
+        outd.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outd, eager), f"replay {i}"

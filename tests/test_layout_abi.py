@@ -83,7 +83,7 @@ class TestABI:
         assert set(syms) == set(_lib.EXPORTED)
 
     def test_version(self):
-        assert _lib.load().rq_abi_version() == 3
+        assert _lib.load().rq_abi_version() == 4
 
     def test_argument_validation_without_gpu(self):
         """Bad arguments are rejected before any device work, with a message."""
@@ -98,6 +98,14 @@ class TestABI:
         rc = lib.rq_fused_decode(None, 1, 1, 40, 0, 0, None, 1, 16, 0, 0, 2, 128, None, 1, 1, None, 16, None, 8,
                                  None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
         assert rc == 1 and b"integer <= 16" in lib.rq_last_error()
+        # rq_paged_attention: head_dim, GQA width, rotation block, centroid count
+        base = dict(q=None, dtype=1, total_q=1, hq=32, qst=0, qsh=0, cu=None, ns=1, mq=1, causal=1, kv=None, nb=1,
+                    bs=16, sb=0, st=0, h=8, d=128, bt=None, mb=1, bss=1, sl=None, kc=None, nk=8, vc=None, nv=8,
+                    r=None, rb=4, sm=0.1, out=None, ost=0, osh=0, stream=None)
+        for change, msg in ((dict(d=64), b"head_dim"), (dict(hq=136), b"integer <= 16"), (dict(rb=8), b"rot_block"),
+                            (dict(nk=17), b"centroid"), (dict(dtype=2), b"dtype")):
+            rc = lib.rq_paged_attention(*{**base, **change}.values())
+            assert rc == 1 and msg in lib.rq_last_error(), change
         with pytest.raises(ValueError):
             _lib.check(1, "x")
 

@@ -263,3 +263,87 @@ def test_planted_missing_scale_is_caught(monkeypatch):
     monkeypatch.setattr(O, "_scores", lambda qr, K, sm_scale: qr @ K.T)
     assert check_two_keys() > 1e-3
     assert check_decode_vs_sdpa(_decode_case()) > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# unfused_attention: the non-fused path (K/V decompressed to the q dtype)
+# ---------------------------------------------------------------------------
+
+def check_unfused_vs_sdpa(case, causal: bool) -> float:
+    """unfused_attention_rot's math against float64 SDPA over K/V rounded by torch's
+    own cast of the dequantized values (the pages flash attention reads)."""
+    p = case["p"]
+    pn = p.np()
+    got = O.prefill_attention_rot(case["q"].float().numpy(), case["cu"], case["cache"], case["bt"], case["lens"],
+                                  case["H"], D, pn["kc"], pn["vc"], pn["R"], case["sm_scale"], "bfloat16",
+                                  causal=causal, kv_dtype="bfloat16")
+    err = 0.0
+    G = case["HQ"] // case["H"]
+    for b in range(len(case["lens"])):
+        s0, s1, L = int(case["cu"][b]), int(case["cu"][b + 1]), int(case["lens"][b])
+        K, V = torch_dequant(case["cache"], case["bt"][b], L, case["H"], pn["kc"], pn["vc"])
+        K, V = K.float().to(torch.bfloat16).double(), V.float().to(torch.bfloat16).double()
+        qr = torch_q_rot(case["q"][s0:s1], p.R)
+        T = s1 - s0
+        pos = [L - T + i for i in range(T)] if causal else [L - 1] * T
+        exp = sdpa_rot(qr, K, V, G, pos, case["sm_scale"]).numpy()
+        err = max(err, rel_err(got[s0:s1], exp))
+    return err
+
+
+def check_unfused_noncausal_rows_are_decodes(case) -> float:
+    """A non-causal row equals the decode oracle over the whole context (two code paths)."""
+    p = case["p"]
+    pn = p.np()
+    args = (case["H"], D, pn["kc"], pn["vc"], pn["R"], case["sm_scale"], "bfloat16")
+    full = O.prefill_attention_rot(case["q"].float().numpy(), case["cu"], case["cache"], case["bt"], case["lens"],
+                                   *args, causal=False, kv_dtype="bfloat16")
+    err = 0.0
+    for b in range(len(case["lens"])):
+        s0, s1, L = int(case["cu"][b]), int(case["cu"][b + 1]), int(case["lens"][b])
+        for i in sorted({0, (s1 - s0) // 2, s1 - s0 - 1}):
+            dec = O.decode_attention_rot(case["q"][s0 + i:s0 + i + 1].float().numpy(), case["cache"],
+                                         case["bt"][b:b + 1], np.asarray([L]), *args, kv_dtype="bfloat16")
+            err = max(err, rel_err(full[s0 + i], dec[0]))
+    return err
+
+
+def test_unfused_pages_equal_torch_cast():
+    case = _prefill_case()
+    pn = case["p"].np()
+    L = int(case["lens"][0])
+    K, V = O.gather_seq(case["cache"], case["bt"][0], L, case["H"], D, pn["kc"], pn["vc"], kv_dtype="bfloat16")
+    Kt, Vt = torch_dequant(case["cache"], case["bt"][0], L, case["H"], pn["kc"], pn["vc"])
+    assert np.array_equal(K, Kt.float().to(torch.bfloat16).double().numpy())
+    assert np.array_equal(V, Vt.float().to(torch.bfloat16).double().numpy())
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_unfused_matches_float64_sdpa(causal):
+    assert check_unfused_vs_sdpa(_prefill_case(), causal) < 1e-10
+
+
+def test_unfused_noncausal_rows_equal_decodes():
+    assert check_unfused_noncausal_rows_are_decodes(_prefill_case()) < 1e-12
+
+
+def test_unfused_entry_is_the_rounded_pages_path():
+    """unfused_attention == prefill_attention with kv_dtype = the q dtype."""
+    case = _prefill_case()
+    pn = case["p"].np()
+    args = (case["q"].float().numpy(), case["cu"], case["cache"], case["bt"], case["lens"], case["H"], D, pn["kc"],
+            pn["vc"], pn["R"], case["sm_scale"], "bfloat16")
+    assert np.array_equal(O.unfused_attention(*args, causal=False),
+                          O.prefill_attention(*args, causal=False, kv_dtype="bfloat16"))
+
+
+def test_planted_unrounded_pages_are_caught(monkeypatch):
+    monkeypatch.setattr(O, "decompress", lambda p, n, c, dt: O.decompress_f32(p, n, c))
+    assert check_unfused_vs_sdpa(_prefill_case(), True) > 1e-4
+
+
+def test_planted_noncausal_truncation_is_caught(monkeypatch):
+    """A non-causal mask that drops keys (here: the last 40) fails the SDPA check."""
+    orig = O._visible
+    monkeypatch.setattr(O, "_visible", lambda pos, L: orig(np.minimum(np.asarray(pos), L - 40), L))
+    assert check_unfused_vs_sdpa(_prefill_case(), False) > 1e-3
