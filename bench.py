@@ -56,9 +56,13 @@ def config1_lens(B=64, cfg=1):
     return torch.randint(1024, 8192 + 1, (B,), generator=torch.Generator().manual_seed(1000 * cfg + 4)).tolist()
 
 
-def decode_bytes(lens, H, HQ, D, BS):
+def decode_bytes(lens, H, HQ, D, BS, dense3=False):
+    """Algorithmic bytes of one decode call: each token's K/V payload once (136 B per
+    head at D 128; 104 B in the dense 3-bit layout), the block-table entries, q and
+    out, the lengths."""
     B = len(lens)
-    return (sum(lens) * 136 * H * D // 128 + sum((L + BS - 1) // BS for L in lens) * 4 + B * HQ * D * 2 * 2 + 4 * B)
+    per_head = (104 if dense3 else 136) * D // 128
+    return (sum(lens) * per_head * H + sum((L + BS - 1) // BS for L in lens) * 4 + B * HQ * D * 2 * 2 + 4 * B)
 
 
 def time_decode(inp, steps, warmup, graphs=False):
@@ -87,7 +91,8 @@ def time_decode(inp, steps, warmup, graphs=False):
     outs = [torch.empty_like(inp["q"]) for _ in range(n)]
 
     launchers = [K.fused_paged_rq_decode_launcher(inp["q"], caches[i], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
-                                                  inp["D"], inp["BS"], out=outs[i], max_seq_len=max_len, workspace=ws)
+                                                  inp["D"], inp["BS"], out=outs[i], max_seq_len=max_len, workspace=ws,
+                                                  dense3=inp.get("dense3", False))
                  for i in range(n)]
 
     def call(i):
@@ -243,6 +248,23 @@ def time_mixed_cfg4(steps=5):
     ops = 2 * causal_macs(q_lens, ctx, 28)
     out = dict(chunks=4, prefix_tokens=pre, us=round(ms * 1e3, 1),
                algorithmic_TOPS=round(ops / (ms * 1e-3) / 1e12, 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
+def decode_config1_dense3(steps=20):
+    """Config 1's decode batch with the cache in the opt-in dense 3-bit layout
+    (RQ_DENSE_3BIT: 104 payload bytes per token and head instead of 136), same
+    tokens and queries as the headline line; GB/s on the dense layout's bytes."""
+    import torch
+    lens = config1_lens()
+    inp = build_decode_inputs(lens, dense3=True)
+    t, _ = time_decode(inp, steps, 5)
+    nb = decode_bytes(lens, 8, 32, 128, 16, dense3=True)
+    gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
+    out = dict(us=round(t["avg_ms"] * 1e3, 1), algorithmic_bytes=int(nb), GBps=round(gbs, 1),
+               pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2), decode_tok_per_s=round(len(lens) / (t["avg_ms"] * 1e-3), 1))
     del inp
     torch.cuda.empty_cache()
     return out
@@ -547,7 +569,7 @@ def main():
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
-                                       "config0", "config4_forward", "unfused1", "unfused3"],
+                                       "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -565,7 +587,8 @@ def main():
               "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4,
               "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
               "config0": config0_roundtrip, "config4_forward": time_config4_one_forward,
-              "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3)}[args.only]
+              "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3),
+              "decode1_dense3": decode_config1_dense3}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -621,6 +644,7 @@ def main():
         result["decode_config4"] = decode_config(4)
         result["prefill_config4_chunks"] = time_mixed_cfg4()
         result["config4_one_forward"] = time_config4_one_forward()
+        result["decode_config1_dense3"] = decode_config1_dense3()
         result["unfused_config1_decode"] = time_unfused(1)
         result["unfused_config3_prefill"] = time_unfused(3)
     if not args.no_cpu_baseline:

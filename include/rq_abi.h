@@ -34,8 +34,8 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 4  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
-                              4: rq_paged_attention */
+#define RQ_ABI_VERSION 5  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
+                              4: rq_paged_attention; 5: index_layout on the entry points that touch slots */
 
 enum rq_status {
     RQ_OK = 0,
@@ -48,6 +48,27 @@ enum rq_dtype {
     RQ_DTYPE_F16 = 0,
     RQ_DTYPE_BF16 = 1,
     RQ_DTYPE_F32 = 2
+};
+
+/*
+ * Index layout of the packed cache (the `index_layout` argument of every entry
+ * point that reads or writes cache slots):
+ *   RQ_INDEX_NIBBLE: the reference's slot, head_dim / 2 index bytes per head,
+ *     byte j = idx[2j] << 4 | idx[2j + 1] (rq_backend.py:155-188);
+ *   RQ_INDEX_DENSE3: opt-in, 3-bit indices only (8-entry codebooks, head_dim a
+ *     multiple of 32): 3 head_dim / 8 bytes per head, each 32 indices of dims
+ *     32G .. 32G+31 in 12 bytes (dwords A, B, C; byte k of each):
+ *       A[k] = i[2k]    | i[2k+1] << 3  | (i[24+2k] & 3) << 6
+ *       B[k] = i[8+2k]  | i[9+2k] << 3  | (i[25+2k] & 3) << 6
+ *       C[k] = i[16+2k] | i[17+2k] << 3 | (i[24+2k] >> 2) << 6 | (i[25+2k] >> 2) << 7
+ *     The slot is [K idx | K norms | V idx | V norms | pad] as before, with the
+ *     smaller index parts (104 payload bytes per head at head_dim 128 instead of
+ *     136).  No counterpart in the reference, whose roadmap lists 3-bit storage
+ *     (PKG-INFO:110).
+ */
+enum rq_index_layout {
+    RQ_INDEX_NIBBLE = 0,
+    RQ_INDEX_DENSE3 = 1
 };
 
 /* Version of this ABI (RQ_ABI_VERSION). */
@@ -95,7 +116,7 @@ int rq_compress(const void *x, int32_t x_dtype, int64_t n_rows, int32_t head_dim
 int rq_compress_store(const void *key, const void *value, int32_t dtype, int64_t n_tokens,
                       int64_t k_stride_token, int64_t k_stride_head,
                       int64_t v_stride_token, int64_t v_stride_head,
-                      int32_t num_kv_heads, int32_t head_dim,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                       const int64_t *slot_mapping,
                       uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                       int64_t stride_block, int64_t stride_token, int32_t total_bytes,
@@ -139,7 +160,7 @@ int rq_decompress(const uint8_t *packed, const float *norms, int64_t n_rows, int
 int64_t rq_paged_decompress_workspace_bytes(int64_t num_blocks);
 int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                         int64_t stride_block, int64_t stride_token,
-                        int32_t num_kv_heads, int32_t head_dim,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                         const int32_t *block_table, int64_t num_seqs, int64_t max_blocks,
                         int64_t bt_stride_seq, const int32_t *seq_lens,
                         const float *k_centroids, int32_t n_k_centroids,
@@ -177,7 +198,7 @@ int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_
                     int64_t q_stride_seq, int64_t q_stride_head,
                     const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                     int64_t stride_block, int64_t stride_token,
-                    int32_t num_kv_heads, int32_t head_dim,
+                    int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                     const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
                     const int32_t *seq_lens, int64_t max_seq_len,
                     const float *k_centroids, int32_t n_k_centroids,
@@ -209,7 +230,7 @@ int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num_seqs, int3
                             int64_t q_stride_seq, int64_t q_stride_head,
                             const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                             int64_t stride_block, int64_t stride_token,
-                            int32_t num_kv_heads, int32_t head_dim,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                             const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
                             const int32_t *seq_lens, int64_t max_seq_len,
                             const float *k_centroids, int32_t n_k_centroids,
@@ -241,7 +262,7 @@ int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q
                     const int32_t *cu_seqlens_q, int64_t num_seqs, int64_t max_q_len,
                     const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                     int64_t stride_block, int64_t stride_token,
-                    int32_t num_kv_heads, int32_t head_dim,
+                    int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                     const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
                     const int32_t *seq_lens, int64_t max_seq_len,
                     const float *k_centroids, int32_t n_k_centroids,
@@ -285,7 +306,7 @@ int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q, int32_t nu
                        const int32_t *cu_seqlens_q, int64_t num_seqs, int64_t max_q_len, int32_t causal,
                        const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                        int64_t stride_block, int64_t stride_token,
-                       int32_t num_kv_heads, int32_t head_dim,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
                        const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
                        const int32_t *seq_lens,
                        const float *k_centroids, int32_t n_k_centroids,

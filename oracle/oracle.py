@@ -12,6 +12,9 @@ Restates the reference (tpurtell/rotorquant-vllm) on the CPU:
   lloyd_max_closed_form ........ src/rotorquant_vllm/quantization/lloyd_max.py:32-86
                                  (same schedule, exact Gaussian integrals)
   slot layout .................. src/rotorquant_vllm/vllm/rq_backend.py:155-188, :482-490
+  dense3_pack / _unpack ........ the opt-in dense 3-bit index layout (this build's own
+                                 format; the reference only lists it on its roadmap,
+                                 PKG-INFO:110)
   compress_store ............... rq_backend.py:585-657
   paged_decompress ............. rq_backend.py:737-852
   decode_attention ............. src/rotorquant_vllm/triton/fused_paged_rq_decode.py:252-312
@@ -37,6 +40,9 @@ Pins (what each function is checked against, besides the product):
     decode over the visible prefix; the q / out roundings against torch's
     own casts.  Mistakes planted through _kv_head, _visible and _scores
     (GQA map, mask offset, missing scale) fail these checks.
+  dense3_pack: a bit permutation (each of the 3 x 32 input bits of a group lands
+    on its own output bit, checked bit by bit) and unpack inverts it, on all
+    index values at every position (tests/test_oracle_golden.py).
   unfused_attention: K/V equal to torch's decompress-then-cast; a non-causal
     row equals the decode oracle over the whole context (two code paths);
     causal rows with fp32 K/V equal prefill_attention.
@@ -228,26 +234,93 @@ def lloyd_max_closed_form(d: int, bits: int, max_iter: int = 200, tol: float = 1
 # Slot layout (rq_backend.py:155-188, :482-490)
 # ---------------------------------------------------------------------------
 
-def slot_layout(num_kv_heads: int, head_dim: int) -> dict:
-    half = head_dim // 2
+def slot_layout(num_kv_heads: int, head_dim: int, dense3: bool = False) -> dict:
+    """Byte offsets of the slot [K idx | K norms | V idx | V norms | pad]
+    (rq_backend.py:155-188, :482-490); dense3: 3-bit indices in 3 D / 8 bytes
+    per head (dense3_pack) instead of D / 2."""
+    ib = 3 * head_dim // 8 if dense3 else head_dim // 2
     H = num_kv_heads
-    k_idx_end = H * half
+    k_idx_end = H * ib
     k_norm_end = k_idx_end + 4 * H
-    v_idx_end = k_norm_end + H * half
+    v_idx_end = k_norm_end + H * ib
     v_norm_end = v_idx_end + 4 * H
-    per_head = 1 << (2 * (half + 4) - 1).bit_length()  # next_power_of_2(136) = 256
+    per_head = 1 << (2 * (ib + 4) - 1).bit_length()  # next_power_of_2(136) = 256 (dense: 104 -> 128)
     return dict(k_idx_end=k_idx_end, k_norm_end=k_norm_end, v_idx_end=v_idx_end,
-                v_norm_end=v_norm_end, total_bytes=H * per_head)
+                v_norm_end=v_norm_end, total_bytes=H * per_head, index_bytes=ib)
 
 
-def compress_store(cache: np.ndarray, slot_mapping: np.ndarray, k_packed, k_norms, v_packed, v_norms) -> None:
+# ---------------------------------------------------------------------------
+# Dense 3-bit index layout (opt-in, no counterpart in the reference)
+# ---------------------------------------------------------------------------
+# 32 indices i[0..31] of a head (dims 32G .. 32G+31) -> 12 bytes: dwords A, B, C,
+# byte k (k = 0..3) of each:
+#   A[k] = i[2k]      | i[2k+1] << 3  | (i[24+2k] & 3) << 6
+#   B[k] = i[8+2k]    | i[9+2k] << 3  | (i[25+2k] & 3) << 6
+#   C[k] = i[16+2k]   | i[17+2k] << 3 | (i[24+2k] >> 2) << 6 | (i[25+2k] >> 2) << 7
+
+def nibbles_to_indices(packed: np.ndarray) -> np.ndarray:
+    """(..., D/2) nibble-packed bytes -> (..., D) indices (byte j = idx[2j] << 4 | idx[2j+1])."""
+    p = np.asarray(packed, np.uint8)
+    return np.stack([p >> 4, p & 15], axis=-1).reshape(*p.shape[:-1], 2 * p.shape[-1])
+
+
+def indices_to_nibbles(idx: np.ndarray) -> np.ndarray:
+    i = np.asarray(idx, np.uint8)
+    return ((i[..., 0::2] << 4) | i[..., 1::2]).astype(np.uint8)
+
+
+def dense3_pack(packed: np.ndarray) -> np.ndarray:
+    """(..., D/2) nibble-packed 3-bit indices -> (..., 3 D / 8) dense bytes."""
+    i = nibbles_to_indices(packed).astype(np.uint8)
+    if i.max(initial=0) > 7:
+        raise ValueError("dense 3-bit layout needs indices < 8")
+    g = i.reshape(*i.shape[:-1], -1, 32)
+    k2 = 2 * np.arange(4)
+    A = g[..., k2] | g[..., k2 + 1] << 3 | (g[..., 24 + k2] & 3) << 6
+    B = g[..., 8 + k2] | g[..., 9 + k2] << 3 | (g[..., 25 + k2] & 3) << 6
+    C = g[..., 16 + k2] | g[..., 17 + k2] << 3 | (g[..., 24 + k2] >> 2) << 6 | (g[..., 25 + k2] >> 2) << 7
+    out = np.concatenate([A, B, C], axis=-1).astype(np.uint8)  # (..., groups, 12)
+    return out.reshape(*i.shape[:-1], -1)
+
+
+def dense3_unpack(dense: np.ndarray) -> np.ndarray:
+    """(..., 3 D / 8) dense bytes -> (..., D/2) nibble-packed indices."""
+    d = np.asarray(dense, np.uint8)
+    g = d.reshape(*d.shape[:-1], -1, 12)
+    A, B, C = g[..., 0:4], g[..., 4:8], g[..., 8:12]
+    idx = np.zeros((*g.shape[:-1], 32), np.uint8)
+    k2 = 2 * np.arange(4)
+    idx[..., k2], idx[..., k2 + 1] = A & 7, (A >> 3) & 7
+    idx[..., 8 + k2], idx[..., 9 + k2] = B & 7, (B >> 3) & 7
+    idx[..., 16 + k2], idx[..., 17 + k2] = C & 7, (C >> 3) & 7
+    idx[..., 24 + k2] = (A >> 6) | ((C >> 6) & 1) << 2
+    idx[..., 25 + k2] = (B >> 6) | ((C >> 7) & 1) << 2
+    return indices_to_nibbles(idx.reshape(*d.shape[:-1], -1))
+
+
+def dense3_cache_to_nibbles(cache: np.ndarray, num_kv_heads: int, head_dim: int) -> np.ndarray:
+    """A dense-3-bit cache -> the nibble-layout cache holding the same tokens (same
+    indices and norms), so that the attention oracles read it unchanged."""
+    NB, BS, _ = cache.shape
+    kp, kn, vp, vn = read_slots(cache, num_kv_heads, head_dim, dense3=True)
+    lay = slot_layout(num_kv_heads, head_dim)
+    out = np.zeros((NB, BS, lay["total_bytes"]), np.uint8)
+    compress_store(out, np.arange(NB * BS), kp, kn, vp, vn)
+    return out
+
+
+def compress_store(cache: np.ndarray, slot_mapping: np.ndarray, k_packed, k_norms, v_packed, v_norms,
+                   dense3: bool = False) -> None:
     """Assemble rows [K idx | K norms | V idx | V norms | 0] and scatter (rq_backend.py:609-657).
 
     cache: (NB, BS, total_bytes) uint8, modified in place.  Slots < 0 are
-    skipped (the reference would wrap them to the last slot).
+    skipped (the reference would wrap them to the last slot).  k_packed /
+    v_packed are nibble-packed; dense3 stores them in the dense 3-bit layout.
     """
     N, H, half = k_packed.shape
-    lay = slot_layout(H, 2 * half)
+    lay = slot_layout(H, 2 * half, dense3)
+    if dense3:
+        k_packed, v_packed = dense3_pack(k_packed), dense3_pack(v_packed)
     rows = np.zeros((N, cache.shape[-1]), np.uint8)
     rows[:, :lay["k_idx_end"]] = k_packed.reshape(N, -1)
     rows[:, lay["k_idx_end"]:lay["k_norm_end"]] = np.ascontiguousarray(k_norms.reshape(N, H), np.float32).view(np.uint8)
@@ -260,16 +333,20 @@ def compress_store(cache: np.ndarray, slot_mapping: np.ndarray, k_packed, k_norm
             flat[s] = rows[t]
 
 
-def read_slots(cache: np.ndarray, num_kv_heads: int, head_dim: int):
-    """Split a (NB, BS, total_bytes) cache into per-token K/V packed indices and norms."""
+def read_slots(cache: np.ndarray, num_kv_heads: int, head_dim: int, dense3: bool = False):
+    """Split a (NB, BS, total_bytes) cache into per-token K/V packed indices (nibble
+    layout; a dense3 cache is unpacked) and norms."""
     NB, BS, TB = cache.shape
-    H, half = num_kv_heads, head_dim // 2
-    lay = slot_layout(H, head_dim)
+    H = num_kv_heads
+    lay = slot_layout(H, head_dim, dense3)
+    ib = lay["index_bytes"]
     flat = cache.reshape(NB * BS, TB)
-    kp = flat[:, :lay["k_idx_end"]].reshape(-1, H, half)
+    kp = flat[:, :lay["k_idx_end"]].reshape(-1, H, ib)
     kn = np.ascontiguousarray(flat[:, lay["k_idx_end"]:lay["k_norm_end"]]).view(np.float32).reshape(-1, H, 1)
-    vp = flat[:, lay["k_norm_end"]:lay["v_idx_end"]].reshape(-1, H, half)
+    vp = flat[:, lay["k_norm_end"]:lay["v_idx_end"]].reshape(-1, H, ib)
     vn = np.ascontiguousarray(flat[:, lay["v_idx_end"]:lay["v_norm_end"]]).view(np.float32).reshape(-1, H, 1)
+    if dense3:
+        kp, vp = dense3_unpack(kp), dense3_unpack(vp)
     return kp, kn, vp, vn
 
 

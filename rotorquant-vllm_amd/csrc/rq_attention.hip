@@ -90,6 +90,7 @@ struct AttnArgs {
     int block_size, bs_shift;
     int64_t num_blocks;
     int H, G;
+    int dense3;  // dense 3-bit index layout of the cache
     int hsplit;  // workgroups per kv head: each takes G / hsplit query heads
     const int32_t *bt;
     int64_t bt_ss, max_blocks;
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
         ktab[tid] = tid < a.nkc ? a.kc[tid] : 0.f;
         vtab[tid] = tid < a.nvc ? a.vc[tid] : 0.f;
     }
-    const SlotLayout SL(a.H, kD);
+    const SlotLayout SL(a.H, kD, a.dense3 != 0);
     const uint32_t lds0 = lds_addr(lds);
     uint64_t *soff = reinterpret_cast<uint64_t *>(lds + kSOff);
 
@@ -178,17 +179,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
     auto stage = [&]() {
         for (int c = wave; c < kCopies; c += nwaves) {
             int key, byte_off, dst;
+            bool on = true;
             if (c < 32) {  // index dwords: keys 4 (c % 16) + lane / 16, dword lane % 16
                 const bool isk = c < 16;
                 key = 4 * (c & 15) + (lane >> 4);
-                byte_off = (isk ? SL.k_idx : SL.v_idx) + h * 64 + 4 * (lane & 15);
+                byte_off = (isk ? SL.k_idx : SL.v_idx) + h * SL.ib + 4 * (lane & 15);
                 dst = (isk ? kSKi : kSVi) + (c & 15) * 256;
+                on = 4 * (lane & 15) < SL.ib;  // the dense layout has 12 index dwords per head
             } else {  // norms: key = lane
                 key = lane;
                 byte_off = (c == 32 ? SL.k_norm : SL.v_norm) + 4 * h;
                 dst = c == 32 ? kSKn : kSVn;
             }
-            copy4(a.cache + soff[key] + byte_off, __builtin_amdgcn_readfirstlane(lds0 + dst));
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + dst);
+            if (on) copy4(a.cache + soff[key] + byte_off, m0);
         }
     };
     // Returns the tile's V exponent e: 2^e above its largest v norm, clamped to
@@ -209,7 +213,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * kq + i;
-                    const uint32_t x = *reinterpret_cast<const uint32_t *>(lds + kSKi + r * 64 + 4 * dw);
+                    const uint32_t x = idx_dword(lds + kSKi + r * 64, dw, a.dense3 != 0);
                     const float nrm = r < nk ? kn[r] : 0.f;
                     uint32_t wd[4];
 #pragma unroll
@@ -230,7 +234,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
                 float nrm[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    x[i] = *reinterpret_cast<const uint32_t *>(lds + kSVi + (t0 + i) * 64 + 4 * dw);
+                    x[i] = idx_dword(lds + kSVi + (t0 + i) * 64, dw, a.dense3 != 0);
                     nrm[i] = t0 + i < nk ? vn[t0 + i] : 0.f;
                 }
 #pragma unroll
@@ -356,7 +360,8 @@ extern "C" int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q,
                                   int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
                                   int64_t num_seqs, int64_t max_q_len, int32_t causal, const uint8_t *kv_cache,
                                   int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
-                                  int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                                  const int32_t *block_table,
                                   int64_t max_blocks, int64_t bt_stride_seq, const int32_t *seq_lens,
                                   const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                                   int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
@@ -371,6 +376,8 @@ extern "C" int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q,
     RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0 &&
                      num_blocks >= 0,
                  "bad sizes");
+    const int lrc = check_index_layout(index_layout, head_dim, n_k_centroids, n_v_centroids);
+    if (lrc) return lrc;
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache slots must be 4-byte aligned");
     RQ_CHECK_ARG(((uintptr_t)q % 16) == 0 && (q_stride_tok * 2) % 16 == 0 && (q_stride_head * 2) % 16 == 0,
@@ -393,6 +400,7 @@ extern "C" int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q,
     a.num_blocks = num_blocks;
     a.H = num_kv_heads;
     a.G = num_q_heads / num_kv_heads;
+    a.dense3 = index_layout == RQ_INDEX_DENSE3;
     a.bt = block_table;
     a.bt_ss = bt_stride_seq;
     a.max_blocks = max_blocks;

@@ -27,19 +27,74 @@ int check_launch(const char *what);
 
 // ---------------------------------------------------------------------------
 // Packed slot layout: [K idx | K norms | V idx | V norms | pad]
-// (reference: src/rotorquant_vllm/vllm/rq_backend.py:155-188, :482-490)
+// (reference: src/rotorquant_vllm/vllm/rq_backend.py:155-188, :482-490).
+// Index bytes per head: D / 2 (nibbles, the reference's layout) or, with the
+// opt-in dense 3-bit layout, 3 D / 8 (see below).
 // ---------------------------------------------------------------------------
 struct SlotLayout {
     int32_t H, D, half;
+    int32_t ib;  // index bytes per head
     int32_t k_idx, k_norm, v_idx, v_norm, payload;
-    __host__ __device__ SlotLayout(int32_t h, int32_t d) : H(h), D(d), half(d / 2) {
+    __host__ __device__ SlotLayout(int32_t h, int32_t d, bool dense3 = false)
+        : H(h), D(d), half(d / 2), ib(dense3 ? 3 * d / 8 : d / 2) {
         k_idx = 0;
-        k_norm = H * half;
+        k_norm = H * ib;
         v_idx = k_norm + 4 * H;
-        v_norm = v_idx + H * half;
+        v_norm = v_idx + H * ib;
         payload = v_norm + 4 * H;
     }
 };
+
+// ---------------------------------------------------------------------------
+// Dense 3-bit index layout (opt-in; no counterpart in the reference, which
+// lists 3-bit storage on its roadmap only).  The 32 indices i[0..31] of dims
+// 32G .. 32G+31 of a head take 12 bytes, dwords A, B, C; byte k (k = 0..3):
+//   A[k] = i[2k]    | i[2k+1] << 3  | (i[24+2k] & 3) << 6
+//   B[k] = i[8+2k]  | i[9+2k] << 3  | (i[25+2k] & 3) << 6
+//   C[k] = i[16+2k] | i[17+2k] << 3 | (i[24+2k] >> 2) << 6 | (i[25+2k] >> 2) << 7
+// so that position w < 3 of the group (dims 8w .. 8w+7) reads like a nibble
+// dword: one mask gives its even dims' indices one per byte (the selector a
+// v_perm lookup takes), a shift and a mask its odd dims'; position 3 gathers
+// its bits from the spare top bits of A, B and C.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint32_t d3_even(uint32_t x) { return x & 0x07070707u; }
+__host__ __device__ __forceinline__ uint32_t d3_odd(uint32_t x) { return (x >> 3) & 0x07070707u; }
+__host__ __device__ __forceinline__ uint32_t d3_even3(uint32_t a, uint32_t c) {
+    return ((a >> 6) & 0x03030303u) | ((c >> 4) & 0x04040404u);
+}
+__host__ __device__ __forceinline__ uint32_t d3_odd3(uint32_t b, uint32_t c) {
+    return ((b >> 6) & 0x03030303u) | ((c >> 5) & 0x04040404u);
+}
+// Nibble dword (byte k = i[8w+2k] << 4 | i[8w+2k+1]) of position w of a group.
+__host__ __device__ __forceinline__ uint32_t d3_nibbles(uint32_t a, uint32_t b, uint32_t c, int w) {
+    const uint32_t x = w == 0 ? a : (w == 1 ? b : c);
+    const uint32_t e = w < 3 ? d3_even(x) : d3_even3(a, c);
+    const uint32_t o = w < 3 ? d3_odd(x) : d3_odd3(b, c);
+    return (e << 4) | o;
+}
+// Host check of an index_layout argument against head_dim and the codebook sizes.
+inline int check_index_layout(int layout, int D, int n_k, int n_v) {
+    RQ_CHECK_ARG(layout == RQ_INDEX_NIBBLE || layout == RQ_INDEX_DENSE3, "index_layout %d unknown", layout);
+    if (layout == RQ_INDEX_DENSE3)
+        RQ_CHECK_ARG(D % 32 == 0 && n_k <= 8 && n_v <= 8,
+                     "the dense 3-bit layout needs head_dim %% 32 == 0 and at most 8 centroids / 7 boundaries "
+                     "(head_dim %d, %d and %d)", D, n_k, n_v);
+    return RQ_OK;
+}
+
+// The nibble dword of dims 8 dw .. 8 dw + 7 of a head whose index bytes start at
+// p (4-byte aligned): a plain load, or the dense group's dwords.
+__device__ __forceinline__ uint32_t idx_dword(const uint8_t *p, int dw, bool dense3) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+    if (!dense3) return q[dw];
+    const uint32_t *g = q + 3 * (dw >> 2);
+    const int w = dw & 3;
+    if (w < 3) {
+        const uint32_t x = g[w];
+        return (d3_even(x) << 4) | d3_odd(x);
+    }
+    return d3_nibbles(g[0], g[1], g[2], 3);
+}
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 

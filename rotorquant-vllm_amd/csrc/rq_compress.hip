@@ -66,6 +66,7 @@ struct RowMap {
     int32_t total_bytes;
     int32_t H;
     int32_t pad_vec;    // slot padding can be cleared with 16-byte stores
+    int32_t dense3;     // store mode: dense 3-bit index layout
 };
 
 // Per-row addresses, resolved once per workgroup.
@@ -337,8 +338,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compre
                 ref.src = reinterpret_cast<const uint8_t *>(is_v ? m.value : m.key) + off * EB;
                 base = slot_base(m, sid);
                 if (base != nullptr) {
-                    const SlotLayout L(m.H, D);
-                    ref.idx_dst = base + (is_v ? L.v_idx : L.k_idx) + h * half;
+                    const SlotLayout L(m.H, D, m.dense3 != 0);
+                    ref.idx_dst = base + (is_v ? L.v_idx : L.k_idx) + h * L.ib;
                     ref.norm_dst = reinterpret_cast<float *>(base + (is_v ? L.v_norm : L.k_norm) + 4 * h);
                 }
                 ref.is_v = is_v;
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compre
             }
         }
         if (m.store) {
-            const int pay = SlotLayout(m.H, D).payload;
+            const int pay = SlotLayout(m.H, D, m.dense3 != 0).payload;
             const int npad = misc[buf];
             uint8_t *const *pads = pads_all + buf * (kRows / 2);
             if (m.pad_vec) {
@@ -571,7 +572,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(compre
                     word |= idx << (8 * (e >> 1) + ((e & 1) ? 0 : 4));
                 }
             }
-            gbl(dst)[part] = word;
+            if (m.dense3) {
+                // Lanes 4G .. 4G+3 of the row hold positions 0..3 of index group G (dims
+                // 32G .. 32G+31); positions 0..2 write dwords A, B, C, topped up with
+                // position 3's bits.
+                const uint32_t x3 = __shfl(word, (lane & ~3) | 3);
+                const uint32_t e3 = (x3 >> 4) & 0x0f0f0f0fu, o3 = x3 & 0x0f0f0f0fu;
+                const int w = part & 3;
+                const uint32_t own = ((word >> 4) & 0x0f0f0f0fu) | ((word & 0x0f0f0f0fu) << 3);
+                const uint32_t top = w == 0 ? (e3 & 0x03030303u) << 6
+                                   : w == 1 ? (o3 & 0x03030303u) << 6
+                                            : (((e3 >> 2) & 0x01010101u) << 6) | (((o3 >> 2) & 0x01010101u) << 7);
+                if (w < 3) gbl(dst)[3 * (part >> 2) + w] = own | top;
+            } else {
+                gbl(dst)[part] = word;
+            }
         }
         if (!has_next) break;
         g = gn;
@@ -675,7 +690,7 @@ extern "C" int rq_compress(const void *x, int32_t x_dtype, int64_t n_rows, int32
 extern "C" int rq_compress_store(const void *key, const void *value, int32_t dtype, int64_t n_tokens,
                                  int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_token,
                                  int64_t v_stride_head, int32_t num_kv_heads, int32_t head_dim,
-                                 const int64_t *slot_mapping, uint8_t *kv_cache, int64_t num_blocks,
+                                 int32_t index_layout, const int64_t *slot_mapping, uint8_t *kv_cache, int64_t num_blocks,
                                  int32_t block_size, int64_t stride_block, int64_t stride_token,
                                  int32_t total_bytes, const float *rot_t_even, const float *rot_t_odd,
                                  int32_t rot_block, const float *k_boundaries, int32_t n_k_boundaries,
@@ -683,10 +698,13 @@ extern "C" int rq_compress_store(const void *key, const void *value, int32_t dty
     int rc = check_common(dtype, head_dim, rot_block, n_k_boundaries, n_v_boundaries);
     if (rc) return rc;
     RQ_CHECK_ARG(num_kv_heads >= 1 && n_tokens >= 0 && block_size >= 1 && num_blocks >= 0, "bad sizes");
+    rc = check_index_layout(index_layout, head_dim, n_k_boundaries + 1, n_v_boundaries + 1);
+    if (rc) return rc;
     if (n_tokens == 0) return RQ_OK;
     RQ_CHECK_ARG(key && value && slot_mapping && kv_cache && rot_t_even && rot_t_odd && k_boundaries && v_boundaries,
                  "null pointer");
-    SlotLayout L(num_kv_heads, head_dim);
+    const bool dense3 = index_layout == RQ_INDEX_DENSE3;
+    SlotLayout L(num_kv_heads, head_dim, dense3);
     RQ_CHECK_ARG(total_bytes >= L.payload && total_bytes % 4 == 0, "total_bytes %d < payload %d or not 4-aligned",
                  total_bytes, L.payload);
     RQ_CHECK_ARG(stride_token >= total_bytes && stride_token % 4 == 0 && stride_block % 4 == 0,
@@ -713,6 +731,7 @@ extern "C" int rq_compress_store(const void *key, const void *value, int32_t dty
     m.stride_token = stride_token;
     m.total_bytes = total_bytes;
     m.H = num_kv_heads;
+    m.dense3 = dense3;
     m.pad_vec = L.payload % 16 == 0 && total_bytes % 16 == 0 && stride_token % 16 == 0 && stride_block % 16 == 0 &&
                 ((uintptr_t)kv_cache % 16) == 0;
     int64_t n_rows = n_tokens * 2 * num_kv_heads;

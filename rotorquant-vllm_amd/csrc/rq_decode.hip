@@ -93,11 +93,20 @@ __device__ __forceinline__ Table16 make_table(const Centroids &cv) {
 // One packed dword (8 nibbles, coordinates e0..e7 of one token) -> MFMA
 // operand of 8 16-bit values in the order e0 e2 e4 e6 e1 e3 e5 e7.
 template <int BITS>
-__device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
-    uint32_t odd = x & 0x0f0f0f0fu;          // e1 e3 e5 e7
-    uint32_t even = (x >> 4) & 0x0f0f0f0fu;  // e0 e2 e4 e6
+__device__ __forceinline__ u32x4 decode_row8_sel(const Table16 &t, uint32_t even, uint32_t odd) {
     uint2 e = lookup4<BITS>(t, even), o = lookup4<BITS>(t, odd);
     return u32x4{e.x, e.y, o.x, o.y};
+}
+template <int BITS>
+__device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
+    return decode_row8_sel<BITS>(t, (x >> 4) & 0x0f0f0f0fu, x & 0x0f0f0f0fu);  // e0 e2 e4 e6 | e1 e3 e5 e7
+}
+
+// Value of lane (l & ~3) + perm[l & 3] of the lane's quad (DPP quad_perm, ctrl =
+// perm[0] | perm[1] << 2 | perm[2] << 4 | perm[3] << 6).
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_pick(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
 }
 
 struct TileDesc;
@@ -122,7 +131,7 @@ struct DecodeArgs {
     int max_len;        // min(max_blocks * block_size, max_seq_len): lengths are clamped to it
     int64_t num_blocks; // physical blocks; table entries outside [0, num_blocks) read block 0
     int hpw;            // kv heads per workgroup = waves per workgroup (divides H, <= 8)
-    int tok_stride;     // LDS bytes per staged token: 128 * hpw (K and V indices) + 16 (bank skew)
+    int tok_stride;     // LDS bytes per staged token: 2 * index bytes * hpw (K and V indices) + 16 (bank skew)
     int stage_bytes;    // LDS bytes per stage: kTile * tok_stride + 2 * hpw * kTile * 4 (norms)
     int grid_w;         // decode workgroups per kv-head group (the tile ranges)
     int split_c;        // workgroups per rank: workgroup w has rank min(w / split_c, 3)
@@ -452,7 +461,8 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
 // Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
 constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
 
-template <int DT, int KB, int VB, int HPW>
+// D3: the cache holds the dense 3-bit index layout (48 index bytes per head).
+template <int DT, int KB, int VB, int HPW, bool D3>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
     const int w = blockIdx.x;
     const int NT = *a.n_tiles_total;
@@ -469,8 +479,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int col = lane & 15;  // MFMA column (query head inside the GQA group) / row
     const int h0 = blockIdx.z * hpw;
     const int h = h0 + wave;
-    const SlotLayout SL(a.H, kD);
-    const int TS = HPW > 0 ? 128 * HPW + 16 : a.tok_stride;
+    const SlotLayout SL(a.H, kD, D3);
+    constexpr int IB = D3 ? 48 : 64;  // index bytes per head
+    const int TS = HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride;
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
     const int tl = lane & 31;  // token of this lane in a tile (slot base, norm copy)
@@ -497,11 +508,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         const int valid = __builtin_amdgcn_readfirstlane(d.valid);
         const uint64_t base = d.off[lane_now() & 31];
         const uint32_t dst = lds_addr(sb);
-        const uint32_t kv_src = lane < 4 * hpw ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * lane)
-                                               : (uint32_t)(SL.v_idx + 64 * h0 + 16 * (lane - 4 * hpw));
+        constexpr int PH = IB / 16;  // 16-byte pieces per head
+        const uint32_t kv_src = lane < PH * hpw ? (uint32_t)(SL.k_idx + IB * h0 + 16 * lane)
+                                                : (uint32_t)(SL.v_idx + IB * h0 + 16 * (lane - PH * hpw));
         for (int tt = wave; tt < valid; tt += hpw) {
             const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
-            if (lane < 8 * hpw) copy16(tok, kv_src, dst + tt * TS);
+            if (lane < 2 * PH * hpw) copy16(tok, kv_src, dst + tt * TS);
         }
         if constexpr (HPW > 0) {
             // Norms in 16-byte pieces: a token's K norms and V norms of the hpw heads
@@ -641,11 +653,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             begin_segment();
         }
         // ---- this wave's operands of the tile ------------------------------------
-        const uint8_t *kb = sb + col * TS + 64 * wave + 16 * g;                 // token col, K bytes 16g..
-        const uint8_t *vb = sb + 4 * g * TS + 64 * hpw + 64 * wave + 4 * col;  // token 4g, V dword col
+        // token col, K dims 32g .. 32g+31 (16 nibble bytes, or the 12-byte dense group g)
+        const uint8_t *kb = sb + col * TS + IB * wave + (D3 ? 12 : 16) * g;
+        // token 4g, V dims 8 col .. 8 col + 7: nibble dword col; dense: dword min(col % 4, 2)
+        // of group col / 4 (position 3 is assembled from the quad's other three lanes)
+        const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave +
+                            (D3 ? 12 * (col >> 2) + 4 * min(col & 3, 2) : 4 * col);
         const uint8_t *nb = sb + norm_off + 128 * wave + 16 * g;               // K norms of tokens 4g..4g+3
-        const uint4 kw0 = *reinterpret_cast<const uint4 *>(kb);
-        const uint4 kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
+        uint4 kw0, kw1;
+        if constexpr (D3) {
+            const uint32_t *k0p = reinterpret_cast<const uint32_t *>(kb);
+            const uint32_t *k1p = reinterpret_cast<const uint32_t *>(kb + 16 * TS);
+            kw0 = make_uint4(k0p[0], k0p[1], k0p[2], 0u);
+            kw1 = make_uint4(k1p[0], k1p[1], k1p[2], 0u);
+        } else {
+            kw0 = *reinterpret_cast<const uint4 *>(kb);
+            kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
+        }
         uint32_t vw[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
@@ -724,7 +748,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
 
         // ---- S^T = K Q^T ----------------------------------------------------
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
-        {
+        if constexpr (D3) {
+            // dense group (A, B, C): positions 0..2 from their own dword, 3 from the top bits
+            const uint32_t a0[3] = {kw0.x, kw0.y, kw0.z}, a1[3] = {kw1.x, kw1.y, kw1.z};
+    #pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t e0 = c < 3 ? d3_even(a0[c]) : d3_even3(a0[0], a0[2]);
+                const uint32_t o0 = c < 3 ? d3_odd(a0[c]) : d3_odd3(a0[1], a0[2]);
+                const uint32_t e1 = c < 3 ? d3_even(a1[c]) : d3_even3(a1[0], a1[2]);
+                const uint32_t o1 = c < 3 ? d3_odd(a1[c]) : d3_odd3(a1[1], a1[2]);
+                s0 = mfma<RQ_DTYPE_F16>(decode_row8_sel<KB>(tk, e0, o0), qop[c], s0);
+                s1 = mfma<RQ_DTYPE_F16>(decode_row8_sel<KB>(tk, e1, o1), qop[c], s1);
+            }
+        } else {
             const uint32_t k0w[4] = {kw0.x, kw0.y, kw0.z, kw0.w};
             const uint32_t k1w[4] = {kw1.x, kw1.y, kw1.z, kw1.w};
     #pragma unroll
@@ -784,10 +820,29 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                           perm(B23, B01, 0x07060302u)};
         uint32_t Gb[4] = {perm(A67, A45, 0x05040100u), perm(A67, A45, 0x07060302u), perm(B67, B45, 0x05040100u),
                           perm(B67, B45, 0x07060302u)};
+        // Index selectors (one index per byte) of dims 8r + 2j (even) and 8r + 2j + 1 (odd).
+        // Dense: lanes of positions 0..2 mask their own bytes; the position-3 lane takes
+        // the top bits of its quad's A, B and C lanes (same tokens): one form for all
+        // lanes, (x >> s1) & m1 | (y >> s2) & m2, with per-lane shifts and masks.
+        auto sel = [&](uint32_t G, uint32_t &ev, uint32_t &od) {
+            if constexpr (D3) {
+                const bool p3 = (col & 3) == 3;
+                const uint32_t xe = quad_pick<0x24>(G), xo = quad_pick<0x64>(G), y = quad_pick<0xa4>(G);
+                const uint32_t m1 = p3 ? 0x03030303u : 0x07070707u, m2 = p3 ? 0x04040404u : 0u;
+                ev = ((xe >> (p3 ? 6 : 0)) & m1) | ((y >> 4) & m2);
+                od = ((xo >> (p3 ? 6 : 3)) & m1) | ((y >> 5) & m2);
+            } else {
+                ev = (G >> 4) & 0x0f0f0f0fu;
+                od = G & 0x0f0f0f0fu;
+            }
+        };
     #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint2 ha = lookup4<VB>(tv, (Ga[j] >> 4) & 0x0f0f0f0fu), hb = lookup4<VB>(tv, (Gb[j] >> 4) & 0x0f0f0f0fu);
-            uint2 la = lookup4<VB>(tv, Ga[j] & 0x0f0f0f0fu), lb = lookup4<VB>(tv, Gb[j] & 0x0f0f0f0fu);
+            uint32_t ea, oa, eb, ob;
+            sel(Ga[j], ea, oa);
+            sel(Gb[j], eb, ob);
+            uint2 ha = lookup4<VB>(tv, ea), hb = lookup4<VB>(tv, eb);
+            uint2 la = lookup4<VB>(tv, oa), lb = lookup4<VB>(tv, ob);
             acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // dim 8r + 2j
             acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // dim 8r + 2j + 1
         }
@@ -891,7 +946,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
 
 // Resident decode workgroups per CU for an LDS size (cached per device and size).
-template <int DT, int KB, int VB, int HPW>
+template <int DT, int KB, int VB, int HPW, bool D3>
 static int decode_per_cu(const DecodeArgs &a, size_t lds) {
     static int cache[64][8][2] = {};  // [device][entry] = {lds, workgroups per CU}
     int dev = 0;
@@ -900,7 +955,7 @@ static int decode_per_cu(const DecodeArgs &a, size_t lds) {
     for (auto &e : cache[dev])
         if (e[0] == (int)lds && e[1] > 0) return e[1];
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW>),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW, D3>),
                                                       64 * a.hpw, lds) != hipSuccess || nb <= 0)
         nb = 1;
     nb = std::min(nb, kMaxWgPerCu);
@@ -915,15 +970,15 @@ static int decode_per_cu(const DecodeArgs &a, size_t lds) {
 
 // configure: set the grid and range split only (before the prep kernel, which
 // needs them); otherwise launch.
-template <int DT, int KB, int VB, int HPW>
+template <int DT, int KB, int VB, int HPW, bool D3>
 static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
     if (!configure) {
-        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw),
+        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw),
                            lds, st, a);
         return;
     }
     // as many workgroups per kv-head group as are resident at once
-    const int per_cu = decode_per_cu<DT, KB, VB, HPW>(a, lds);
+    const int per_cu = decode_per_cu<DT, KB, VB, HPW, D3>(a, lds);
     const int groups = a.H / a.hpw;
     a.grid_w = std::max(1, per_cu * device_cus() / groups);
     // rank weights by workgroups per CU (workgroups [r CUs, (r+1) CUs) are
@@ -940,16 +995,18 @@ static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool conf
     a.split_r = UINT64_MAX / tot;
 }
 
-template <int DT, int KB, int VB>
+template <int DT, int KB, int VB, bool D3 = false>
 static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
-    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8>(a, lds, st, configure);
-    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4>(a, lds, st, configure);
-    else launch_decode_h<DT, KB, VB, 0>(a, lds, st, configure);
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3>(a, lds, st, configure);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3>(a, lds, st, configure);
+    else launch_decode_h<DT, KB, VB, 0, D3>(a, lds, st, configure);
 }
 
 template <int DT>
-static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, hipStream_t st, bool configure) {
-    if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st, configure);
+static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, bool dense3, hipStream_t st,
+                               bool configure) {
+    if (dense3) launch_decode<DT, 3, 3, true>(a, lds, st, configure);  // the layout holds 3-bit indices only
+    else if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st, configure);
     else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st, configure);
     else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st, configure);
     else launch_decode<DT, 4, 4>(a, lds, st, configure);
@@ -986,7 +1043,8 @@ extern "C" int64_t rq_fused_decode_workspace_bytes(int64_t num_seqs, int32_t num
 static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
                              int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
                              int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
-                             int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                             const int32_t *block_table, int64_t max_blocks,
                              int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
                              const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                              int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
@@ -996,14 +1054,16 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
 extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
                                int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
                                int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
-                               int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                             const int32_t *block_table, int64_t max_blocks,
                                int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
                                const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                                int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
                                void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
                                int64_t workspace_bytes, void *stream) {
     return fused_decode_impl(q, dtype, num_seqs, num_q_heads, q_stride_seq, q_stride_head, kv_cache, num_blocks,
-                             block_size, stride_block, stride_token, num_kv_heads, head_dim, block_table, max_blocks,
+                             block_size, stride_block, stride_token, num_kv_heads, head_dim, index_layout, block_table,
+                             max_blocks,
                              bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids, v_centroids,
                              n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq, out_stride_head,
                              workspace, workspace_bytes, stream);
@@ -1051,7 +1111,8 @@ extern "C" int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num
                                        int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
                                        int64_t num_blocks, int32_t block_size, int64_t stride_block,
                                        int64_t stride_token, int32_t num_kv_heads, int32_t head_dim,
-                                       const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                                       int32_t index_layout, const int32_t *block_table, int64_t max_blocks,
+                                       int64_t bt_stride_seq,
                                        const int32_t *seq_lens, int64_t max_seq_len, const float *k_centroids,
                                        int32_t n_k_centroids, const float *v_centroids, int32_t n_v_centroids,
                                        const float *rotation, int32_t rot_block, float sm_scale, void *out,
@@ -1067,7 +1128,8 @@ extern "C" int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num
     void *ws = device_scratch();
     if (ws == nullptr) return RQ_ELAUNCH;
     return fused_decode_impl(q, dtype, num_seqs, num_q_heads, q_stride_seq, q_stride_head, kv_cache, num_blocks,
-                             block_size, stride_block, stride_token, num_kv_heads, head_dim, block_table, max_blocks,
+                             block_size, stride_block, stride_token, num_kv_heads, head_dim, index_layout, block_table,
+                             max_blocks,
                              bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids, v_centroids,
                              n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq, out_stride_head, ws,
                              RQ_DECODE_SCRATCH_BYTES, stream);
@@ -1077,7 +1139,8 @@ extern "C" int rq_fused_decode_noalloc(const void *q, int32_t dtype, int64_t num
 static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
                              int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
                              int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
-                             int32_t num_kv_heads, int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                             const int32_t *block_table, int64_t max_blocks,
                              int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
                              const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                              int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
@@ -1093,6 +1156,9 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
                  "centroid counts must be 8 or 16");
     RQ_CHECK_ARG(rot_block == 2 || rot_block == 4, "rot_block %d must be 2 or 4", rot_block);
     RQ_CHECK_ARG(num_seqs >= 0 && max_seq_len >= 0 && block_size >= 1 && max_blocks >= 0, "bad sizes");
+    const int lrc = check_index_layout(index_layout, head_dim, n_k_centroids, n_v_centroids);
+    if (lrc) return lrc;
+    const bool dense3 = index_layout == RQ_INDEX_DENSE3;
     RQ_CHECK_ARG(max_seq_len <= max_blocks * block_size, "max_seq_len exceeds block table capacity");
     RQ_CHECK_ARG(stride_token % 16 == 0 && stride_block % 16 == 0 && ((uintptr_t)kv_cache % 16) == 0,
                  "cache slots must be 16-byte aligned");
@@ -1147,7 +1213,7 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
             a.hpw = d;
             break;
         }
-    a.tok_stride = 128 * a.hpw + 16;
+    a.tok_stride = 2 * SlotLayout(num_kv_heads, head_dim, dense3).ib * a.hpw + 16;
     a.stage_bytes = kTile * a.tok_stride + 2 * a.hpw * kTile * 4;
     a.max_len = num_blocks > 0 ? (int)std::min<int64_t>(max_blocks * block_size, max_seq_len) : 0;
     a.out = out;
@@ -1160,8 +1226,8 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
     const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * (a.G * 256 + 64);
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, true);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st, true);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, true);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, true);
         // Descriptor workgroups per sequence (y >= 1): enough that each thread writes at
         // most two steps of four tokens of the longest sequence (a fixed three made the
         // prep kernel of a 131072-token sequence take ~49 us).
@@ -1174,8 +1240,8 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
         else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, plds, st, a);
         int rc = check_launch("decode_prep_kernel");
         if (rc) return rc;
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, st, false);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, st, false);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, false);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, false);
         rc = check_launch("decode_kernel");
         if (rc) return rc;
     }

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const uint8_t *__restrict__
                                                      const int32_t *__restrict__ compact, int64_t capacity,
                                                      const float *__restrict__ kc, int nkc,
                                                      const float *__restrict__ vc, int nvc, void *out_k,
-                                                     void *out_v) {
+                                                     void *out_v, int dense3) {
     __shared__ float cbk[16], cbv[16];
     const int64_t p = blockIdx.x;
     if (threadIdx.x < 16) {
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const uint8_t *__restrict__
     if (!flag[p]) return;
     const int64_t c = compact[p];
     if (c >= capacity) return;
-    SlotLayout L(H, D);
+    SlotLayout L(H, D, dense3 != 0);
     // Rows are (component, token, head); a row has D / 8 packed dwords.  The launch
     // uses a multiple of D / 8 threads, so each thread keeps one dword position w and
     // steps over rows: one division (by H) per row instead of three per dword.
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const uint8_t *__restrict__
         const int rr = r - comp * rows_per_comp;
         const int tok = (int)((uint32_t)rr / (uint32_t)H), h = rr - tok * H;
         const uint8_t *slot = cache + p * stride_block + (int64_t)tok * stride_token;
-        uint32_t word = reinterpret_cast<const uint32_t *>(slot + (comp ? L.v_idx : L.k_idx) + h * L.half)[w];
+        const uint32_t word = idx_dword(slot + (comp ? L.v_idx : L.k_idx) + h * L.ib, w, dense3 != 0);
         float norm = *reinterpret_cast<const float *>(slot + (comp ? L.v_norm : L.k_norm) + 4 * h);
         float v[8];
         unpack8(word, comp ? cbv : cbk, norm, v);
@@ -220,7 +220,8 @@ extern "C" int64_t rq_paged_decompress_workspace_bytes(int64_t num_blocks) {
 
 extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
                                    int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
-                                   int32_t head_dim, const int32_t *block_table, int64_t num_seqs,
+                                   int32_t head_dim, int32_t index_layout, const int32_t *block_table,
+                                   int64_t num_seqs,
                                    int64_t max_blocks, int64_t bt_stride_seq, const int32_t *seq_lens,
                                    const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                                    int32_t n_v_centroids, void *out_k, void *out_v, int32_t out_dtype,
@@ -231,6 +232,8 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
                  "bad sizes");
     RQ_CHECK_ARG(n_k_centroids >= 1 && n_k_centroids <= 16 && n_v_centroids >= 1 && n_v_centroids <= 16,
                  "centroid counts must be 1..16");
+    const int lrc = check_index_layout(index_layout, head_dim, n_k_centroids, n_v_centroids);
+    if (lrc) return lrc;
     RQ_CHECK_ARG(out_dtype == RQ_DTYPE_F16 || out_dtype == RQ_DTYPE_BF16 || out_dtype == RQ_DTYPE_F32,
                  "bad out_dtype %d", out_dtype);
     RQ_CHECK_ARG(workspace_bytes >= rq_paged_decompress_workspace_bytes(num_blocks), "workspace too small");
@@ -255,7 +258,8 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
 #define RQ_EXPAND(DT)                                                                                              \
     hipLaunchKernelGGL(expand_kernel<DT>, dim3((unsigned)num_blocks), dim3(ethreads), 0, st, kv_cache, block_size, \
                        stride_block, stride_token, num_kv_heads, head_dim, flag, compact, capacity_blocks,         \
-                       k_centroids, n_k_centroids, v_centroids, n_v_centroids, out_k, out_v)
+                       k_centroids, n_k_centroids, v_centroids, n_v_centroids, out_k, out_v,                      \
+                       index_layout == RQ_INDEX_DENSE3)
                 case RQ_DTYPE_F16: RQ_EXPAND(RQ_DTYPE_F16); break;
                 case RQ_DTYPE_BF16: RQ_EXPAND(RQ_DTYPE_BF16); break;
                 default: RQ_EXPAND(RQ_DTYPE_F32); break;

@@ -69,6 +69,7 @@ struct PrefillArgs {
     int block_size, bs_shift;
     int64_t num_blocks;
     int H, G, HQ;
+    int dense3;         // dense 3-bit index layout of the cache
     const int32_t *bt;
     int64_t bt_ss, max_blocks;
     const int32_t *seq_lens;
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     const int nk = min(kKT, L_eff - k0);
     const int tid = threadIdx.x;
     uint8_t *img = a.ws + (((int64_t)seq * a.H + h) * a.max_tiles + tile) * kImBytes;
-    const SlotLayout SL(a.H, kPD);
+    const SlotLayout SL(a.H, kPD, a.dense3 != 0);
     __shared__ uint64_t toff[kKT];
     const float kmax = codebook_max(a.kc, a.nkc);
 
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
     for (int w = tid; w < kKT * 16; w += 256) {
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
-        const uint32_t x = *reinterpret_cast<const uint32_t *>(a.cache + toff[tk] + SL.k_idx + h * 64 + 4 * dw);
+        const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
         const float rho = krho[tk];
         uint32_t hw[2], lw[2];  // [0]: even dims (high nibbles), [1]: odd dims (low nibbles)
 #pragma unroll
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         uint32_t x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            x[i] = *reinterpret_cast<const uint32_t *>(a.cache + toff[4 * tq + i] + SL.v_idx + h * 64 + 4 * dw);
+            x[i] = idx_dword(a.cache + toff[4 * tq + i] + SL.v_idx + h * SL.ib, dw, a.dense3 != 0);
         const int t0 = 4 * tq;
         const int b = t0 >> 4, gg = (t0 >> 2) & 3;
         const int piece = 4 * (b >> 1) + gg, elem_off = 8 * (b & 1);
@@ -450,8 +451,9 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
                                int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
                                int64_t num_seqs, int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks,
                                int32_t block_size, int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
-                               int32_t head_dim, const int32_t *block_table, int64_t max_blocks,
-                               int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
+                               int32_t head_dim, int32_t index_layout, const int32_t *block_table,
+                               int64_t max_blocks, int64_t bt_stride_seq, const int32_t *seq_lens,
+                               int64_t max_seq_len,
                                const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                                int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
                                void *out, int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
@@ -466,6 +468,8 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0 &&
                      max_seq_len >= 0,
                  "bad sizes");
+    const int lrc = check_index_layout(index_layout, head_dim, n_k_centroids, n_v_centroids);
+    if (lrc) return lrc;
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache slots must be 4-byte aligned");
     RQ_CHECK_ARG(((uintptr_t)q % 16) == 0 && (q_stride_tok * 2) % 16 == 0 && (q_stride_head * 2) % 16 == 0,
@@ -490,6 +494,7 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.H = num_kv_heads;
     a.G = num_q_heads / num_kv_heads;
     a.HQ = num_q_heads;
+    a.dense3 = index_layout == RQ_INDEX_DENSE3;
     a.bt = block_table;
     a.bt_ss = bt_stride_seq;
     a.max_blocks = max_blocks;

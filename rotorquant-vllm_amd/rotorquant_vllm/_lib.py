@@ -24,30 +24,29 @@ _SIGNATURES = {
     "rq_abi_version": (_c_i32, []),
     "rq_last_error": (ctypes.c_char_p, []),
     "rq_compress": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_p]),
-    "rq_compress_store": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32,
-                                   _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_i32,
-                                   _c_p, _c_i32, _c_p, _c_i32, _c_p]),
+    "rq_compress_store": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
+                                   _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_p,
+                                   _c_i32, _c_p, _c_i32, _c_p]),
     "rq_decompress": (_c_i32, [_c_p, _c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_p]),
     "rq_paged_decompress_workspace_bytes": (_c_i64, [_c_i64]),
-    "rq_paged_decompress": (_c_i32, [_c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
-                                     _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_p,
-                                     _c_p, _c_p, _c_i64, _c_p]),
+    "rq_paged_decompress": (_c_i32, [_c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64,
+                                     _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i64,
+                                     _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "rq_fused_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i64]),
-    "rq_fused_decode": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64,
-                                 _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i32, _c_p,
+    "rq_fused_decode": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64, _c_i64,
+                                 _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i32, _c_p,
                                  _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
-    "rq_fused_decode_noalloc": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32,
-                                         _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
+    "rq_fused_decode_noalloc": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64,
+                                         _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
                                          _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p]),
     "rq_int8_prefill_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i64]),
-    "rq_int8_prefill": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p,
-                                 _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p,
-                                 _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64,
-                                 _c_p, _c_i64, _c_p]),
-    "rq_paged_attention": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32,
-                                    _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
-                                    _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64,
-                                    _c_p]),
+    "rq_int8_prefill": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64,
+                                 _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64,
+                                 _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p, _c_i64,
+                                 _c_p]),
+    "rq_paged_attention": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_p,
+                                    _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
+                                    _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

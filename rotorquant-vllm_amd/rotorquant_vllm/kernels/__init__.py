@@ -104,6 +104,11 @@ def _f32(t: torch.Tensor, device) -> torch.Tensor:
     return t.to(device=device, dtype=torch.float32).contiguous()
 
 
+def _layout(dense3: bool) -> int:
+    """index_layout argument of the C ABI: RQ_INDEX_NIBBLE (0) or RQ_INDEX_DENSE3 (1)."""
+    return 1 if dense3 else 0
+
+
 # ---------------------------------------------------------------------------
 # Compress / decompress
 # ---------------------------------------------------------------------------
@@ -175,11 +180,12 @@ def planar_decompress(packed: torch.Tensor, norms: torch.Tensor, centroids: torc
 
 def compress_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
                    rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor, k_boundaries: torch.Tensor,
-                   v_boundaries: torch.Tensor, rot_block: int | None = None) -> None:
+                   v_boundaries: torch.Tensor, rot_block: int | None = None, dense3: bool = False) -> None:
     """Compress key/value (N, H, D) and write full slots of kv_cache (NB, BS, total_bytes).
 
     Replaces RQAttentionImpl._compress_and_store (rq_backend.py:585-657).
-    Slots < 0 are skipped.
+    Slots < 0 are skipped.  dense3: write the dense 3-bit index layout
+    (RQ_INDEX_DENSE3 in include/rq_abi.h; 3-bit codebooks only).
     """
     dev = _require_device(key, value, kv_cache, slot_mapping)
     N, H, D = key.shape
@@ -198,7 +204,7 @@ def compress_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tenso
     kb, vb = _f32(k_boundaries, dev), _f32(v_boundaries, dev)
     rc = _lib.load().rq_compress_store(
         key.data_ptr(), value.data_ptr(), _lib.dtype_code(key.dtype), N, key.stride(0), key.stride(1),
-        value.stride(0), value.stride(1), H, D, sm.data_ptr(), kv_cache.data_ptr(), NB, BS,
+        value.stride(0), value.stride(1), H, D, _layout(dense3), sm.data_ptr(), kv_cache.data_ptr(), NB, BS,
         kv_cache.stride(0), kv_cache.stride(1), TB, _f32(rot_T_even, dev).data_ptr(),
         _f32(rot_T_odd, dev).data_ptr(), blk, kb.data_ptr(), kb.numel(), vb.data_ptr(), vb.numel(),
         _lib.stream_ptr(dev))
@@ -212,14 +218,15 @@ def compress_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tenso
 def paged_decompress(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
                      num_kv_heads: int, head_dim: int, k_centroids: torch.Tensor, v_centroids: torch.Tensor,
                      dtype: torch.dtype, out_k: torch.Tensor | None = None, out_v: torch.Tensor | None = None,
-                     workspace: torch.Tensor | None = None):
+                     workspace: torch.Tensor | None = None, dense3: bool = False):
     """Decompress the physical blocks referenced by block_table.
 
     Returns (key_cache, value_cache, remapped_block_table, num_unique) with
     key/value of shape (capacity, BS, H, D); the first num_unique blocks hold
     the referenced physical blocks in ascending physical order, as the
     reference's _decompress_cache_paged (rq_backend.py:737-852).  num_unique is
-    a 1-element device int32 tensor (no host sync).
+    a 1-element device int32 tensor (no host sync).  dense3: the cache holds the
+    dense 3-bit index layout.
     """
     dev = _require_device(kv_cache, block_table, seq_lens)
     NB, BS, _ = kv_cache.shape
@@ -241,7 +248,7 @@ def paged_decompress(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens
     kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
     rc = _lib.load().rq_paged_decompress(
         kv_cache.data_ptr(), NB, BS, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
-        bt.data_ptr(), B, MB, bt.stride(0), sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(),
+        _layout(dense3), bt.data_ptr(), B, MB, bt.stride(0), sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(),
         vc.numel(), out_k.data_ptr(), out_v.data_ptr(), _lib.dtype_code(dtype), cap, remapped.data_ptr(),
         count.data_ptr(), workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "rq_paged_decompress")
@@ -274,7 +281,7 @@ def shared_workspace(device, kind: str, nbytes: int) -> torch.Tensor:
 
 
 def _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads,
-                       head_dim, block_size, sm_scale, out, max_seq_len, workspace):
+                       head_dim, block_size, sm_scale, out, max_seq_len, workspace, dense3=False):
     """Validated argument tuple of one rq_fused_decode call (tensors it creates are returned to keep them alive)."""
     num_seqs, H_Q, D = q.shape
     assert D == head_dim, f"D={D} != head_dim={head_dim}"
@@ -303,7 +310,8 @@ def _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroid
     sl = seq_lens.contiguous()
     args = (q.data_ptr(), _lib.dtype_code(q.dtype), num_seqs, H_Q, q.stride(0), q.stride(1), kv_cache.data_ptr(),
             kv_cache.shape[0], block_size, kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim,
-            block_table.data_ptr(), MB, block_table.stride(0), sl.data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(),
+            _layout(dense3), block_table.data_ptr(), MB, block_table.stride(0), sl.data_ptr(), max_seq_len,
+            kc.data_ptr(), kc.numel(),
             vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0),
             out.stride(1), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     return L, args, out, (q, block_table, R, kc, vc, sl, ws)
@@ -313,17 +321,20 @@ def fused_paged_rq_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: 
                           seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
                           rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
                           sm_scale: float | None = None, out: torch.Tensor | None = None,
-                          max_seq_len: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                          max_seq_len: int | None = None, workspace: torch.Tensor | None = None,
+                          dense3: bool = False) -> torch.Tensor:
     """Fused paged decode attention; q (num_seqs, H_Q, D) in original space -> output in original space.
 
     Reference: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312 (same
     arguments; `max_seq_len` optionally bounds seq_lens and sizes the split-KV
     grid, default block_table.shape[1] * block_size; `workspace` optionally
     supplies the scratch, a uint8 device tensor of at least
-    rq_fused_decode_workspace_bytes(...) bytes, reusable across calls).
+    rq_fused_decode_workspace_bytes(...) bytes, reusable across calls; dense3:
+    the cache holds the dense 3-bit index layout).
     """
     L, args, out, _keep = _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation,
-                                             num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace)
+                                             num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace,
+                                             dense3)
     _lib.check(L.rq_fused_decode(*args), "rq_fused_decode")
     return out
 
@@ -332,13 +343,15 @@ def fused_paged_rq_decode_launcher(q: torch.Tensor, kv_cache: torch.Tensor, bloc
                                    seq_lens: torch.Tensor, centroids_k: torch.Tensor, centroids_v: torch.Tensor,
                                    rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
                                    sm_scale: float | None = None, out: torch.Tensor | None = None,
-                                   max_seq_len: int | None = None, workspace: torch.Tensor | None = None):
+                                   max_seq_len: int | None = None, workspace: torch.Tensor | None = None,
+                                   dense3: bool = False):
     """Validate once and return a zero-argument callable that re-issues the same
     rq_fused_decode call (same buffers, the stream current now) without
     per-call Python work -- for loops over static buffers such as a benchmark.
     The callable returns `out`; the tensors must outlive it."""
     L, args, out, keep = _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation,
-                                            num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace)
+                                            num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace,
+                                            dense3)
     fn = L.rq_fused_decode
 
     def launch():
@@ -361,7 +374,7 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
                                 sm_scale: float | None = None, out: torch.Tensor | None = None,
                                 cu_seqlens_q: torch.Tensor | None = None,
                                 max_q_len: int | None = None, max_seq_len: int | None = None,
-                                workspace: torch.Tensor | None = None) -> torch.Tensor:
+                                workspace: torch.Tensor | None = None, dense3: bool = False) -> torch.Tensor:
     """Causal prefill attention from the packed cache with Q K^T and P V on int8 MFMA.
 
     Reference: src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:247-363.
@@ -371,7 +384,8 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
     there must be one sequence (as in the reference).
     max_seq_len bounds every seq_lens entry (default: the block table's capacity)
     and sizes the int8 tile-image workspace; workspace may be passed to reuse a
-    buffer of rq_int8_prefill_workspace_bytes bytes.
+    buffer of rq_int8_prefill_workspace_bytes bytes.  dense3: the cache holds the
+    dense 3-bit index layout.
     """
     num_tokens, H_Q, D = q.shape
     assert D == head_dim
@@ -411,7 +425,7 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
     rc = L.rq_int8_prefill(
         q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
         num_seqs, max_q_len, kv_cache.data_ptr(), kv_cache.shape[0], block_size, kv_cache.stride(0),
-        kv_cache.stride(1), num_kv_heads, head_dim, bt.data_ptr(), bt.shape[1], bt.stride(0),
+        kv_cache.stride(1), num_kv_heads, head_dim, _layout(dense3), bt.data_ptr(), bt.shape[1], bt.stride(0),
         seq_lens.contiguous().data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(),
         R.data_ptr(), blk, float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
         _lib.stream_ptr(dev))
@@ -427,7 +441,7 @@ def paged_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.
                     cu_seqlens_q: torch.Tensor, max_q_len: int, k_centroids: torch.Tensor,
                     v_centroids: torch.Tensor, rotation: torch.Tensor, num_kv_heads: int, head_dim: int,
                     block_size: int, sm_scale: float | None = None, causal: bool = True,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, dense3: bool = False) -> torch.Tensor:
     """Attention of the new query tokens over the packed cache, q and output in original space.
 
     The reference's non-fused path (rq_backend.py:937-1036: q_rot = q R^T cast to
@@ -436,7 +450,8 @@ def paged_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.
     q: (num_tokens, H_Q, D); cu_seqlens_q (num_seqs + 1,) int32; seq_lens
     (num_seqs,) int32 context lengths including the new tokens; max_q_len: a host
     int bounding every q_len (it sizes the grid).  Query i of sequence b sits at
-    position seq_lens[b] - q_len_b + i.
+    position seq_lens[b] - q_len_b + i.  dense3: the cache holds the dense 3-bit
+    index layout.
     """
     num_tokens, H_Q, D = q.shape
     assert D == head_dim
@@ -460,7 +475,8 @@ def paged_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.
     rc = L.rq_paged_attention(
         q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
         sl.numel(), int(max_q_len), 1 if causal else 0, kv_cache.data_ptr(), kv_cache.shape[0], block_size,
-        kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim, bt.data_ptr(), bt.shape[1], bt.stride(0),
+        kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim, _layout(dense3), bt.data_ptr(), bt.shape[1],
+        bt.stride(0),
         sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale),
         out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(dev))
     _lib.check(rc, "rq_paged_attention")

@@ -78,6 +78,16 @@ def _parse_kv_bits() -> tuple[int, int]:
     return k_bits, v_bits
 
 
+def _parse_dense3() -> bool:
+    """RQ_DENSE_3BIT=1 (opt-in, no counterpart in the reference): the dense 3-bit index
+    layout, 3 D / 8 index bytes per head instead of D / 2 (RQ_INDEX_DENSE3 in
+    include/rq_abi.h).  It holds 3-bit indices only."""
+    on = os.environ.get("RQ_DENSE_3BIT", "").lower() in ("1", "true", "yes")
+    if on and _parse_kv_bits() != (3, 3):
+        raise ValueError("RQ_DENSE_3BIT needs 3-bit K and V (RQ_BITS=3, RQ_K_BITS / RQ_V_BITS unset or 3)")
+    return on
+
+
 def _parse_iso_mode() -> str:
     mode = os.environ.get("RQ_ISO_MODE", "fast").lower()
     if mode not in ("fast", "full"):
@@ -151,9 +161,12 @@ def _accepted_keywords(fn) -> frozenset | None:
 def _call_hook(fn, *args, **kwargs):
     """fn(*args, **kwargs) with the keyword arguments fn does not accept left out; only
     the optional extras of this build (workspace, max_seq_len, cu_seqlens_q, max_q_len)
-    are ever dropped: the reference's own keywords are accepted by every hook."""
+    are ever dropped: the reference's own keywords are accepted by every hook.  A hook
+    that cannot read the dense 3-bit layout is refused when the cache holds it."""
     names = _accepted_keywords(fn)
     if names is not None:
+        if kwargs.get("dense3") and "dense3" not in names:
+            raise RuntimeError(f"{getattr(fn, '__name__', fn)} does not take the dense 3-bit cache (RQ_DENSE_3BIT)")
         kwargs = {k: v for k, v in kwargs.items() if k in names}
     return fn(*args, **kwargs)
 
@@ -167,23 +180,28 @@ def _next_power_of_2(n: int) -> int:
     return 1 << (n - 1).bit_length() if n > 0 else 1
 
 
-def _rq_bytes_per_component(head_dim: int, num_kv_heads: int) -> int:
-    """Nibble-packed indices (head_dim / 2 bytes) plus one fp32 norm, per head."""
-    return num_kv_heads * (head_dim // 2) + num_kv_heads * RQ_NORM_BYTES
+def _rq_index_bytes(head_dim: int, dense3: bool = False) -> int:
+    """Index bytes per head: nibbles (head_dim / 2), or the dense 3-bit layout (3 head_dim / 8)."""
+    return 3 * head_dim // 8 if dense3 else head_dim // 2
 
 
-def _rq_bytes_per_token_kv(head_dim: int, num_kv_heads: int) -> int:
-    """K + V payload per token (1088 B for 8 heads of 128)."""
-    return 2 * _rq_bytes_per_component(head_dim, num_kv_heads)
+def _rq_bytes_per_component(head_dim: int, num_kv_heads: int, dense3: bool = False) -> int:
+    """Packed indices plus one fp32 norm, per head."""
+    return num_kv_heads * _rq_index_bytes(head_dim, dense3) + num_kv_heads * RQ_NORM_BYTES
 
 
-def _rq_padded_slot_bytes(head_dim: int) -> int:
-    """Per-head slot share, padded to a power of two (256 B for head_dim 128)."""
-    return _next_power_of_2(_rq_bytes_per_token_kv(head_dim, 1))
+def _rq_bytes_per_token_kv(head_dim: int, num_kv_heads: int, dense3: bool = False) -> int:
+    """K + V payload per token (1088 B for 8 heads of 128; 832 B in the dense 3-bit layout)."""
+    return 2 * _rq_bytes_per_component(head_dim, num_kv_heads, dense3)
 
 
-def _rq_total_bytes(head_dim: int, num_kv_heads: int) -> int:
-    return num_kv_heads * _rq_padded_slot_bytes(head_dim)
+def _rq_padded_slot_bytes(head_dim: int, dense3: bool = False) -> int:
+    """Per-head slot share, padded to a power of two (256 B for head_dim 128; dense 3-bit: 128 B)."""
+    return _next_power_of_2(_rq_bytes_per_token_kv(head_dim, 1, dense3))
+
+
+def _rq_total_bytes(head_dim: int, num_kv_heads: int, dense3: bool = False) -> int:
+    return num_kv_heads * _rq_padded_slot_bytes(head_dim, dense3)
 
 
 # ---------------------------------------------------------------------------
@@ -331,7 +349,7 @@ class RQFullAttentionSpec(FullAttentionSpec):
 
     @property
     def real_page_size_bytes(self) -> int:  # noqa: D102
-        return self.block_size * _rq_total_bytes(self.head_size, self.num_kv_heads)
+        return self.block_size * _rq_total_bytes(self.head_size, self.num_kv_heads, _parse_dense3())
 
 
 # ---------------------------------------------------------------------------
@@ -408,7 +426,7 @@ class RQAttentionBackend(_BackendBase):
     def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
                            cache_dtype_str: str = "auto") -> tuple[int, ...]:
         """(num_blocks, block_size, total_bytes) uint8."""
-        return (num_blocks, block_size, _rq_total_bytes(head_size, num_kv_heads))
+        return (num_blocks, block_size, _rq_total_bytes(head_size, num_kv_heads, _parse_dense3()))
 
     @staticmethod
     def get_kv_cache_stride_order(include_num_layers_dimension: bool = False) -> tuple[int, ...]:
@@ -459,12 +477,16 @@ class RQAttentionImpl(_ImplBase):
         self._rq_rot_T_odd = self._rq_rot_T[:, 1::2].contiguous()
         self._rq_rot_block = 4 if rq_mode == "iso" else 2
         self._half_d = head_size // 2
+        self._dense3 = _parse_dense3()
+        if self._dense3 and head_size % 32:
+            raise ValueError(f"RQ_DENSE_3BIT needs head_size % 32 == 0 (got {head_size})")
+        ib = _rq_index_bytes(head_size, self._dense3)
 
-        self._k_idx_end = num_kv_heads * self._half_d
+        self._k_idx_end = num_kv_heads * ib
         self._k_norm_end = self._k_idx_end + num_kv_heads * RQ_NORM_BYTES
-        self._v_idx_end = self._k_norm_end + num_kv_heads * self._half_d
+        self._v_idx_end = self._k_norm_end + num_kv_heads * ib
         self._v_norm_end = self._v_idx_end + num_kv_heads * RQ_NORM_BYTES
-        self._total_bytes = _rq_total_bytes(head_size, num_kv_heads)
+        self._total_bytes = _rq_total_bytes(head_size, num_kv_heads, self._dense3)
 
         self._cg_buffers_ready = False
         self._max_model_len = vllm_config.model_config.max_model_len if vllm_config is not None else 8192
@@ -515,6 +537,11 @@ class RQAttentionImpl(_ImplBase):
                 _shared_workspace(dev, "prefill", lib.rq_int8_prefill_workspace_bytes(1, self.num_kv_heads, cap))
         self._cg_buffers_ready = True
 
+    def _layout_kw(self) -> dict:
+        """{"dense3": True} when the cache holds the dense 3-bit layout; else nothing, so
+        the kernel hooks are called exactly as the reference calls them."""
+        return {"dense3": True} if getattr(self, "_dense3", False) else {}
+
     def _launch_operands(self):
         """(K centroids, V centroids, R) for the kernel hooks: the device copies once
         _init_cg_buffers ran, else the quantizers' own tensors."""
@@ -530,7 +557,7 @@ class RQAttentionImpl(_ImplBase):
             raise RuntimeError("RotorQuant HIP kernels are not available")
         n = slot_mapping.shape[0]
         _compress_store_fn(key[:n], value[:n], kv_cache, slot_mapping, self._dev_rte, self._dev_rto,
-                           self._dev_kb, self._dev_vb, rot_block=self._rq_rot_block)
+                           self._dev_kb, self._dev_vb, rot_block=self._rq_rot_block, **self._layout_kw())
 
     # -- fused paths -----------------------------------------------------------
 
@@ -549,7 +576,7 @@ class RQAttentionImpl(_ImplBase):
                 n, query.shape[1], self.head_size, cap))
         _call_hook(_fused_paged_rq_decode_fn, query[:n], kv_cache, block_table, seq_lens, kc, vc, R,
                    self.num_kv_heads, self.head_size, BS, sm_scale=self.scale, out=output[:n], max_seq_len=cap,
-                   workspace=ws)
+                   workspace=ws, **self._layout_kw())
 
     def _prefill_groups(self, lens: list, q_lens: list, b0: int, BS: int, max_blocks: int, device):
         """Split sequences [b0, B) into contiguous groups whose tile images fit the
@@ -595,7 +622,7 @@ class RQAttentionImpl(_ImplBase):
             _call_hook(_fused_paged_rq_int8_prefill_fn, query[:num_actual_tokens], kv_cache, bt[g0:g1],
                        md.seq_lens[g0:g1], kc, vc, R, self.num_kv_heads, self.head_size, BS, sm_scale=self.scale,
                        out=output[:num_actual_tokens], cu_seqlens_q=md.query_start_loc[g0:g1 + 1], max_q_len=mq,
-                       max_seq_len=mx)
+                       max_seq_len=mx, **self._layout_kw())
         return output
 
     # -- non-fused path -----------------------------------------------------------
@@ -619,7 +646,8 @@ class RQAttentionImpl(_ImplBase):
             kc, vc, R = self._launch_operands()
             _paged_attention_fn(q, kv_cache, md.block_table, md.seq_lens, md.query_start_loc, int(max_q), kc, vc, R,
                                 self.num_kv_heads, self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                causal=bool(getattr(md, "causal", True)), out=output[:num_actual_tokens])
+                                causal=bool(getattr(md, "causal", True)), out=output[:num_actual_tokens],
+                                **self._layout_kw())
             return output
         return self._forward_unfused_torch(query, kv_cache, md, output, num_actual_tokens)
 
@@ -650,7 +678,7 @@ class RQAttentionImpl(_ImplBase):
         out_k = torch.empty(cap, BS, H, D, dtype=torch.float32, device=q.device)
         k_cache, v_cache, bt, _ = _paged_decompress_fn(kv_cache, md.block_table, md.seq_lens, H, D, self._dev_kc,
                                                        self._dev_vc, torch.float32, out_k=out_k,
-                                                       out_v=torch.empty_like(out_k))
+                                                       out_v=torch.empty_like(out_k), **self._layout_kw())
         out_rot = torch.zeros(num_actual_tokens, HQ, D, dtype=torch.float32, device=q.device)
         for b, L in enumerate(lens):
             s0, s1 = starts[b], starts[b + 1]
@@ -720,7 +748,8 @@ class RQAttentionImpl(_ImplBase):
                 kc, vc, R = self._launch_operands()
                 _call_hook(_fused_paged_rq_int8_prefill_fn, query[:num_actual_tokens], kv_cache,
                            attn_metadata.block_table, attn_metadata.seq_lens, kc, vc, R, self.num_kv_heads,
-                           self.head_size, kv_cache.shape[1], sm_scale=self.scale, out=output[:num_actual_tokens])
+                           self.head_size, kv_cache.shape[1], sm_scale=self.scale, out=output[:num_actual_tokens],
+                           **self._layout_kw())
                 return output
             return self._fused_batch(query, kv_cache, attn_metadata, output, num_actual_tokens)
 

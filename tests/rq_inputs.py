@@ -103,8 +103,9 @@ def lens_loguniform(B, lo, hi, cfg):
 
 
 def gpu_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=3, v_bits=3, iso_mode="fast",
-                      copies=3, kv="config0", kv_dtype="float16"):
-    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store.
+                      copies=3, kv="config0", kv_dtype="float16", dense3=False):
+    """Device inputs for a decode benchmark; the cache is filled by rq_compress_store
+    (dense3: in the dense 3-bit index layout).
 
     kv: "config0" K and V N(0,1) * (1 + |N(0,3)|) per (head, channel); "kscale"
     only K scaled that way, V N(0,1); "outlier" K N(0,1) with 4 seeded channels
@@ -114,7 +115,7 @@ def gpu_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=
     dev = torch.device("cuda")
     p = Params(mode, k_bits, v_bits, iso_mode=iso_mode, head_dim=D)
     bt, NB, slots = paged_layout(lens, BS, cfg)
-    total_bytes = 256 * H
+    total_bytes = (128 if dense3 else 256) * H
     cache = torch.zeros(NB, BS, total_bytes, dtype=torch.uint8, device=dev)
     slot_all = torch.from_numpy(np.concatenate(slots)).to(dev)
     g = torch.Generator(device=dev).manual_seed(1000 * cfg)
@@ -135,12 +136,12 @@ def gpu_decode_inputs(lens, H=8, HQ=32, D=128, BS=16, cfg=1, mode="iso", k_bits=
         n = min(chunk, slot_all.numel() - s)
         k = (torch.randn(n, H, D, generator=g, device=dev) * k_scale).to(kdt)
         v = (torch.randn(n, H, D, generator=g, device=dev) * v_scale).to(kdt)
-        K.compress_store(k, v, cache, slot_all[s:s + n], rte, rto, kb, vb, rot_block=p.blk)
+        K.compress_store(k, v, cache, slot_all[s:s + n], rte, rto, kb, vb, rot_block=p.blk, dense3=dense3)
     caches = [cache] + [cache.clone() for _ in range(copies - 1)]
     q = torch.randn(len(lens), HQ, D, generator=torch.Generator(device=dev).manual_seed(1000 * cfg + 6),
                     device=dev).to(torch.bfloat16)
     return dict(p=p, caches=caches, bt=torch.from_numpy(bt).to(dev), lens=torch.tensor(lens, dtype=torch.int32,
-                device=dev), q=q, H=H, HQ=HQ, D=D, BS=BS, lens_host=list(lens), bt_host=bt, NB=NB)
+                device=dev), q=q, H=H, HQ=HQ, D=D, BS=BS, lens_host=list(lens), bt_host=bt, NB=NB, dense3=dense3)
 
 
 def gpu_prefill_inputs(q_lens, ctx_lens, H, HQ, cfg, mode, bits, iso_mode="fast"):

@@ -17,8 +17,9 @@ from rq_inputs import (Params, gen, gpu_decode_inputs, gpu_prefill_inputs, host_
                        kv_config0, kv_outlier_k, kv_unit, lens_loguniform, lens_uniform, paged_layout)
 
 
-def build_cache_oracle(k, v, slot_ids, num_blocks, block_size, p: Params):
-    """Pack (N, H, D) K/V with the CPU oracle into a fresh (NB, BS, total_bytes) cache."""
+def build_cache_oracle(k, v, slot_ids, num_blocks, block_size, p: Params, dense3: bool = False):
+    """Pack (N, H, D) K/V with the CPU oracle into a fresh (NB, BS, total_bytes) cache
+    (dense3: the dense 3-bit index layout)."""
     N, H, D = k.shape
     dt = str(k.dtype).replace("torch.", "")
     kb, _ = O.to_bits(k)
@@ -26,8 +27,8 @@ def build_cache_oracle(k, v, slot_ids, num_blocks, block_size, p: Params):
     pn = p.np()
     kp, kn = O.compress(kb, dt, pn["rte"], pn["rto"], pn["kb"], p.blk)
     vp, vn = O.compress(vb, dt, pn["rte"], pn["rto"], pn["vb"], p.blk)
-    cache = np.zeros((num_blocks, block_size, _rq_total_bytes(D, H)), np.uint8)
-    O.compress_store(cache, slot_ids, kp, kn, vp, vn)
+    cache = np.zeros((num_blocks, block_size, _rq_total_bytes(D, H, dense3=dense3)), np.uint8)
+    O.compress_store(cache, slot_ids, kp, kn, vp, vn, dense3=dense3)
     return cache
 
 

@@ -34,7 +34,8 @@ class TestCacheLayout:
     def test_oracle_layout_agrees(self):
         import oracle as O
         lay = O.slot_layout(8, 128)
-        assert lay == dict(k_idx_end=512, k_norm_end=544, v_idx_end=1056, v_norm_end=1088, total_bytes=2048)
+        assert lay == dict(k_idx_end=512, k_norm_end=544, v_idx_end=1056, v_norm_end=1088, total_bytes=2048,
+                           index_bytes=64)
 
 
 class TestEnv:
@@ -83,7 +84,7 @@ class TestABI:
         assert set(syms) == set(_lib.EXPORTED)
 
     def test_version(self):
-        assert _lib.load().rq_abi_version() == 4
+        assert _lib.load().rq_abi_version() == 5
 
     def test_argument_validation_without_gpu(self):
         """Bad arguments are rejected before any device work, with a message."""
@@ -92,18 +93,23 @@ class TestABI:
         assert rc == 1 and b"dtype" in lib.rq_last_error()
         rc = lib.rq_compress(None, 0, 1, 100, None, None, 4, None, 7, None, None, None)
         assert rc == 1 and b"head_dim" in lib.rq_last_error()
-        rc = lib.rq_fused_decode(None, 1, 1, 32, 0, 0, None, 1, 16, 0, 0, 8, 64, None, 1, 1, None, 16, None, 8, None,
-                                 8, None, 4, 0.1, None, 0, 0, None, 0, None)
+        rc = lib.rq_fused_decode(None, 1, 1, 32, 0, 0, None, 1, 16, 0, 0, 8, 64, 0, None, 1, 1, None, 16, None, 8,
+                                 None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
         assert rc == 1 and b"head_dim" in lib.rq_last_error()
-        rc = lib.rq_fused_decode(None, 1, 1, 40, 0, 0, None, 1, 16, 0, 0, 2, 128, None, 1, 1, None, 16, None, 8,
+        rc = lib.rq_fused_decode(None, 1, 1, 40, 0, 0, None, 1, 16, 0, 0, 2, 128, 0, None, 1, 1, None, 16, None, 8,
                                  None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
         assert rc == 1 and b"integer <= 16" in lib.rq_last_error()
+        # the dense 3-bit layout takes 8-entry codebooks only
+        rc = lib.rq_fused_decode(None, 1, 1, 32, 0, 0, None, 1, 16, 0, 0, 8, 128, 1, None, 1, 1, None, 16, None, 16,
+                                 None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
+        assert rc == 1 and b"dense" in lib.rq_last_error()
         # rq_paged_attention: head_dim, GQA width, rotation block, centroid count
         base = dict(q=None, dtype=1, total_q=1, hq=32, qst=0, qsh=0, cu=None, ns=1, mq=1, causal=1, kv=None, nb=1,
-                    bs=16, sb=0, st=0, h=8, d=128, bt=None, mb=1, bss=1, sl=None, kc=None, nk=8, vc=None, nv=8,
-                    r=None, rb=4, sm=0.1, out=None, ost=0, osh=0, stream=None)
+                    bs=16, sb=0, st=0, h=8, d=128, il=0, bt=None, mb=1, bss=1, sl=None, kc=None, nk=8, vc=None,
+                    nv=8, r=None, rb=4, sm=0.1, out=None, ost=0, osh=0, stream=None)
         for change, msg in ((dict(d=64), b"head_dim"), (dict(hq=136), b"integer <= 16"), (dict(rb=8), b"rot_block"),
-                            (dict(nk=17), b"centroid"), (dict(dtype=2), b"dtype")):
+                            (dict(nk=17), b"centroid"), (dict(dtype=2), b"dtype"), (dict(il=1, nv=16), b"dense"),
+                            (dict(il=2), b"index_layout")):
             rc = lib.rq_paged_attention(*{**base, **change}.values())
             assert rc == 1 and msg in lib.rq_last_error(), change
         with pytest.raises(ValueError):

@@ -199,3 +199,63 @@ def test_param_device_env(monkeypatch):
     monkeypatch.setenv("RQ_PARAM_DEVICE", "gpu")
     with pytest.raises(ValueError, match="RQ_PARAM_DEVICE must be"):
         IsoQuantMSE(128, 3)
+
+
+# ---------------------------------------------------------------------------
+# Dense 3-bit index layout (opt-in; this build's own format)
+# ---------------------------------------------------------------------------
+
+def test_dense3_is_a_bit_permutation():
+    """Each of the 96 input bits of a 32-index group (index i, bit b) lands on exactly
+    one output bit, and no two on the same one: the layout loses nothing and
+    needs exactly 3 bits per index."""
+    seen = set()
+    for i in range(32):
+        for b in range(3):
+            idx = np.zeros(32, np.uint8)
+            idx[i] = 1 << b
+            out = O.dense3_pack(O.indices_to_nibbles(idx))
+            assert out.shape == (12,)
+            bits = np.unpackbits(out, bitorder="little")
+            assert bits.sum() == 1, (i, b)
+            pos = int(np.flatnonzero(bits)[0])
+            assert pos not in seen
+            seen.add(pos)
+    assert len(seen) == 96
+
+
+def test_dense3_round_trip_every_value_at_every_position():
+    rng = np.random.default_rng(5)
+    idx = rng.integers(0, 8, (64, 8, 128), dtype=np.uint8)
+    for v in range(8):  # every value at every position
+        idx[v] = v
+    nib = O.indices_to_nibbles(idx)
+    dense = O.dense3_pack(nib)
+    assert dense.shape == (64, 8, 48)
+    assert np.array_equal(O.dense3_unpack(dense), nib)
+    with pytest.raises(ValueError):
+        O.dense3_pack(O.indices_to_nibbles(np.full(32, 8, np.uint8)))
+
+
+def test_dense3_slot_layout_and_cache_round_trip():
+    lay = O.slot_layout(8, 128, dense3=True)
+    assert (lay["index_bytes"], lay["k_idx_end"], lay["k_norm_end"], lay["v_idx_end"], lay["v_norm_end"],
+            lay["total_bytes"]) == (48, 384, 416, 800, 832, 1024)
+    from rotorquant_vllm.vllm.rq_backend import _rq_total_bytes
+    assert _rq_total_bytes(128, 8, dense3=True) == 1024 and _rq_total_bytes(128, 8) == 2048
+    rng = np.random.default_rng(6)
+    N, H = 40, 4
+    kp = O.indices_to_nibbles(rng.integers(0, 8, (N, H, 128), dtype=np.uint8))
+    vp = O.indices_to_nibbles(rng.integers(0, 8, (N, H, 128), dtype=np.uint8))
+    kn = rng.standard_normal((N, H, 1)).astype(np.float32)
+    vn = rng.standard_normal((N, H, 1)).astype(np.float32)
+    cache = np.zeros((4, 16, O.slot_layout(H, 128, True)["total_bytes"]), np.uint8)
+    slots = rng.permutation(64)[:N]
+    O.compress_store(cache, slots, kp, kn, vp, vn, dense3=True)
+    rkp, rkn, rvp, rvn = O.read_slots(cache, H, 128, dense3=True)
+    assert np.array_equal(rkp[slots], kp) and np.array_equal(rvp[slots], vp)
+    assert np.array_equal(rkn[slots], kn) and np.array_equal(rvn[slots], vn)
+    nib = O.dense3_cache_to_nibbles(cache, H, 128)
+    ref = np.zeros((4, 16, O.slot_layout(H, 128)["total_bytes"]), np.uint8)
+    O.compress_store(ref, np.arange(64), rkp, rkn, rvp, rvn)
+    assert np.array_equal(nib, ref)

@@ -20,7 +20,8 @@ SCRATCH_BYTES = 256 << 20  # RQ_DECODE_SCRATCH_BYTES in include/rq_abi.h
 
 
 def _args(case, dev):
-    """Argument tuple shared by both entry points (everything but the workspace)."""
+    """Argument tuple shared by both entry points (everything but the workspace);
+    index layout 0 (nibbles)."""
     from rotorquant_vllm import _lib
     p = case["p"]
     t = dict(q=case["q"].to(dev), cache=torch.from_numpy(case["cache"]).to(dev),
@@ -31,7 +32,7 @@ def _args(case, dev):
     NB, BS, _ = t["cache"].shape
     max_len = int(case["lens"].max())
     head = (t["q"].data_ptr(), _lib.DTYPE_BF16, B, HQ, t["q"].stride(0), t["q"].stride(1), t["cache"].data_ptr(), NB,
-            BS, t["cache"].stride(0), t["cache"].stride(1), case["H"], D, t["bt"].data_ptr(), t["bt"].shape[1],
+            BS, t["cache"].stride(0), t["cache"].stride(1), case["H"], D, 0, t["bt"].data_ptr(), t["bt"].shape[1],
             t["bt"].stride(0), t["sl"].data_ptr(), max_len, t["kc"].data_ptr(), 8, t["vc"].data_ptr(), 8,
             t["R"].data_ptr(), p.blk, float(case["sm_scale"]))
     return t, head, max_len
@@ -74,8 +75,8 @@ def test_noalloc_refuses_oversize_without_launch():
     head = list(head)
     huge = 1 << 26  # 67 M tokens of max_seq_len: tile descriptors alone need > 256 MiB
     assert L.rq_fused_decode_workspace_bytes(2, 32, 128, huge) > SCRATCH_BYTES
-    head[17] = huge           # max_seq_len
-    head[14] = huge // 16     # max_blocks (the table is not read: the call is refused first)
+    head[18] = huge           # max_seq_len
+    head[15] = huge // 16     # max_blocks (the table is not read: the call is refused first)
     sentinel = t["out"].clone()
     rc = L.rq_fused_decode_noalloc(*head, t["out"].data_ptr(), t["out"].stride(0), t["out"].stride(1),
                                    _lib.stream_ptr(dev))
