@@ -20,6 +20,7 @@ the C ABI (include/rq_abi.h).  Differences, all deliberate:
 from __future__ import annotations
 
 import math
+import weakref
 
 import torch
 
@@ -58,7 +59,22 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
 # Rotation block structure (checked once per tensor)
 # ---------------------------------------------------------------------------
 
+# Keyed by tensor identity and checked against a weak reference to the tensor (a
+# new tensor that reuses a freed tensor's memory, or even its id, never sees the
+# old entry; entries are dropped when their tensor dies), with the tensor's
+# version counter to catch in-place writes.
 _block_cache: dict = {}
+
+
+def _cache_get(t: torch.Tensor):
+    ent = _block_cache.get(id(t))
+    return ent if ent is not None and ent[0]() is t and ent[1] == t._version else None
+
+
+def _cache_put(t: torch.Tensor, *vals):
+    key = id(t)
+    ref = weakref.ref(t, lambda _r, k=key: _block_cache.pop(k, None) if _block_cache.get(k, (None,))[0] is _r else None)
+    _block_cache[key] = (ref, t._version, *vals)
 
 
 def _block_of(RT: torch.Tensor) -> int:
@@ -76,28 +92,25 @@ def _block_of(RT: torch.Tensor) -> int:
 
 
 def rotation_block(rotation: torch.Tensor) -> int:
-    """Diagonal block width of a (D, D) rotation R (cached per tensor version)."""
-    key = ("R", rotation.data_ptr(), rotation._version, tuple(rotation.shape), str(rotation.device))
-    blk = _block_cache.get(key)
-    if blk is None:
-        blk = _block_of(rotation.detach().float().cpu())
-        _block_cache[key] = blk
-    return blk
+    """Diagonal block width of a (D, D) rotation R (checked once per tensor and version)."""
+    ent = _cache_get(rotation)
+    if ent is None:
+        _cache_put(rotation, _block_of(rotation.detach().float().cpu()))
+        ent = _cache_get(rotation)
+    return ent[2]
 
 
 def _rt_block(rot_T_even: torch.Tensor, rot_T_odd: torch.Tensor) -> int:
-    key = ("RT", rot_T_even.data_ptr(), rot_T_even._version, rot_T_odd.data_ptr(), rot_T_odd._version,
-           tuple(rot_T_even.shape), str(rot_T_even.device))
-    blk = _block_cache.get(key)
-    if blk is None:
+    ent = _cache_get(rot_T_even)
+    if ent is None or ent[3]() is not rot_T_odd or ent[4] != rot_T_odd._version:
         e, o = rot_T_even.detach().float().cpu(), rot_T_odd.detach().float().cpu()
         D = e.shape[0]
         RT = torch.empty(D, D)
         RT[:, 0::2] = e
         RT[:, 1::2] = o
-        blk = _block_of(RT)
-        _block_cache[key] = blk
-    return blk
+        _cache_put(rot_T_even, _block_of(RT), weakref.ref(rot_T_odd), rot_T_odd._version)
+        ent = _cache_get(rot_T_even)
+    return ent[2]
 
 
 def _f32(t: torch.Tensor, device) -> torch.Tensor:

@@ -30,7 +30,9 @@ import logging
 import os
 from dataclasses import dataclass
 from dataclasses import fields as dc_fields
+from fractions import Fraction
 
+import numpy as np
 import torch
 
 from rotorquant_vllm.quantization.isoquant import IsoQuantMSE
@@ -225,21 +227,62 @@ def _quat_right_conj(w, x, y, z) -> torch.Tensor:
                          [-z, -y, x, w]], dtype=torch.float32)
 
 
+def _round_f32(x: Fraction) -> float:
+    """x rounded to the nearest fp32 value (ties to even), from its exact value."""
+    c = np.float32(float(x))  # within one fp32 ulp of the answer
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        key = (abs(Fraction(float(cand)) - x), int(np.asarray(cand, np.float32).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, float(cand))
+    return best[1]
+
+
+def _block_product_f32(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """A @ B for small fp32 blocks in one fixed order: entry (i, j) is the fma chain
+    over k = 1, 2, ... starting from the rounded product A[i,0] * B[0,j], each step
+    computed exactly and rounded once.  That is the order of the fp32 sgemm that
+    produced the reference-side fixture (MKL on AVX-512); evaluated this way the
+    result is the same on every host and device, where torch's own matmul differs
+    by BLAS path."""
+    a = [[Fraction(float(v)) for v in row] for row in A.tolist()]
+    b = [[Fraction(float(v)) for v in row] for row in B.tolist()]
+    n, m, kk = len(a), len(b[0]), len(b)
+    out = torch.empty(n, m, dtype=torch.float32)
+    for i in range(n):
+        for j in range(m):
+            acc = _round_f32(a[i][0] * b[0][j])
+            for k in range(1, kk):
+                acc = _round_f32(a[i][k] * b[k][j] + Fraction(acc))
+            out[i, j] = acc
+    return out
+
+
+_iso_R_cache: dict = {}
+
+
 def _build_iso_R(quantizer, d: int, device, mode: str = "fast") -> torch.Tensor:
     """Block-diagonal R with 4x4 blocks: 'fast' v -> q_L v conj(q_L), 'full' v -> q_L v conj(q_R).
 
-    The fp32 4x4 block products are formed on the CPU (init-time, 32 blocks)
-    and R is then moved to `device`.
+    The fp32 4x4 block products (init-time, 32 blocks) are formed in a fixed
+    order on the host (_block_product_f32) and R is then moved to `device`, so R
+    and every cache byte written with it are the same on any machine.
     """
     qL = quantizer.q_L.detach().float().cpu()
     qR = quantizer.q_R.detach().float().cpu() if mode == "full" else qL
     D_pad = quantizer.d_padded
-    R = torch.eye(D_pad, dtype=torch.float32)
-    for g in range(quantizer.n_groups):
-        lw, lx, ly, lz = (float(v) for v in qL[g])
-        rw, rx, ry, rz = (float(v) for v in qR[g])
-        R[4 * g:4 * g + 4, 4 * g:4 * g + 4] = _quat_left(lw, lx, ly, lz) @ _quat_right_conj(rw, rx, ry, rz)
-    return R[:d, :d].contiguous().to(device)
+    key = (d, D_pad, qL.numpy().tobytes(), qR.numpy().tobytes())
+    R = _iso_R_cache.get(key)  # every layer draws the same seeded parameters
+    if R is None:
+        R = torch.eye(D_pad, dtype=torch.float32)
+        for g in range(quantizer.n_groups):
+            lw, lx, ly, lz = (float(v) for v in qL[g])
+            rw, rx, ry, rz = (float(v) for v in qR[g])
+            R[4 * g:4 * g + 4, 4 * g:4 * g + 4] = _block_product_f32(_quat_left(lw, lx, ly, lz),
+                                                                     _quat_right_conj(rw, rx, ry, rz))
+        R = R[:d, :d].contiguous()
+        _iso_R_cache[key] = R
+    return R.clone().to(device)
 
 
 def _build_planar_R(quantizer, d: int, device) -> torch.Tensor:

@@ -120,3 +120,20 @@ class TestABI:
         with pytest.raises(RuntimeError, match="no CPU path"):
             K.iso_decompress(torch.zeros(1, 1, 64, dtype=torch.uint8), torch.ones(1, 1, 1), torch.zeros(8),
                              torch.float16)
+
+
+def test_rotation_block_cache_is_per_tensor_object():
+    """Two tensor objects over the same memory (as when a freed R's memory is reused
+    by the next one) each get their own block width: the cache is keyed by the
+    tensor object, not by its address."""
+    from rotorquant_vllm import kernels as K
+    from rq_testlib import Params
+    iso, planar = Params("iso", 3, 3).R, Params("planar", 3, 3).R
+    s = torch.zeros(128 * 128)
+    s.numpy()[:] = planar.numpy().ravel()  # written behind torch's version counter
+    a = s.view(128, 128)
+    assert K.rotation_block(a) == 2
+    s.numpy()[:] = iso.numpy().ravel()
+    b = s.view(128, 128)
+    assert b.data_ptr() == a.data_ptr() and b._version == a._version
+    assert K.rotation_block(b) == 4
