@@ -381,6 +381,21 @@ def fused_paged_rq_decode_launcher(q: torch.Tensor, kv_cache: torch.Tensor, bloc
 # INT8 prefill
 # ---------------------------------------------------------------------------
 
+_cu_cache: dict = {}
+
+
+def _single_cu_seqlens(device, num_tokens: int) -> torch.Tensor:
+    """[0, num_tokens] on the device, made once per (device, length) and kept: the
+    reference's single-sequence call form then costs no host-to-device copy per call
+    (and none inside a captured graph after the first)."""
+    key = (str(device), int(num_tokens))
+    t = _cu_cache.get(key)
+    if t is None:
+        t = torch.tensor([0, num_tokens], dtype=torch.int32, device=device)
+        _cu_cache[key] = t
+    return t
+
+
 def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
                                 seq_lens: torch.Tensor, k_centroids: torch.Tensor, v_centroids: torch.Tensor,
                                 rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
@@ -411,7 +426,7 @@ def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_t
             raise ValueError(
                 f"fused_paged_rq_int8_prefill supports only a single sequence, "
                 f"but got seq_lens.numel() == {seq_lens.numel()}.")
-        cu_seqlens_q = torch.tensor([0, num_tokens], dtype=torch.int32, device=q.device)
+        cu_seqlens_q = _single_cu_seqlens(q.device, num_tokens)
         max_q_len = num_tokens
     dev = _require_device(q, kv_cache, block_table, seq_lens, cu_seqlens_q)
     if sm_scale is None:
