@@ -550,6 +550,30 @@ def time_config4_one_forward(steps=5):
     return dict(decodes=128, decode_ctx_tokens=int(sum(dec)), chunks=4, chunk_prefixes=pre, **res)
 
 
+def hbm_read_probe(gib=2, reps=10):
+    """Achievable HBM read bandwidth on this device, for context next to the 8 TB/s
+    peak: torch's int64 sum over a `gib` GiB device buffer (a plain streaming read;
+    on MI355X it reaches ~6.1 TB/s, about 76 % of the published peak)."""
+    import torch
+    x = torch.ones((gib << 30) // 8, dtype=torch.int64, device="cuda")
+    for _ in range(3):
+        x.sum()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        x.sum()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = x.numel() * 8
+    del x
+    torch.cuda.empty_cache()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(method=f"torch int64 sum over {gib} GiB (plain streaming read)", bytes=nbytes, us=round(ms * 1e3, 1),
+                GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+
+
 def measured_traffic():
     """HBM bytes per decode call measured with rocprofv3 counters (see the JSON for the commands)."""
     p = os.path.join(ROOT, "profiles", "decode_cfg1_traffic.json")
@@ -569,7 +593,8 @@ def main():
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
-                                       "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3"],
+                                       "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3",
+                                       "hbm_probe"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -588,7 +613,7 @@ def main():
               "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
               "config0": config0_roundtrip, "config4_forward": time_config4_one_forward,
               "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3),
-              "decode1_dense3": decode_config1_dense3}[args.only]
+              "decode1_dense3": decode_config1_dense3, "hbm_probe": hbm_read_probe}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -647,6 +672,9 @@ def main():
         result["decode_config1_dense3"] = decode_config1_dense3()
         result["unfused_config1_decode"] = time_unfused(1)
         result["unfused_config3_prefill"] = time_unfused(3)
+        probe = hbm_read_probe()
+        probe["decode_value_frac_of_probe"] = round(gbs / probe["GBps"], 4)
+        result["hbm_read_probe"] = probe
     if not args.no_cpu_baseline:
         result["config0_roundtrip"] = config0_roundtrip()
         result["cpu_baseline"] = cpu_baseline(inp, gpu_out)
