@@ -270,6 +270,23 @@ def decode_config1_dense3(steps=20):
     return out
 
 
+def decode_config1_tp8_slice(steps=20):
+    """One GPU's share of config 1 under tensor parallelism 8: the same 64 sequences
+    with 1 kv head and 4 query heads (the layout a TP-8 rank holds; attention needs
+    no exchange).  GB/s on that slice's algorithmic bytes."""
+    import torch
+    lens = config1_lens()
+    inp = build_decode_inputs(lens, H=1, HQ=4)
+    t, _ = time_decode(inp, steps, 5)
+    nb = decode_bytes(lens, 1, 4, 128, 16)
+    gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
+    out = dict(kv_heads=1, q_heads=4, us=round(t["avg_ms"] * 1e3, 1), algorithmic_bytes=int(nb), GBps=round(gbs, 1),
+               pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2), decode_tok_per_s=round(len(lens) / (t["avg_ms"] * 1e-3), 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
 def unfused_call(inp, q, cu, max_q):
     """One rq_paged_attention call (the backend's non-fused path) over a prepared cache."""
     import torch
@@ -550,7 +567,7 @@ def time_config4_one_forward(steps=5):
     return dict(decodes=128, decode_ctx_tokens=int(sum(dec)), chunks=4, chunk_prefixes=pre, **res)
 
 
-def hbm_read_probe(gib=2, reps=10):
+def hbm_read_probe(gib=4, reps=10):
     """Achievable HBM read bandwidth on this device, for context next to the 8 TB/s
     peak: torch's int64 sum over a `gib` GiB device buffer (a plain streaming read;
     on MI355X it reaches ~6.1 TB/s, about 76 % of the published peak)."""
@@ -594,7 +611,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
                                        "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3",
-                                       "hbm_probe"],
+                                       "hbm_probe", "decode1_tp8"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
     ap.add_argument("--calib-copy", action="store_true",
@@ -613,7 +630,8 @@ def main():
               "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
               "config0": config0_roundtrip, "config4_forward": time_config4_one_forward,
               "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3),
-              "decode1_dense3": decode_config1_dense3, "hbm_probe": hbm_read_probe}[args.only]
+              "decode1_dense3": decode_config1_dense3, "hbm_probe": hbm_read_probe,
+              "decode1_tp8": decode_config1_tp8_slice}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
     if args.calib_copy:
@@ -670,6 +688,7 @@ def main():
         result["prefill_config4_chunks"] = time_mixed_cfg4()
         result["config4_one_forward"] = time_config4_one_forward()
         result["decode_config1_dense3"] = decode_config1_dense3()
+        result["decode_config1_tp8_slice"] = decode_config1_tp8_slice()
         result["unfused_config1_decode"] = time_unfused(1)
         result["unfused_config3_prefill"] = time_unfused(3)
         probe = hbm_read_probe()

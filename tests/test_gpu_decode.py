@@ -92,6 +92,14 @@ def test_decode_gqa7_iso_full():
     check(decode_case(4, 4, 4, 28, lens, p=p), "cfg4-gqa7")
 
 
+@pytest.mark.parametrize("H,HQ", [(1, 4), (2, 8)])
+def test_decode_tensor_parallel_slices(H, HQ):
+    """One GPU's share of the config-1 layer under tensor parallelism (TP 8: 1 kv / 4 q
+    heads; TP 4: 2 / 8): one or two waves per decode workgroup."""
+    lens = lens_uniform(8, 1024, 8192, cfg=14)
+    check(decode_case(14, 8, H, HQ, lens), f"tp-slice H={H} HQ={HQ}")
+
+
 def test_decode_k3_v4_and_block_size_32():
     p = Params("iso", 3, 4)
     lens = [700, 33, 64]
