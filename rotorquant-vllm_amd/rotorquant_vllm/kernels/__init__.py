@@ -381,19 +381,11 @@ def fused_paged_rq_decode_launcher(q: torch.Tensor, kv_cache: torch.Tensor, bloc
 # INT8 prefill
 # ---------------------------------------------------------------------------
 
-_cu_cache: dict = {}
-
-
 def _single_cu_seqlens(device, num_tokens: int) -> torch.Tensor:
-    """[0, num_tokens] on the device, made once per (device, length) and kept: the
-    reference's single-sequence call form then costs no host-to-device copy per call
-    (and none inside a captured graph after the first)."""
-    key = (str(device), int(num_tokens))
-    t = _cu_cache.get(key)
-    if t is None:
-        t = torch.tensor([0, num_tokens], dtype=torch.int32, device=device)
-        _cu_cache[key] = t
-    return t
+    """[0, num_tokens] made on the device by a fill kernel: the reference's
+    single-sequence call form then costs no host-to-device copy per call and stays
+    capturable in a HIP graph."""
+    return torch.arange(2, dtype=torch.int32, device=device).mul_(int(num_tokens))
 
 
 def fused_paged_rq_int8_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
