@@ -24,9 +24,9 @@
 // head of the GQA group, 16-position group), as in rq_prefill.hip.  The
 // workgroup decodes each 64-key tile of its (sequence, kv head) from the
 // packed slots into a double-buffered LDS tile (K rows in the q dtype, fp16
-// V'^T rows): while tile t is computed, each thread holds its share of tile
-// t+1's packed bytes in registers, loaded before the compute and decoded into
-// the other buffer after it.  No workspace, no decompressed copy of the cache.
+// V'^T rows): while tile t is computed, tile t+1's packed bytes are copied
+// cache -> LDS staging with direct global -> LDS copies, and decoded into the
+// other buffer after it.  No workspace, no decompressed copy of the cache.
 //
 // MFMA v_mfma_f32_16x16x32_{bf16,f16} for S^T = K Q^T (wave64, lane l,
 // g = l / 16, col = l % 16), four k-steps of 32 head dims:
@@ -47,9 +47,9 @@ constexpr int kPQ = kAttnPQ;
 
 // LDS, per workgroup:
 //   two tile buffers: K rows (64 keys x 256 bytes in the q dtype, 16-byte piece
-//     c = dims 8c .. 8c+7 of key r at r * 256 + 16 * (c ^ (r & 15)): the 16 keys
-//     one MFMA operand read touches hit 16 distinct piece slots), then V'^T
-//     (vt_piece);
+//     c = dims 8c .. 8c+7 of key r, in the order e0 e2 e4 e6 e1 e3 e5 e7, at
+//     r * 256 + 16 * (c ^ (r & 15)): the 16 keys one MFMA operand read touches
+//     hit 16 distinct piece slots), then V'^T (vt_piece);
 //   staging: the next tile's packed bytes as copied from the cache -- K index
 //     dwords [key][16], V index dwords [key][16], K norms [key], V norms [key];
 //   slot offsets of the keys of the tile staged next.
@@ -208,21 +208,40 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
         const int e_v = min(24, max(-14, (int)((__float_as_uint(vx) >> 23) & 0xffu) - 126));
         const float vs = ldexpf(1.f, -e_v);
         for (int w = tid; w < kItems; w += nthr) {
-            if (w < 256) {  // K rows: dims 8 dw .. 8 dw + 7 of keys 4 kq + i
-                const int kq = w >> 4, dw = w & 15;
+            if (w < 256) {
+                // K rows: key r, dims 32 qq .. 32 qq + 31 (index dwords 4 qq .. 4 qq + 3).  The
+                // key's 16-bit table dtype(centroid * norm) of every codebook entry is built in
+                // registers, and its 32 indices are looked up with byte permutes; a piece holds
+                // dims 8c .. 8c+7 in the order e0 e2 e4 e6 e1 e3 e5 e7 (the query operand's).
+                const int r = w >> 2, qq = w & 3;
+                const float nrm = r < nk ? kn[r] : 0.f;
+                Table16 tab;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    uint32_t pr[2];
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2) {
+                        const int j = 4 * c + 2 * h2;
+                        pr[h2] = Elem<DT>::from_f32(opaque(ktab[j] * nrm)) |
+                                 (Elem<DT>::from_f32(opaque(ktab[j + 1] * nrm)) << 16);
+                    }
+                    tab.lo[c] = perm(pr[1], pr[0], 0x06040200u);  // low bytes of entries 4c .. 4c+3
+                    tab.hi[c] = perm(pr[1], pr[0], 0x07050301u);
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * kq + i;
+                    const int dw = 4 * qq + i;
                     const uint32_t x = idx_dword(lds + kSKi + r * 64, dw, a.dense3 != 0);
-                    const float nrm = r < nk ? kn[r] : 0.f;
-                    uint32_t wd[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {  // byte j: dims 2j (high nibble), 2j + 1 (low)
-                        const float ev = opaque(ktab[(x >> (8 * j + 4)) & 15u] * nrm);
-                        const float od = opaque(ktab[(x >> (8 * j)) & 15u] * nrm);
-                        wd[j] = Elem<DT>::from_f32(ev) | (Elem<DT>::from_f32(od) << 16);
+                    const uint32_t ev = (x >> 4) & 0x0f0f0f0fu, od = x & 0x0f0f0f0fu;
+                    uint2 e, o;
+                    if (a.nkc <= 8) {
+                        e = lookup4<3>(tab, ev);
+                        o = lookup4<3>(tab, od);
+                    } else {
+                        e = lookup4<4>(tab, ev);
+                        o = lookup4<4>(tab, od);
                     }
-                    *reinterpret_cast<u32x4 *>(tb + kTK + kt_piece(r, dw)) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+                    *reinterpret_cast<u32x4 *>(tb + kTK + kt_piece(r, dw)) = u32x4{e.x, e.y, o.x, o.y};
                 }
             } else {  // V'^T rows 8 dw + 2j + par, keys 4 tq .. 4 tq + 3 (8 bytes each)
                 const int u = w - 256;
@@ -284,9 +303,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
 #pragma unroll
             for (int k = 0; k < 8; ++k) xin[k] = Elem<DT>::to_f32((w16[k >> 1] >> (16 * (k & 1))) & 0xffffu);
             rotate_q8<DT>(xin, base, a.R, a.rot_block, qr);
+            // dims in the K rows' order e0 e2 e4 e6 e1 e3 e5 e7
             uint32_t pk[4];
+            constexpr int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) pk[k] = Elem<DT>::from_f32(qr[2 * k]) | (Elem<DT>::from_f32(qr[2 * k + 1]) << 16);
+            for (int k = 0; k < 4; ++k)
+                pk[k] = Elem<DT>::from_f32(qr[ord[2 * k]]) | (Elem<DT>::from_f32(qr[ord[2 * k + 1]]) << 16);
             qop[s_] = u32x4{pk[0], pk[1], pk[2], pk[3]};
         }
     }
