@@ -103,6 +103,7 @@ struct AttnArgs {
     float score_scale;  // sm_scale * log2(e)
     int qb;             // query positions per workgroup (= 16 * position groups)
     int npg;            // position groups per workgroup
+    int ncomp;          // waves that compute (query head, position group); the rest only decode tiles
     void *out;
     int64_t o_st, o_sh;
 };
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
     const int pg = wave % a.npg;                     // 16-position group
     const int hq = h * a.G + gh;
     const int i0 = qblk * a.qb + pg * kPQ;  // first query index of this wave
-    const bool wave_active = i0 < T;
+    const bool wave_active = wave < a.ncomp && i0 < T;
     const int my_pos = pos_base + i0 + col;
     // V'^T pieces of this lane (dim col, pieces g and 4 + g)
     const int voff0 = vt_piece(col, g), voff1 = vt_piece(col, 4 + g);
@@ -438,18 +439,22 @@ extern "C" int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q,
     // GQA groups of more than kMaxWaves heads go to hsplit workgroups per kv head
     // (the smallest split into equal parts of at most kMaxWaves heads); then
     // 16-position groups per workgroup: up to kMaxWaves waves for long queries,
-    // one group when every query is short, at least kMinWaves waves (they share
-    // the tile decode).
+    // at least kMinWaves waves (they share the tile decode).  When every query is
+    // short (one position group), the workgroup has kMaxWaves waves anyway: the
+    // waves past the GQA group's only decode tiles, which is most of a
+    // decode-shaped call's time.
     a.hsplit = 1;
     while (a.G % a.hsplit != 0 || a.G / a.hsplit > kMaxWaves) ++a.hsplit;
     const int gw = a.G / a.hsplit;
     a.npg = max_q_len > kPQ ? std::max(1, kMaxWaves / gw) : 1;
-    while (gw * a.npg < kMinWaves) ++a.npg;
+    if (max_q_len > kPQ)
+        while (gw * a.npg < kMinWaves) ++a.npg;
     a.qb = kPQ * a.npg;
+    a.ncomp = gw * a.npg;
     a.out = out;
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
-    const int nwaves = gw * a.npg;
+    const int nwaves = max_q_len > kPQ ? a.ncomp : kMaxWaves;
     dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)(a.H * a.hsplit), (unsigned)num_seqs);
     const size_t lds = kLdsBytes;
     hipStream_t st = (hipStream_t)stream;
