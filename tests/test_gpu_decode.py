@@ -100,6 +100,14 @@ def test_decode_tensor_parallel_slices(H, HQ):
     check(decode_case(14, 8, H, HQ, lens), f"tp-slice H={H} HQ={HQ}")
 
 
+@pytest.mark.parametrize("BS", [1, 12, 64, 128])
+def test_decode_block_sizes(BS):
+    """Block sizes other than 16: one token per block, a non-power of two (division
+    instead of shifts), and blocks larger than a 32-token tile."""
+    lens = [1, 70, 300, 1000]
+    check(decode_case(15, len(lens), 8, 32, lens, block_size=BS), f"bs{BS}")
+
+
 def test_decode_k3_v4_and_block_size_32():
     p = Params("iso", 3, 4)
     lens = [700, 33, 64]

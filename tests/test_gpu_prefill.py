@@ -90,6 +90,13 @@ def test_prefill_unit_scale_bf16_iso4():
     check(case, "unit-iso4-bf16", plain_max_abs=True)
 
 
+@pytest.mark.parametrize("BS", [12, 32, 64])
+def test_prefill_block_sizes(BS):
+    """Block sizes other than 16 (a non-power of two among them), chunks after prefixes."""
+    p = Params("iso", 4, 4)
+    check(prefill_case(36, [70, 1, 130], [70 + 45, 80, 130], 8, 32, p, BS=BS), f"bs{BS}")
+
+
 def test_prefill_gqa16_one_kv_head():
     """16 query heads on one kv head: the widest workgroup (16 waves), where the per-wave
     output staging buffers fill the tile area; two (sequence, kv head) pairs also take
