@@ -77,13 +77,15 @@ def test_compress_fp32_input():
     assert np.array_equal(norms.cpu().numpy().view(np.uint32), on.view(np.uint32))
 
 
-@pytest.mark.parametrize("H,mode,kb,vb", [(8, "iso", 3, 3), (4, "iso", 4, 3), (8, "planar", 4, 3), (1, "iso", 3, 4),
-                                          (2, "planar", 3, 3)])
-def test_compress_store_slots_bit_exact(H, mode, kb, vb):
-    """Fused K+V compress into random slots: every byte of the cache matches the oracle store."""
+@pytest.mark.parametrize("H,mode,kb,vb,BS", [(8, "iso", 3, 3, 16), (4, "iso", 4, 3, 16), (8, "planar", 4, 3, 16),
+                                             (1, "iso", 3, 4, 16), (2, "planar", 3, 3, 16), (8, "iso", 3, 3, 12),
+                                             (4, "iso", 3, 3, 1)])
+def test_compress_store_slots_bit_exact(H, mode, kb, vb, BS):
+    """Fused K+V compress into random slots: every byte of the cache matches the oracle store
+    (block sizes 16, 12 and 1)."""
     K = _kernels()
     p = Params(mode, kb, vb)
-    BS, NB = 16, 40
+    NB = 640 // BS
     N = 300
     k, v = kv_config0(N, H, 128, cfg=3)
     g = torch.Generator().manual_seed(11)
