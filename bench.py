@@ -619,7 +619,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the decode path shards by (sequence, kv head) with no exchange, see DESIGN.md", file=sys.stderr)
+              "the decode path shards by (sequence, kv head) with no exchange", file=sys.stderr)
         sys.exit(2)
 
     import torch
