@@ -355,7 +355,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void paged_attn_kernel(AttnArgs a) 
 #pragma unroll
                 for (int j = 0; j < 16; ++j) s[j] = (16 * (j >> 2) + (j & 3)) < lim ? s[j] : -INFINITY;
             }
-            softmax_pv(st, s, a.score_scale, 1.f, e_cur, tb + kTVt, voff0, voff1, col);
+            softmax_pv(st, s, a.score_scale, 1.f, e_cur, tb + kTVt, voff0, voff1, rowsum_operand(e_cur, col));
         }
         if (more) {
             wait_copies<0>();

@@ -112,14 +112,22 @@ struct AttnState {
     }
 };
 
+// Row-sum operand of a tile: lanes of MFMA row 0 (col == 0) hold 2^-e_v in fp16
+// (normal or denormal), the others zero.
+__device__ __forceinline__ u32x4 rowsum_operand(int e_v, int col) {
+    const uint32_t w = col == 0 ? pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v)) : 0u;
+    return u32x4{w, w, w, w};
+}
+
 // Online softmax over one tile and O^T += V'^T P'^T.
 //   s: this lane's 16 scores (masked ones -INFINITY); the base-2 score proper is
 //      s * s_unit * sq (s_unit: per tile, sq: per position);
 //   e_v: the tile's V exponent, V' = V 2^-e_v in fp16 (|V'| below max|centroid|);
 //   vt: the tile's V'^T rows; koff0 / koff1: this lane's pieces g and 4 + g of row
-//       col (vt_piece(col, g), vt_piece(col, 4 + g)); col = lane % 16.
+//       col (vt_piece(col, g), vt_piece(col, 4 + g));
+//   ones: the tile's row-sum operand (rowsum_operand(e_v, col), col = lane % 16).
 __device__ __forceinline__ void softmax_pv(AttnState &st, const float (&s)[16], float s_unit, float sq, int e_v,
-                                           const uint8_t *vt, int koff0, int koff1, int col) {
+                                           const uint8_t *vt, int koff0, int koff1, const u32x4 ones) {
     float tmax = s[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
@@ -160,12 +168,8 @@ __device__ __forceinline__ void softmax_pv(AttnState &st, const float (&s)[16], 
         for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * t + e], usq, bias));
         pop[t] = u32x4{pack_f16(p[0], p[1]), pack_f16(p[2], p[3]), pack_f16(p[4], p[5]), pack_f16(p[6], p[7])};
     }
-    {
-        const uint32_t w = col == 0 ? pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v)) : 0u;  // fp16 normal or denormal
-        const u32x4 ones = u32x4{w, w, w, w};
-        st.lsum = mfma_f16(ones, pop[0], st.lsum);
-        st.lsum = mfma_f16(ones, pop[1], st.lsum);
-    }
+    st.lsum = mfma_f16(ones, pop[0], st.lsum);
+    st.lsum = mfma_f16(ones, pop[1], st.lsum);
     // 8 blocks of 16 head dims (dim 16m + col; its swizzle term is col & 7), two k-steps
 #pragma unroll
     for (int m = 0; m < 8; ++m) {

@@ -101,7 +101,8 @@ __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * 
 // V^T row d (128 bytes: 8 pieces of 8 keys) uses the K row swizzle: piece c at k_piece(d, c).
 constexpr int kImSk = kImVt + kPD * kKT * 2;        // float: score unit = tile k scale * kmax/127 * score_scale / 128
 constexpr int kImVe = kImSk + 4;                    // int: e_tile, 2^e_tile > the tile's largest v norm
-constexpr int kImBytes = (kImVe + 4 + 1023) / 1024 * 1024;  // whole 1 KB copies
+constexpr int kImOnes = kImSk + 16;                 // row-sum operand: 4 dwords of 2^-e_tile (fp16 pair), 4 zero dwords
+constexpr int kImBytes = (kImOnes + 32 + 1023) / 1024 * 1024;  // whole 1 KB copies
 constexpr int kImChunks = kImBytes / 1024;
 
 // Largest |centroid| of a codebook (1 when all are zero): int8 unit = this / 127.
@@ -181,6 +182,9 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         if (tid == 0) {
             *reinterpret_cast<float *>(img + kImSk) = s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f));
             *reinterpret_cast<int *>(img + kImVe) = e_v;
+            const uint32_t w = pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v));
+            *reinterpret_cast<u32x4 *>(img + kImOnes) = u32x4{w, w, w, w};
+            *reinterpret_cast<u32x4 *>(img + kImOnes + 16) = u32x4{0u, 0u, 0u, 0u};
             vscale = ldexpf(1.f, -e_v);
         }
     }
@@ -262,6 +266,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int g = lane >> 4, col = lane & 15;
     // this lane's operand pieces in a tile image: key col, pieces g and 4 + g; dim col, piece g
     const int koff0 = k_piece(col, g), koff1 = k_piece(col, 4 + g);
+    const int ones_off = kImOnes + (col == 0 ? 0 : 16);  // the row-sum operand (MFMA row 0 = col 0)
     const int gh = wave / a.npg;            // query head inside the GQA group
     const int pg = wave - gh * a.npg;       // 16-position group
     const int hq = h * a.G + gh;
@@ -409,7 +414,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             for (int j = 0; j < 16; ++j) s[j] = (16 * (j >> 2) + (j & 3)) < lim ? s[j] : -INFINITY;
         }
         // ---- online softmax and O^T += V'^T P'^T ----
-        softmax_pv(st, s, s_unit, sq, *reinterpret_cast<const int *>(tb + kImVe), tb + kImVt, koff0, koff1, col);
+        softmax_pv(st, s, s_unit, sq, *reinterpret_cast<const int *>(tb + kImVe), tb + kImVt, koff0, koff1,
+                   *reinterpret_cast<const u32x4 *>(tb + ones_off));
         }
         wait_copies<0>();  // the next tile's image has landed
         __syncthreads();   // ... for every wave; this buffer is refilled next
