@@ -570,7 +570,7 @@ def time_config4_one_forward(steps=5):
 def hbm_read_probe(gib=4, reps=10):
     """Achievable HBM read bandwidth on this device, for context next to the 8 TB/s
     peak: torch's int64 sum over a `gib` GiB device buffer (a plain streaming read;
-    on MI355X it reaches ~6.1 TB/s, about 76 % of the published peak)."""
+    on MI355X it reaches 5.8-6.2 TB/s, 73-77 % of the published peak)."""
     import torch
     x = torch.ones((gib << 30) // 8, dtype=torch.int64, device="cuda")
     for _ in range(3):
