@@ -7,7 +7,6 @@ the static scratch holds the first call's larger contents when the second one
 runs -- and a call needing more scratch than RQ_DECODE_SCRATCH_BYTES must be
 refused with RQ_ENOSPACE before anything is launched.
 """
-import numpy as np
 import pytest
 import torch
 
