@@ -174,6 +174,12 @@ __device__ __forceinline__ float opaque(float x) {
     asm volatile("" : "+v"(x));
     return x;
 }
+// The same for a wave-uniform int (kept in an SGPR): code that uses the result
+// cannot be moved above the point where it is taken.
+__device__ __forceinline__ int opaque_s(int x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     // gfx950 converts with v_cvt_pk_bf16_f32 (round to nearest even).

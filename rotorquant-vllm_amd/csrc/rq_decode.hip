@@ -721,12 +721,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         float nk[8] = {nk0.x, nk0.y, nk0.z, nk0.w, nk1.x, nk1.y, nk1.z, nk1.w};
         float nv[8] = {nv0.x, nv0.y, nv0.z, nv0.w, nv1.x, nv1.y, nv1.z, nv1.w};
         if (valid < kTile) {
+            // (each masking block takes `valid` through an empty asm, so that its
+            // compares stay inside the block instead of running for every full tile)
+            const int vv = opaque_s(valid);
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
-                nk[i] = tt < valid ? nk[i] : 0.f;
-                nv[i] = tt < valid ? nv[i] : 0.f;
-                vw[i] = tt < valid ? vw[i] : 0u;
+                nk[i] = tt < vv ? nk[i] : 0.f;
+                nv[i] = tt < vv ? nv[i] : 0.f;
+                vw[i] = tt < vv ? vw[i] : 0u;
             }
         }
         // A V norm at or above 2^e_run (rare after the first tile): raise e_run to the
@@ -775,10 +778,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         float s[8] = {s0.x * nk[0], s0.y * nk[1], s0.z * nk[2], s0.w * nk[3],
                       s1.x * nk[4], s1.y * nk[5], s1.z * nk[6], s1.w * nk[7]};
         if (valid < kTile) {
+            const int vv = opaque_s(valid);
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
-                s[i] = tt < valid ? s[i] : -INFINITY;
+                s[i] = tt < vv ? s[i] : -INFINITY;
             }
         }
         float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
