@@ -102,6 +102,15 @@ __device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
     return decode_row8_sel<BITS>(t, (x >> 4) & 0x0f0f0f0fu, x & 0x0f0f0f0fu);  // e0 e2 e4 e6 | e1 e3 e5 e7
 }
 
+typedef __attribute__((ext_vector_type(2))) int i32x2;
+// ds_read_b64_tr_b8 (gfx950): per 16 lanes, lanes 2i and 2i + 1 name the two 8-byte
+// halves of row i of an 8 x 16 byte block, and lane c receives byte c of rows 0..7
+// (row i in byte i).  p: an LDS address, 8-byte aligned.
+__device__ __forceinline__ i32x2 ds_read_tr8(const uint8_t *p) {
+    typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2 *)(p));
+}
+
 // Value of lane (l & ~3) + perm[l & 3] of the lane's quad (DPP quad_perm, ctrl =
 // perm[0] | perm[1] << 2 | perm[2] << 4 | perm[3] << 6).
 template <int CTRL>
@@ -481,6 +490,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int h = h0 + wave;
     const SlotLayout SL(a.H, kD, D3);
     constexpr int IB = D3 ? 48 : 64;  // index bytes per head
+    constexpr bool kTrV = !D3 && HPW > 0;  // V index bytes by transposing LDS reads
     const int TS = HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride;
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
@@ -604,15 +614,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             uint8_t *pa = reinterpret_cast<uint8_t *>(a.part_acc + slot * kD);
             uint8_t *pm = reinterpret_cast<uint8_t *>(a.part_ml + slot * 2);
             const uint32_t ln = lane_now();
-            const uint32_t lo_off = ((ln & 15) * kD + 32 * (ln >> 4)) * 4;
-            // acc[m][i] = O[col][8 * (4g + i) + m] relative to 2^(m_run + e_run)
+            if constexpr (!kTrV) {
+                // acc[m][i] = O[col][8 * (4g + i) + m] relative to 2^(m_run + e_run)
+                const uint32_t lo_off = ((ln & 15) * kD + 32 * (ln >> 4)) * 4;
     #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float4 lo = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
-                float4 hi = make_float4(acc[4][i], acc[5][i], acc[6][i], acc[7][i]);
-                float4 *dst = reinterpret_cast<float4 *>(pa + lo_off + 32 * i);
-                dst[0] = lo;
-                dst[1] = hi;
+                for (int i = 0; i < 4; ++i) {
+                    float4 lo = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
+                    float4 hi = make_float4(acc[4][i], acc[5][i], acc[6][i], acc[7][i]);
+                    float4 *dst = reinterpret_cast<float4 *>(pa + lo_off + 32 * i);
+                    dst[0] = lo;
+                    dst[1] = hi;
+                }
+            } else {
+                // acc[2r + e][i] = O[col][32r + 8g + 2i + e] relative to 2^(m_run + e_run)
+                const uint32_t lo_off = ((ln & 15) * kD + 8 * (ln >> 4)) * 4;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i)
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<float2 *>(pa + lo_off + 4 * (32 * r + 2 * i)) =
+                            make_float2(acc[2 * r][i], acc[2 * r + 1][i]);
             }
             if (g == 0) *reinterpret_cast<float2 *>(pm + 8u * (lane_now() & 15)) = make_float2(m_run + (float)e_run, lsum);
         }
@@ -655,10 +676,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         // ---- this wave's operands of the tile ------------------------------------
         // token col, K dims 32g .. 32g+31 (16 nibble bytes, or the 12-byte dense group g)
         const uint8_t *kb = sb + col * TS + IB * wave + (D3 ? 12 : 16) * g;
-        // token 4g, V dims 8 col .. 8 col + 7: nibble dword col; dense: dword min(col % 4, 2)
-        // of group col / 4 (position 3 is assembled from the quad's other three lanes)
-        const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave +
-                            (D3 ? 12 * (col >> 2) + 4 * min(col & 3, 2) : 4 * col);
+        // V index bytes of the lane's 8 tokens 4g + k, 16 + 4g + k (k < 4), transposed:
+        // Ga[r] = byte j of tokens 4g .. 4g+3 (byte k = token 4g + k), Gb[r] = byte j of
+        // tokens 16+4g .. 16+4g+3.
+        //   nibbles, 8 or 4 heads per workgroup: j = 16r + col (dims 32r + 2 col, +1) by
+        //     ds_read_b64_tr_b8, which transposes, per 16 lanes, an 8 x 16 byte block:
+        //     lanes 2i and 2i + 1 give the two 8-byte halves of row i (token i of the lane
+        //     group), and lane c gets byte c of every row;
+        //   otherwise j = r of the nibble dword col (dims 8 col + 2r, +1), or dense: of
+        //     dword min(col % 4, 2) of group col / 4 (position 3 is assembled from the
+        //     quad's other three lanes), read per token and byte-transposed in registers
+        //     (the generic-head variant has no VGPRs to spare for the other form).
+        uint32_t vw[8], Ga[4], Gb[4];
         const uint8_t *nb = sb + norm_off + 128 * wave + 16 * g;               // K norms of tokens 4g..4g+3
         uint4 kw0, kw1;
         if constexpr (D3) {
@@ -670,9 +699,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             kw0 = *reinterpret_cast<const uint4 *>(kb);
             kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
         }
-        uint32_t vw[8];
+        if constexpr (!kTrV) {
+            const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave +
+                                (D3 ? 12 * (col >> 2) + 4 * min(col & 3, 2) : 4 * col);
     #pragma unroll
-        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
+            for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
+        } else {
+            const int row = col >> 1;  // token 4g + row (row < 4) or 12 + 4g + row
+            const uint8_t *vr = sb + (row < 4 ? 4 * g + row : 12 + 4 * g + row) * TS + IB * hpw + IB * wave + 8 * (col & 1);
+    #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const i32x2 t = ds_read_tr8(vr + 16 * r);
+                Ga[r] = (uint32_t)t.x;
+                Gb[r] = (uint32_t)t.y;
+            }
+        }
         float4 nk0, nk1, nv0, nv1;
         if constexpr (HPW > 0) {
             // token 4g + i at 256 i + 16 NP q (+1024 for tokens 16.. when TPI = 16),
@@ -729,7 +770,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                 const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
                 nk[i] = tt < vv ? nk[i] : 0.f;
                 nv[i] = tt < vv ? nv[i] : 0.f;
-                vw[i] = tt < vv ? vw[i] : 0u;
+                if constexpr (!kTrV) vw[i] = tt < vv ? vw[i] : 0u;
+            }
+            if constexpr (kTrV) {
+                uint32_t ma = 0, mb = 0;  // bytes of the tokens 4g + k and 16 + 4g + k below valid
+    #pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    ma |= (4 * g + k < vv ? 0xffu : 0u) << (8 * k);
+                    mb |= (16 + 4 * g + k < vv ? 0xffu : 0u) << (8 * k);
+                }
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    Ga[r] &= ma;
+                    Gb[r] &= mb;
+                }
             }
         }
         // A V norm at or above 2^e_run (rare after the first tile): raise e_run to the
@@ -814,17 +868,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         pop.w = pack2<RQ_DTYPE_F16>(p[6] * nv[6], p[7] * nv[7]);
 
         // ---- O^T += V^T P^T ---------------------------------------------------
-        // Byte-transpose the 8 tokens' dwords: Ga[j] = byte j of tokens 0..3,
-        // Gb[j] = byte j of tokens 4..7; then split nibbles per head dim.
-        uint32_t A01 = perm(vw[1], vw[0], 0x05010400u), B01 = perm(vw[1], vw[0], 0x07030602u);
-        uint32_t A23 = perm(vw[3], vw[2], 0x05010400u), B23 = perm(vw[3], vw[2], 0x07030602u);
-        uint32_t A45 = perm(vw[5], vw[4], 0x05010400u), B45 = perm(vw[5], vw[4], 0x07030602u);
-        uint32_t A67 = perm(vw[7], vw[6], 0x05010400u), B67 = perm(vw[7], vw[6], 0x07030602u);
-        uint32_t Ga[4] = {perm(A23, A01, 0x05040100u), perm(A23, A01, 0x07060302u), perm(B23, B01, 0x05040100u),
-                          perm(B23, B01, 0x07060302u)};
-        uint32_t Gb[4] = {perm(A67, A45, 0x05040100u), perm(A67, A45, 0x07060302u), perm(B67, B45, 0x05040100u),
-                          perm(B67, B45, 0x07060302u)};
-        // Index selectors (one index per byte) of dims 8r + 2j (even) and 8r + 2j + 1 (odd).
+        // Ga[j], Gb[j]: byte j of the lane's tokens (read transposed above, or here
+        // byte-transposed from the tokens' dwords); split nibbles per head dim.
+        if constexpr (!kTrV) {
+            const uint32_t A01 = perm(vw[1], vw[0], 0x05010400u), B01 = perm(vw[1], vw[0], 0x07030602u);
+            const uint32_t A23 = perm(vw[3], vw[2], 0x05010400u), B23 = perm(vw[3], vw[2], 0x07030602u);
+            const uint32_t A45 = perm(vw[5], vw[4], 0x05010400u), B45 = perm(vw[5], vw[4], 0x07030602u);
+            const uint32_t A67 = perm(vw[7], vw[6], 0x05010400u), B67 = perm(vw[7], vw[6], 0x07030602u);
+            Ga[0] = perm(A23, A01, 0x05040100u);
+            Ga[1] = perm(A23, A01, 0x07060302u);
+            Ga[2] = perm(B23, B01, 0x05040100u);
+            Ga[3] = perm(B23, B01, 0x07060302u);
+            Gb[0] = perm(A67, A45, 0x05040100u);
+            Gb[1] = perm(A67, A45, 0x07060302u);
+            Gb[2] = perm(B67, B45, 0x05040100u);
+            Gb[3] = perm(B67, B45, 0x07060302u);
+        }
+        // Index selectors (one index per byte) of the even and the odd dim of byte j.
         // Dense: lanes of positions 0..2 mask their own bytes; the position-3 lane takes
         // the top bits of its quad's A, B and C lanes (same tokens): one form for all
         // lanes, (x >> s1) & m1 | (y >> s2) & m2, with per-lane shifts and masks.
@@ -847,8 +907,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             sel(Gb[j], eb, ob);
             uint2 ha = lookup4<VB>(tv, ea), hb = lookup4<VB>(tv, eb);
             uint2 la = lookup4<VB>(tv, oa), lb = lookup4<VB>(tv, ob);
-            acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // dim 8r + 2j
-            acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // dim 8r + 2j + 1
+            acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // even dims
+            acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // odd dims
         }
     }
 
