@@ -765,9 +765,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             // (each masking block takes `valid` through an empty asm, so that its
             // compares stay inside the block instead of running for every full tile)
             const int vv = opaque_s(valid);
+            const int g4 = 4 * (int)(lane_now() >> 4);  // 4g, rebuilt here (not kept live)
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
+                const int tt = i < 4 ? g4 + i : 12 + g4 + i;
                 nk[i] = tt < vv ? nk[i] : 0.f;
                 nv[i] = tt < vv ? nv[i] : 0.f;
                 if constexpr (!kTrV) vw[i] = tt < vv ? vw[i] : 0u;
@@ -776,8 +777,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                 uint32_t ma = 0, mb = 0;  // bytes of the tokens 4g + k and 16 + 4g + k below valid
     #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    ma |= (4 * g + k < vv ? 0xffu : 0u) << (8 * k);
-                    mb |= (16 + 4 * g + k < vv ? 0xffu : 0u) << (8 * k);
+                    ma |= (g4 + k < vv ? 0xffu : 0u) << (8 * k);
+                    mb |= (16 + g4 + k < vv ? 0xffu : 0u) << (8 * k);
                 }
     #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -833,9 +834,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                       s1.x * nk[4], s1.y * nk[5], s1.z * nk[6], s1.w * nk[7]};
         if (valid < kTile) {
             const int vv = opaque_s(valid);
+            const int g4 = 4 * (int)(lane_now() >> 4);
     #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int tt = i < 4 ? 4 * g + i : 12 + 4 * g + i;
+                const int tt = i < 4 ? g4 + i : 12 + g4 + i;
                 s[i] = tt < vv ? s[i] : -INFINITY;
             }
         }
