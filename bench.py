@@ -288,24 +288,35 @@ def decode_config1_tp8_slice(steps=20):
 
 
 def unfused_call(inp, q, cu, max_q):
-    """One rq_paged_attention call (the backend's non-fused path) over a prepared cache."""
+    """The backend's non-fused path over a prepared cache, as it dispatches: queries of
+    at most 16 tokens -> one rq_paged_attention call; longer ones -> one rq_paged_prefill
+    call (its workspace allocated here, outside the timed calls)."""
     import torch
 
+    from rotorquant_vllm import _lib
     from rotorquant_vllm import kernels as K
     p, dev = inp["p"], q.device
     kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
     out = torch.empty_like(q)
+    args = (q, inp["caches"][0], inp["bt"], inp["lens"], cu, max_q, kc, vc, R, inp["H"], 128, inp["BS"])
+    if max_q <= 16:
+        def fn():
+            K.paged_attention(*args, out=out)
+        return fn
+    B = inp["lens"].shape[0]
+    mx = int(inp["lens"].max())
+    ws = torch.empty(_lib.load().rq_paged_prefill_workspace_bytes(B, inp["H"], mx), dtype=torch.uint8, device=dev)
 
     def fn():
-        K.paged_attention(q, inp["caches"][0], inp["bt"], inp["lens"], cu, max_q, kc, vc, R, inp["H"], 128, inp["BS"],
-                          out=out)
+        K.paged_prefill(*args, out=out, max_seq_len=mx, workspace=ws)
     return fn
 
 
 def time_unfused(cfg, steps=5):
-    """The non-fused path (rq_paged_attention: K/V dequantized to bf16 in LDS, 16-bit MFMA)
-    on config 1's decode batch (bytes as the fused decode's roofline) or config 3's
-    causal prefill (algorithmic bf16 flops = 2 x the causal Q K^T + P V multiply-adds)."""
+    """The non-fused path (K/V rounded to bf16, 16-bit MFMA) on config 1's decode batch
+    (rq_paged_attention; bytes as the fused decode's roofline) or config 3's causal
+    prefill (rq_paged_prefill; algorithmic bf16 flops = 2 x the causal Q K^T + P V
+    multiply-adds)."""
     import torch
     if cfg == 1:
         lens = config1_lens()

@@ -34,8 +34,9 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 5  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
-                              4: rq_paged_attention; 5: index_layout on the entry points that touch slots */
+#define RQ_ABI_VERSION 6  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
+                              4: rq_paged_attention; 5: index_layout on the entry points that touch slots;
+                              6: rq_paged_prefill */
 
 enum rq_status {
     RQ_OK = 0,
@@ -314,6 +315,42 @@ int rq_paged_attention(const void *q, int32_t dtype, int64_t total_q, int32_t nu
                        const float *rotation, int32_t rot_block, float sm_scale,
                        void *out, int64_t out_stride_tok, int64_t out_stride_head,
                        void *stream);
+
+/*
+ * The non-fused path of rq_paged_attention, same arithmetic, in two launches for
+ * long queries: a pack kernel decodes every 64-key tile of every (sequence, kv
+ * head) once into a tile image in the workspace (K and V in the q dtype, the
+ * values rq_decompress writes; V scaled exactly into fp16 by a power of two),
+ * and the attention kernel streams the images (Q K^T on the q dtype's MFMA,
+ * exact products and fp32 sums).  rq_paged_attention decodes each tile in
+ * every query block's workgroup instead, which suits single-token queries.
+ *
+ * Replaces the same reference code as rq_paged_attention
+ *   src/rotorquant_vllm/vllm/rq_backend.py:937-1036 (non-fused branch).
+ * Arguments as for rq_paged_attention, plus max_seq_len (bounds every
+ * seq_lens[b]; keys past it are not read) and a workspace of
+ * rq_paged_prefill_workspace_bytes() bytes, 16-byte aligned, no initialisation
+ * needed.  Centroid counts 1..16.
+ */
+int rq_paged_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                     int64_t q_stride_tok, int64_t q_stride_head,
+                     const int32_t *cu_seqlens_q, int64_t num_seqs, int64_t max_q_len, int32_t causal,
+                     const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
+                     int64_t stride_block, int64_t stride_token,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                     const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                     const int32_t *seq_lens, int64_t max_seq_len,
+                     const float *k_centroids, int32_t n_k_centroids,
+                     const float *v_centroids, int32_t n_v_centroids,
+                     const float *rotation, int32_t rot_block, float sm_scale,
+                     void *out, int64_t out_stride_tok, int64_t out_stride_head,
+                     void *workspace, int64_t workspace_bytes,
+                     void *stream);
+
+/* Workspace bytes rq_paged_prefill needs (the same tile images as
+ * rq_int8_prefill_workspace_bytes).  No counterpart in the reference, which
+ * writes a decompressed copy of every referenced page instead. */
+int64_t rq_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len);
 
 #ifdef __cplusplus
 }

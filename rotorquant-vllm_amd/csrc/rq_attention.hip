@@ -70,17 +70,6 @@ constexpr int kItems = 512;
 constexpr int kMinWaves = 4;  // so that a thread has at most 2 items
 constexpr int kMaxWaves = 8;  // GQA groups above 8 heads are split over workgroups
 
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
-    if constexpr (DT == RQ_DTYPE_BF16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                       0, 0, 0);
-    else
-        return mfma_f16(a, b, c);
-}
-
 struct AttnArgs {
     const void *q;
     int64_t q_st, q_sh;

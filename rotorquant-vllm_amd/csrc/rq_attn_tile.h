@@ -32,6 +32,19 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                   0);
 }
 
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+
+// 16-bit MFMA in the q dtype (bf16 or fp16 operands, fp32 accumulation): Q K^T
+// over K rounded to the q dtype.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == RQ_DTYPE_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+    else
+        return mfma_f16(a, b, c);
+}
+
 // Two fp32 values rounded to fp16, packed low | high << 16 (one v_cvt_pk_f16_f32).
 __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;

@@ -78,6 +78,7 @@ struct PrefillArgs {
     const float *R;
     int rot_block;
     float score_scale;  // sm_scale * log2(e)
+    int causal;         // 0: every query sees all seq_lens[b] keys
     int qb;             // query positions per workgroup (= 16 * position groups)
     int npg;            // position groups per workgroup
     int64_t max_tiles;  // tile images per (sequence, kv head) in the workspace
@@ -93,6 +94,13 @@ struct PrefillArgs {
 // gfx950; these swizzles measured conflict-free (same speed as contiguous reads).
 //   K row r, piece c (0..7):   r * 128 + 16 * (c ^ (r & 7))
 //   V^T row d, piece c (0..7): the same (8 keys of 16 bits per piece)
+// K operand modes of the tile image and the attention kernel:
+//   kKqInt8: K hi/lo int8 rows (the int8 prefill, rq_int8_prefill);
+//   kKqDtype: K rows in the q dtype, dtype(centroid * norm) -- the reference's
+//     non-fused numerics (K and V rounded to the q dtype, rq_paged_prefill) --
+//     as two [64 keys][64 dims] halves in the same 16 KB and the same swizzle
+//     (piece c of key r's half h holds dims 64h + 8c .. +7 in order).
+constexpr int kKqInt8 = 0, kKqDtype = 1;
 constexpr int kKP = kPD;                            // K row pitch
 constexpr int kImKhi = 0;                           // [64 keys][kKP] int8, dims permuted per 8
 constexpr int kImKlo = kImKhi + kKT * kKP;          // same, low parts
@@ -120,7 +128,7 @@ __device__ __forceinline__ int visible_keys(const PrefillArgs &a, int64_t seq) {
 }
 
 // ---- pack: one workgroup (256 threads) per (tile, kv head, sequence) --------
-template <int DT>
+template <int DT, int KQ>
 __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     const int tile = blockIdx.x, h = blockIdx.y;
     const int64_t seq = blockIdx.z;
@@ -141,7 +149,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     __shared__ float krho[kKT], vnorm[kKT];
     __shared__ float vscale;  // 2^-e_v
     if (tid < 16) {
-        ktab[tid] = tid < a.nkc ? a.kc[tid] * (127.f / kmax) : 0.f;
+        ktab[tid] = tid < a.nkc ? (KQ == kKqInt8 ? a.kc[tid] * (127.f / kmax) : a.kc[tid]) : 0.f;
         vtab[tid] = tid < a.nvc ? a.vc[tid] : 0.f;
     }
     if (tid < kKT) {
@@ -177,10 +185,11 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         // value: the attention kernel's row-sum MFMA reads it.  Norms above 2^24 would
         // overflow v' in fp16.
         const int e_v = min(24, max(-14, (int)((__float_as_uint(vx) >> 23) & 0xffu) - 126));
-        krho[tid] = nkv / s_k;
+        krho[tid] = KQ == kKqInt8 ? nkv / s_k : nkv;  // q-dtype K: the norm itself
         vnorm[tid] = nvv;
         if (tid == 0) {
-            *reinterpret_cast<float *>(img + kImSk) = s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f));
+            *reinterpret_cast<float *>(img + kImSk) =
+                KQ == kKqInt8 ? s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f)) : a.score_scale;
             *reinterpret_cast<int *>(img + kImVe) = e_v;
             const uint32_t w = pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v));
             *reinterpret_cast<u32x4 *>(img + kImOnes) = u32x4{w, w, w, w};
@@ -189,6 +198,23 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         }
     }
     __syncthreads();
+    if constexpr (KQ == kKqDtype) {
+        // K rows in the q dtype: dims 8 dw .. 8 dw + 7 of key tk, one 16-byte piece
+        for (int w = tid; w < kKT * 16; w += 256) {
+            const int tk = w >> 4, dw = w & 15;
+            const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
+            const float nrm = krho[tk];
+            uint32_t pr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {  // byte j: dim 8 dw + 2j in the high nibble, + 1 in the low one
+                const uint32_t e0 = Elem<DT>::from_f32(opaque(ktab[(x >> (8 * j + 4)) & 15u] * nrm));
+                const uint32_t e1 = Elem<DT>::from_f32(opaque(ktab[(x >> (8 * j)) & 15u] * nrm));
+                pr[j] = e0 | (e1 << 16);
+            }
+            *reinterpret_cast<u32x4 *>(img + kImKhi + (dw >> 3) * (kKT * kKP) + k_piece(tk, dw & 7)) =
+                u32x4{pr[0], pr[1], pr[2], pr[3]};
+        }
+    } else
     // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
     for (int w = tid; w < kKT * 16; w += 256) {
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
@@ -239,7 +265,10 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t idx = (x[i] >> (8 * j + (par ? 0 : 4))) & 15u;
-                    e[i] = f32_to_f16_bits(opaque(vtab[idx] * nv[i]) * vs);
+                    // q-dtype K: V rounded to the q dtype first (exact in fp16 after the scale)
+                    const float v = KQ == kKqInt8 ? opaque(vtab[idx] * nv[i])
+                                                  : Elem<DT>::to_f32(Elem<DT>::from_f32(opaque(vtab[idx] * nv[i])));
+                    e[i] = f32_to_f16_bits(v * vs);
                 }
                 *reinterpret_cast<uint2 *>(img + kImVt + k_piece(d, piece) + elem_off) =
                     make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
@@ -248,7 +277,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     }
 }
 
-template <int DT>
+template <int DT, int KQ>
 __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     int qblk, h;
     int64_t seq;
@@ -280,7 +309,8 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
 
     // ---- key range: causal bound of the whole workgroup --------------------------
     const int last_i = min(T, (qblk + 1) * a.qb) - 1;
-    const int kv_end = min(L_eff, pos_base + last_i + 1);  // keys [0, kv_end) may be visible
+    const bool causal = KQ == kKqInt8 || a.causal;  // the int8 prefill is always causal
+    const int kv_end = causal ? min(L_eff, pos_base + last_i + 1) : L_eff;  // keys [0, kv_end) may be visible
     const int n_tiles = (kv_end + kKT - 1) / kKT;
 
     // Tile images of this (sequence, kv head), copied global -> LDS 1 KB per wave
@@ -307,8 +337,29 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     // ---- Q^T operand (cols = this wave's 16 positions): q_rot rounded to the q dtype,
     //      quantised per position to hi/lo int8, dims in the permuted order of K ----
     u32x4 qh[2], ql[2];
-    float sq = 0.f;
-    if (wave_active) {
+    float sq = KQ == kKqInt8 ? 0.f : 1.f;
+    if (KQ == kKqDtype && wave_active) {
+        // q-dtype K: the operand is q_rot rounded to the q dtype, k-step s = dims 32s + 8g .. +7
+        const int qi = i0 + col;
+        const bool qvalid = qi < T;
+        const uint16_t *qrow = reinterpret_cast<const uint16_t *>(a.q) + (int64_t)(q0 + (qvalid ? qi : 0)) * a.q_st +
+                               (int64_t)hq * a.q_sh;
+#pragma unroll
+        for (int s_ = 0; s_ < 4; ++s_) {
+            const int base = 32 * s_ + 8 * g;
+            const uint4 rw = qvalid ? *reinterpret_cast<const uint4 *>(qrow + base) : make_uint4(0, 0, 0, 0);
+            const uint32_t w16[4] = {rw.x, rw.y, rw.z, rw.w};
+            float xin[8], qr[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) xin[k] = Elem<DT>::to_f32((w16[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+            rotate_q8<DT>(xin, base, a.R, a.rot_block, qr);
+            uint32_t pk[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) pk[k] = Elem<DT>::from_f32(qr[2 * k]) | (Elem<DT>::from_f32(qr[2 * k + 1]) << 16);
+            (s_ < 2 ? qh[s_] : ql[s_ - 2]) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        }
+    }
+    if (KQ == kKqInt8 && wave_active) {
         // Lane (g, col) holds the operand of position i0 + col at dims 64s + 16g .. +15
         // (s = 0, 1): it rotates exactly those 32 dims (rotation blocks are aligned
         // to 2 or 4 dims), q_rot rounded to the q dtype.
@@ -385,13 +436,28 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
         const float s_unit = *reinterpret_cast<const float *>(tb + kImSk);  // score unit of this tile
         if (ti >= 1 && ti + 1 < n_tiles) issue_tile(ti + 1);  // tile 1 went out with tile 0
         // (every wave reaches the barrier at the end of the iteration)
-        if (wave_active && k0 <= pos_base + i0 + kPQ - 1) {  // else: tile entirely above this wave's diagonal
+        if (wave_active && (!causal || k0 <= pos_base + i0 + kPQ - 1)) {  // else: tile above this wave's diagonal
         // every key of the tile visible to all 16 positions of this wave: no mask
-        const bool full = nk == kKT && k0 + kKT - 1 <= pos_base + i0;
+        const bool full = nk == kKT && (!causal || k0 + kKT - 1 <= pos_base + i0);
 
         // ---- S^T = K Q^T for 4 key blocks of 16 ----
         // s = hi.hi * 128 + hi.lo + lo.hi; the score proper is s * s_unit * sq.
         float s[16];
+        if constexpr (KQ == kKqDtype) {
+            // S^T = K Q^T on the q-dtype MFMA: four k-steps of 32 dims (half ks / 2 of the key row)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int ko = (ks >> 1) * (kKT * kKP) + 16 * b * kKP + ((ks & 1) ? koff1 : koff0);
+                    const u32x4 kv = *reinterpret_cast<const u32x4 *>(tb + kImKhi + ko);
+                    c = mfma_qk<DT>(kv, ks < 2 ? qh[ks] : ql[ks - 2], c);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[4 * b + i] = c[i];
+            }
+        } else
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             i32x4 chh = i32x4{0, 0, 0, 0}, cx = chh;
@@ -409,7 +475,7 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) s[4 * b + i] = (float)((chh[i] << 7) + cx[i]);
         }
         if (!full) {  // causal and tile-end mask: key < min(k0 + nk, position + 1)
-            const int lim = min(k0 + nk, my_pos + 1) - (k0 + 4 * g);
+            const int lim = (causal ? min(k0 + nk, my_pos + 1) : k0 + nk) - (k0 + 4 * g);
 #pragma unroll
             for (int j = 0; j < 16; ++j) s[j] = (16 * (j >> 2) + (j & 3)) < lim ? s[j] : -INFINITY;
         }
@@ -429,17 +495,17 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     store_rotated<DT>(st, inv_l, orow, a.R, a.rot_block, g);
 }
 
-template <int DT>
+template <int DT, int KQ>
 static void launch_pack(const PrefillArgs &a, int64_t num_seqs, hipStream_t st) {
     dim3 grid((unsigned)a.max_tiles, (unsigned)a.H, (unsigned)num_seqs);
-    hipLaunchKernelGGL((prefill_pack_kernel<DT>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((prefill_pack_kernel<DT, KQ>), grid, dim3(256), 0, st, a);
 }
 
-template <int DT>
+template <int DT, int KQ>
 static void launch_attn(const PrefillArgs &a, int64_t num_seqs, int64_t max_q_len, int nwaves, hipStream_t st) {
     const size_t lds = 2 * (size_t)kImBytes;
     dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)a.H, (unsigned)num_seqs);
-    hipLaunchKernelGGL((prefill_attn_kernel<DT>), grid, dim3(64 * nwaves), lds, st, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<DT, KQ>), grid, dim3(64 * nwaves), lds, st, a);
 }
 
 static int64_t prefill_tiles(int64_t max_seq_len) { return (max_seq_len + kKT - 1) / kKT; }
@@ -453,23 +519,29 @@ extern "C" int64_t rq_int8_prefill_workspace_bytes(int64_t num_seqs, int32_t num
     return num_seqs * num_kv_heads * prefill_tiles(max_seq_len) * kImBytes;
 }
 
-extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
-                               int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
-                               int64_t num_seqs, int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks,
-                               int32_t block_size, int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
-                               int32_t head_dim, int32_t index_layout, const int32_t *block_table,
-                               int64_t max_blocks, int64_t bt_stride_seq, const int32_t *seq_lens,
-                               int64_t max_seq_len,
-                               const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
-                               int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
-                               void *out, int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
-                               int64_t workspace_bytes, void *stream) {
+namespace {
+
+// The two entry points share the kernels; kq selects the K operand (int8 hi/lo, or
+// rounded to the q dtype with V rounded likewise) and causal the mask.
+int prefill_call(int kq, int causal, const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                 int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q, int64_t num_seqs,
+                 int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
+                 int64_t stride_block, int64_t stride_token, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t index_layout, const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                 const int32_t *seq_lens, int64_t max_seq_len, const float *k_centroids, int32_t n_k_centroids,
+                 const float *v_centroids, int32_t n_v_centroids, const float *rotation, int32_t rot_block,
+                 float sm_scale, void *out, int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
+                 int64_t workspace_bytes, void *stream) {
     RQ_CHECK_ARG(dtype == RQ_DTYPE_BF16 || dtype == RQ_DTYPE_F16, "prefill dtype must be f16 or bf16");
     RQ_CHECK_ARG(head_dim == kPD, "head_dim %d unsupported (only %d)", head_dim, kPD);
     RQ_CHECK_ARG(num_kv_heads >= 1 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 16,
                  "num_q_heads %d / num_kv_heads %d must be an integer <= 16", num_q_heads, num_kv_heads);
-    RQ_CHECK_ARG((n_k_centroids == 8 || n_k_centroids == 16) && (n_v_centroids == 8 || n_v_centroids == 16),
-                 "centroid counts must be 8 or 16");
+    if (kq == kKqInt8)
+        RQ_CHECK_ARG((n_k_centroids == 8 || n_k_centroids == 16) && (n_v_centroids == 8 || n_v_centroids == 16),
+                     "centroid counts must be 8 or 16");
+    else
+        RQ_CHECK_ARG(n_k_centroids >= 1 && n_k_centroids <= 16 && n_v_centroids >= 1 && n_v_centroids <= 16,
+                     "centroid counts must be 1..16");
     RQ_CHECK_ARG(rot_block == 2 || rot_block == 4, "rot_block %d must be 2 or 4", rot_block);
     RQ_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && block_size >= 1 && max_blocks >= 0 &&
                      max_seq_len >= 0,
@@ -512,6 +584,7 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.R = rotation;
     a.rot_block = rot_block;
     a.score_scale = sm_scale * kLog2eP;
+    a.causal = causal != 0;
     a.npg = std::max(1, 8 / a.G);
     a.qb = kPQ * a.npg;
     a.max_tiles = prefill_tiles(max_seq_len);
@@ -521,11 +594,64 @@ extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, in
     a.o_sh = out_stride_head;
     const int nwaves = a.G * a.npg;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == RQ_DTYPE_BF16) launch_pack<RQ_DTYPE_BF16>(a, num_seqs, st);
-    else launch_pack<RQ_DTYPE_F16>(a, num_seqs, st);
+    const bool bf = dtype == RQ_DTYPE_BF16;
+    if (kq == kKqInt8) {
+        if (bf) launch_pack<RQ_DTYPE_BF16, kKqInt8>(a, num_seqs, st);
+        else launch_pack<RQ_DTYPE_F16, kKqInt8>(a, num_seqs, st);
+    } else {
+        if (bf) launch_pack<RQ_DTYPE_BF16, kKqDtype>(a, num_seqs, st);
+        else launch_pack<RQ_DTYPE_F16, kKqDtype>(a, num_seqs, st);
+    }
     int rc = check_launch("prefill_pack_kernel");
     if (rc) return rc;
-    if (dtype == RQ_DTYPE_BF16) launch_attn<RQ_DTYPE_BF16>(a, num_seqs, max_q_len, nwaves, st);
-    else launch_attn<RQ_DTYPE_F16>(a, num_seqs, max_q_len, nwaves, st);
+    if (kq == kKqInt8) {
+        if (bf) launch_attn<RQ_DTYPE_BF16, kKqInt8>(a, num_seqs, max_q_len, nwaves, st);
+        else launch_attn<RQ_DTYPE_F16, kKqInt8>(a, num_seqs, max_q_len, nwaves, st);
+    } else {
+        if (bf) launch_attn<RQ_DTYPE_BF16, kKqDtype>(a, num_seqs, max_q_len, nwaves, st);
+        else launch_attn<RQ_DTYPE_F16, kKqDtype>(a, num_seqs, max_q_len, nwaves, st);
+    }
     return check_launch("prefill_attn_kernel");
+}
+
+}  // namespace
+
+extern "C" int rq_int8_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                               int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
+                               int64_t num_seqs, int64_t max_q_len, const uint8_t *kv_cache, int64_t num_blocks,
+                               int32_t block_size, int64_t stride_block, int64_t stride_token, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t index_layout, const int32_t *block_table,
+                               int64_t max_blocks, int64_t bt_stride_seq, const int32_t *seq_lens,
+                               int64_t max_seq_len,
+                               const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
+                               int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
+                               void *out, int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
+                               int64_t workspace_bytes, void *stream) {
+    return prefill_call(kKqInt8, 1, q, dtype, total_q, num_q_heads, q_stride_tok, q_stride_head, cu_seqlens_q,
+                        num_seqs, max_q_len, kv_cache, num_blocks, block_size, stride_block, stride_token,
+                        num_kv_heads, head_dim, index_layout, block_table, max_blocks, bt_stride_seq, seq_lens,
+                        max_seq_len, k_centroids, n_k_centroids, v_centroids, n_v_centroids, rotation, rot_block,
+                        sm_scale, out, out_stride_tok, out_stride_head, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t rq_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t num_kv_heads, int64_t max_seq_len) {
+    return rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len);
+}
+
+extern "C" int rq_paged_prefill(const void *q, int32_t dtype, int64_t total_q, int32_t num_q_heads,
+                                int64_t q_stride_tok, int64_t q_stride_head, const int32_t *cu_seqlens_q,
+                                int64_t num_seqs, int64_t max_q_len, int32_t causal, const uint8_t *kv_cache,
+                                int64_t num_blocks, int32_t block_size, int64_t stride_block, int64_t stride_token,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                                const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                                const int32_t *seq_lens, int64_t max_seq_len, const float *k_centroids,
+                                int32_t n_k_centroids, const float *v_centroids, int32_t n_v_centroids,
+                                const float *rotation, int32_t rot_block, float sm_scale, void *out,
+                                int64_t out_stride_tok, int64_t out_stride_head, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
+    return prefill_call(kKqDtype, causal, q, dtype, total_q, num_q_heads, q_stride_tok, q_stride_head, cu_seqlens_q,
+                        num_seqs, max_q_len, kv_cache, num_blocks, block_size, stride_block, stride_token,
+                        num_kv_heads, head_dim, index_layout, block_table, max_blocks, bt_stride_seq, seq_lens,
+                        max_seq_len, k_centroids, n_k_centroids, v_centroids, n_v_centroids, rotation, rot_block,
+                        sm_scale, out, out_stride_tok, out_stride_head, workspace, workspace_bytes, stream);
 }

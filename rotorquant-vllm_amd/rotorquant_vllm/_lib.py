@@ -47,6 +47,11 @@ _SIGNATURES = {
     "rq_paged_attention": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_p,
                                     _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
                                     _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p]),
+    "rq_paged_prefill_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i64]),
+    "rq_paged_prefill": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_p,
+                                  _c_i64, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64,
+                                  _c_p, _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64,
+                                  _c_p, _c_i64, _c_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

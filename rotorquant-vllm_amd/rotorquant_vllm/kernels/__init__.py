@@ -15,7 +15,8 @@ the C ABI (include/rq_abi.h).  Differences, all deliberate:
   behaves as the reference: all q tokens are the sequence's last q_len tokens.
 * paged_attention has no op-level counterpart: it is the backend's non-fused
   path (paged decompress + flash_attn_varlen_func + the two rotations,
-  rq_backend.py:937-1036) as one launch.
+  rq_backend.py:937-1036) as one launch; paged_prefill is the same arithmetic
+  in two launches (each 64-key tile decoded once), for long queries.
 """
 from __future__ import annotations
 
@@ -36,6 +37,7 @@ __all__ = [
     "compress_store",
     "paged_decompress",
     "paged_attention",
+    "paged_prefill",
     "rotation_block",
     "shared_workspace",
 ]
@@ -500,4 +502,54 @@ def paged_attention(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.
         sl.data_ptr(), kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(), blk, float(sm_scale),
         out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(dev))
     _lib.check(rc, "rq_paged_attention")
+    return out
+
+
+def paged_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                  cu_seqlens_q: torch.Tensor, max_q_len: int, k_centroids: torch.Tensor, v_centroids: torch.Tensor,
+                  rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
+                  sm_scale: float | None = None, causal: bool = True, out: torch.Tensor | None = None,
+                  max_seq_len: int | None = None, workspace: torch.Tensor | None = None,
+                  dense3: bool = False) -> torch.Tensor:
+    """paged_attention's arithmetic (the reference's non-fused path, rq_backend.py:937-1036)
+    in two launches for long queries (rq_paged_prefill): every 64-key tile of every
+    (sequence, kv head) is decoded once into a tile image (K and V in q's dtype),
+    then streamed by the attention kernel.
+
+    Arguments as for paged_attention; max_seq_len bounds every seq_lens entry
+    (default: the block table's capacity) and sizes the workspace, which may be
+    passed (rq_paged_prefill_workspace_bytes bytes) or comes from the shared
+    per-device prefill buffer.
+    """
+    num_tokens, H_Q, D = q.shape
+    assert D == head_dim
+    assert H_Q % num_kv_heads == 0
+    assert kv_cache.dtype == torch.uint8
+    assert block_table.dtype == torch.int32 and seq_lens.dtype == torch.int32
+    assert cu_seqlens_q.dtype == torch.int32
+    dev = _require_device(q, kv_cache, block_table, seq_lens, cu_seqlens_q)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    bt = block_table if block_table.stride(-1) == 1 else block_table.contiguous()
+    blk = rotation_block(rotation)
+    R = _f32(rotation, dev)
+    kc, vc = _f32(k_centroids, dev), _f32(v_centroids, dev)
+    cu, sl = cu_seqlens_q.contiguous(), seq_lens.contiguous()
+    if max_seq_len is None:
+        max_seq_len = bt.shape[1] * block_size
+    L = _lib.load()
+    need = L.rq_paged_prefill_workspace_bytes(sl.numel(), num_kv_heads, max_seq_len)
+    ws = workspace if workspace is not None and workspace.numel() >= need else shared_workspace(dev, "prefill", need)
+    rc = L.rq_paged_prefill(
+        q.data_ptr(), _lib.dtype_code(q.dtype), num_tokens, H_Q, q.stride(0), q.stride(1), cu.data_ptr(),
+        sl.numel(), int(max_q_len), 1 if causal else 0, kv_cache.data_ptr(), kv_cache.shape[0], block_size,
+        kv_cache.stride(0), kv_cache.stride(1), num_kv_heads, head_dim, _layout(dense3), bt.data_ptr(), bt.shape[1],
+        bt.stride(0), sl.data_ptr(), max_seq_len, kc.data_ptr(), kc.numel(), vc.data_ptr(), vc.numel(), R.data_ptr(),
+        blk, float(sm_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
+        _lib.stream_ptr(dev))
+    _lib.check(rc, "rq_paged_prefill")
     return out

@@ -15,7 +15,9 @@ librq_hip.so (include/rq_abi.h):
     decode            -> rq_fused_decode     (Q and output rotation inside)
     prefill           -> rq_int8_prefill     (int8 MFMA, multi-sequence)
     non-fused path    -> rq_paged_attention  (K/V dequantized to the q dtype in
-                         LDS, 16-bit MFMA; head_size 128), other head sizes
+                         LDS, 16-bit MFMA; head_size 128; decodes), and for
+                         longer queries rq_paged_prefill (the same arithmetic,
+                         each tile decoded once); other head sizes
                          rq_paged_decompress + device attention in fp32
 
 vLLM itself is imported lazily: without vLLM the module still imports (the
@@ -112,6 +114,7 @@ _fused_paged_rq_int8_prefill_fn = None
 _compress_store_fn = None
 _paged_decompress_fn = None
 _paged_attention_fn = None
+_paged_prefill_fn = None
 _shared_workspace = None
 try:
     from rotorquant_vllm import _lib as _rq_lib
@@ -119,6 +122,7 @@ try:
     from rotorquant_vllm.kernels import fused_paged_rq_decode as _fused_paged_rq_decode_fn
     from rotorquant_vllm.kernels import fused_paged_rq_int8_prefill as _fused_paged_rq_int8_prefill_fn
     from rotorquant_vllm.kernels import paged_attention as _paged_attention_fn
+    from rotorquant_vllm.kernels import paged_prefill as _paged_prefill_fn
     from rotorquant_vllm.kernels import paged_decompress as _paged_decompress_fn
     from rotorquant_vllm.kernels import shared_workspace as _shared_workspace
 
@@ -127,6 +131,12 @@ try:
     _fused_prefill_kernel_available = True
 except (ImportError, OSError, RuntimeError) as exc:
     logger.info("RotorQuant HIP kernels unavailable: %s", exc)
+
+# Queries of at most this many tokens take the non-fused path's one-launch kernel
+# (rq_paged_attention: one query block per (sequence, kv head), each tile decoded
+# once anyway); longer ones take rq_paged_prefill, which decodes each tile once
+# for all query blocks instead of once per block.
+RQ_UNFUSED_SHORT_Q = 16
 
 # Shapes the fused kernels take (checked again by the C ABI): head_dim 128, a
 # GQA group of at most 16 query heads, at most 64 kv heads.
@@ -576,7 +586,7 @@ class RQAttentionImpl(_ImplBase):
             if self._fused_paged_available:
                 _shared_workspace(dev, "decode", lib.rq_fused_decode_workspace_bytes(
                     self._max_num_seqs, self.num_heads, self.head_size, cap))
-            if self._fused_prefill_available:
+            if self._fused_prefill_available or self._unfused_kernel_ok(compute_dtype, self.num_heads):
                 _shared_workspace(dev, "prefill", lib.rq_int8_prefill_workspace_bytes(1, self.num_kv_heads, cap))
         self._cg_buffers_ready = True
 
@@ -670,29 +680,62 @@ class RQAttentionImpl(_ImplBase):
 
     # -- non-fused path -----------------------------------------------------------
 
+    def _unfused_kernel_ok(self, dtype, num_heads: int) -> bool:
+        """The non-fused kernels take this layer's shapes and dtype."""
+        return (_paged_attention_fn is not None and dtype in (torch.float16, torch.bfloat16)
+                and _fused_shape_ok(num_heads, self.num_kv_heads, self.head_size) is None)
+
     def _forward_unfused(self, query, kv_cache, md, output, num_actual_tokens):
         """Non-fused path (replaces :937-1036: q pre-rotation, paged decompress to the q
         dtype, flash_attn_varlen_func, back-rotation).
 
-        head_size 128, f16/bf16: one rq_paged_attention launch over the whole batch
-        (K/V tiles dequantized to the q dtype in LDS; no workspace, no host read of
-        the metadata, capturable in a HIP graph).  Other shapes: the device path
+        head_size 128, f16/bf16: queries of at most RQ_UNFUSED_SHORT_Q tokens (decodes)
+        take one rq_paged_attention launch over the whole batch (K/V tiles dequantized
+        to the q dtype in LDS; no workspace, no host read of the metadata, capturable
+        in a HIP graph).  A batch with longer queries sends its leading short ones
+        (vLLM orders decodes first) to rq_paged_attention and the rest to
+        rq_paged_prefill (same arithmetic; each 64-key tile decoded once into the
+        prefill workspace, in groups that fit it).  Other shapes: the device path
         _forward_unfused_torch."""
         q = query[:num_actual_tokens]
-        if (_paged_attention_fn is not None and q.dtype in (torch.float16, torch.bfloat16)
-                and _fused_shape_ok(q.shape[1], self.num_kv_heads, self.head_size) is None):
-            max_q = getattr(md, "max_query_len", None)
-            if max_q is None:
-                qsl = getattr(md, "rq_query_start_loc_cpu", None)
-                qsl = qsl if qsl is not None else md.query_start_loc.cpu()
-                max_q = int((qsl[1:] - qsl[:-1]).max()) if qsl.numel() > 1 else 0
-            kc, vc, R = self._launch_operands()
+        if not self._unfused_kernel_ok(q.dtype, q.shape[1]):
+            return self._forward_unfused_torch(query, kv_cache, md, output, num_actual_tokens)
+        max_q = getattr(md, "max_query_len", None)
+        qsl_cpu = None
+        if max_q is None:
+            qsl_cpu = getattr(md, "rq_query_start_loc_cpu", None)
+            qsl_cpu = qsl_cpu if qsl_cpu is not None else md.query_start_loc.cpu()
+            max_q = int((qsl_cpu[1:] - qsl_cpu[:-1]).max()) if qsl_cpu.numel() > 1 else 0
+        kc, vc, R = self._launch_operands()
+        BS = kv_cache.shape[1]
+        causal = bool(getattr(md, "causal", True))
+        out = output[:num_actual_tokens]
+        if int(max_q) <= RQ_UNFUSED_SHORT_Q or _paged_prefill_fn is None or _shared_workspace is None:
             _paged_attention_fn(q, kv_cache, md.block_table, md.seq_lens, md.query_start_loc, int(max_q), kc, vc, R,
-                                self.num_kv_heads, self.head_size, kv_cache.shape[1], sm_scale=self.scale,
-                                causal=bool(getattr(md, "causal", True)), out=output[:num_actual_tokens],
+                                self.num_kv_heads, self.head_size, BS, sm_scale=self.scale, causal=causal, out=out,
                                 **self._layout_kw())
             return output
-        return self._forward_unfused_torch(query, kv_cache, md, output, num_actual_tokens)
+        if qsl_cpu is None:
+            qsl_cpu = getattr(md, "rq_query_start_loc_cpu", None)
+            qsl_cpu = qsl_cpu if qsl_cpu is not None else md.query_start_loc.cpu()
+        sl_cpu = getattr(md, "rq_seq_lens_cpu", None)
+        qsl = qsl_cpu.tolist()
+        lens = (sl_cpu if sl_cpu is not None else md.seq_lens.cpu()).tolist()
+        B = len(lens)
+        q_lens = [qsl[b + 1] - qsl[b] for b in range(B)]
+        ns = 0
+        while ns < B and q_lens[ns] <= RQ_UNFUSED_SHORT_Q:
+            ns += 1
+        bt = md.block_table
+        if ns:
+            _paged_attention_fn(q, kv_cache, bt[:ns], md.seq_lens[:ns], md.query_start_loc[:ns + 1],
+                                max(q_lens[:ns]), kc, vc, R, self.num_kv_heads, self.head_size, BS,
+                                sm_scale=self.scale, causal=causal, out=out, **self._layout_kw())
+        for g0, g1, mx, mq in self._prefill_groups(lens, q_lens, ns, BS, bt.shape[1], query.device):
+            _paged_prefill_fn(q, kv_cache, bt[g0:g1], md.seq_lens[g0:g1], md.query_start_loc[g0:g1 + 1], mq, kc, vc,
+                              R, self.num_kv_heads, self.head_size, BS, sm_scale=self.scale, causal=causal, out=out,
+                              max_seq_len=mx, **self._layout_kw())
+        return output
 
     def _forward_unfused_torch(self, query, kv_cache, md, output, num_actual_tokens):
         """Paged decompress + fp32 attention on the device, for shapes rq_paged_attention

@@ -211,10 +211,11 @@ def test_workspace_growth_keeps_captured_buffers_alive(monkeypatch):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_unfused_path_is_one_paged_attention_call(monkeypatch, causal):
-    """Without RQ_USE_FUSED_PAGED a mixed batch is one rq_paged_attention call over the
-    whole batch, with vLLM's device metadata as is (no host copies read) and
-    max_query_len / causal from the metadata."""
+def test_unfused_short_queries_are_one_paged_attention_call(monkeypatch, causal):
+    """Without RQ_USE_FUSED_PAGED a batch whose queries are all short (at most
+    RQ_UNFUSED_SHORT_Q tokens) is one rq_paged_attention call over the whole batch,
+    with vLLM's device metadata as is (no host copies read) and max_query_len /
+    causal from the metadata."""
     impl = _bare_impl(False, False)
     calls = []
 
@@ -226,11 +227,58 @@ def test_unfused_path_is_one_paged_attention_call(monkeypatch, causal):
         out.fill_(2.0)
         return out
 
+    def no_prefill(*a, **k):
+        raise AssertionError("short queries must not reach rq_paged_prefill")
+
     monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", fake)
-    md = _mixed_metadata([1, 1, 40, 7], [500, 30, 300, 107], host_copies=False)
+    monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", no_prefill)
+    md = _mixed_metadata([1, 1, 16, 7], [500, 30, 300, 107], host_copies=False)
     md.causal = causal
     query = torch.randn(md.num_actual_tokens + 3, 32, 128, dtype=torch.bfloat16)  # 3 padding rows
     output = torch.zeros_like(query)
     impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
-    assert calls == [((49, 32, 128), True, True, True, 40, causal, 8, 128, 16, 0.125)]
-    assert torch.all(output[:49] == 2.0) and torch.all(output[49:] == 0.0)
+    assert rq_backend_module.RQ_UNFUSED_SHORT_Q == 16
+    assert calls == [((25, 32, 128), True, True, True, 16, causal, 8, 128, 16, 0.125)]
+    assert torch.all(output[:25] == 2.0) and torch.all(output[25:] == 0.0)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_unfused_long_queries_split_to_paged_prefill(monkeypatch, causal):
+    """A non-fused batch with a query longer than RQ_UNFUSED_SHORT_Q: its leading short
+    queries (sequences 0..1) are one rq_paged_attention call, the rest go to
+    rq_paged_prefill in contiguous groups whose tile images fit the prefill workspace
+    (sized here for 2 x 320 keys x 8 kv heads), each with its own max_seq_len and
+    max_q_len; every query row is written exactly once."""
+    from rotorquant_vllm import _lib
+    from rotorquant_vllm import kernels as K
+    impl = _bare_impl(False, False)
+    calls = []
+
+    def fake_attn(q, kv_cache, block_table, seq_lens, cu_seqlens_q, max_q_len, kc, vc, R, num_kv_heads, head_dim,
+                  block_size, sm_scale=None, causal=True, out=None):
+        calls.append(("attn", seq_lens.tolist(), cu_seqlens_q.tolist(), tuple(block_table.shape), max_q_len, causal))
+        cu = cu_seqlens_q.tolist()
+        out[cu[0]:cu[-1]] += 1.0
+        return out
+
+    def fake_prefill(q, kv_cache, block_table, seq_lens, cu_seqlens_q, max_q_len, kc, vc, R, num_kv_heads, head_dim,
+                     block_size, sm_scale=None, causal=True, out=None, max_seq_len=None, workspace=None):
+        calls.append(("prefill", seq_lens.tolist(), cu_seqlens_q.tolist(), max_q_len, max_seq_len, causal))
+        cu = cu_seqlens_q.tolist()
+        out[cu[0]:cu[-1]] += 1.0
+        return out
+
+    monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", fake_attn)
+    monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", fake_prefill)
+    budget = _lib.load().rq_paged_prefill_workspace_bytes(2, 8, 320)
+    monkeypatch.setitem(K._ws_cache, ("cpu", "prefill"), torch.empty(budget, dtype=torch.uint8))
+    q_lens, seq_lens = [1, 3, 40, 7, 100], [500, 30, 300, 107, 320]
+    md = _mixed_metadata(q_lens, seq_lens)
+    md.causal = causal
+    query = torch.randn(md.num_actual_tokens, 32, 128, dtype=torch.float16)
+    output = torch.zeros_like(query)
+    impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
+    assert calls == [("attn", [500, 30], [0, 1, 4], (2, 64), 3, causal),
+                     ("prefill", [300, 107], [4, 44, 51], 40, 300, causal),
+                     ("prefill", [320], [51, 151], 100, 320, causal)]
+    assert torch.all(output == 1.0)

@@ -1,4 +1,6 @@
-"""GPU parity: rq_paged_attention (the non-fused path in one kernel) vs the float64 oracle.
+"""GPU parity: the non-fused path's kernels vs the float64 oracle -- rq_paged_attention
+(one kernel, K/V tiles dequantized in LDS) and rq_paged_prefill (each 64-key tile
+decoded once into a workspace, then attention), every case run through both.
 
 The oracle is oracle.unfused_attention: the reference's non-fused path
 (rq_backend.py:937-1036) with K/V decompressed to the q dtype and the
@@ -32,10 +34,18 @@ def _dev(x):
     return torch.from_numpy(x).to("cuda") if isinstance(x, np.ndarray) else x.to("cuda")
 
 
-def run(case, causal=True, out=None):
+ENTRIES = ["paged_attention", "paged_prefill"]
+
+
+@pytest.fixture(params=ENTRIES)
+def entry(request):
+    return request.param
+
+
+def run(case, causal=True, out=None, entry="paged_attention"):
     from rotorquant_vllm import kernels as K
     p = case["p"]
-    res = K.paged_attention(_dev(case["q"]), _dev(case["cache"]), _dev(case["bt"]), _dev(case["lens"]),
+    res = getattr(K, entry)(_dev(case["q"]), _dev(case["cache"]), _dev(case["bt"]), _dev(case["lens"]),
                             _dev(case["cu"]), max(case["q_lens"]), _dev(p.kc), _dev(p.vc), _dev(p.R), case["H"], 128,
                             case["BS"], causal=causal, out=out)
     torch.cuda.synchronize()
@@ -50,10 +60,11 @@ def ref(case, causal=True):
                                causal=causal)
 
 
-def check(case, tag, causal=True, plain_max_abs=False):
+def check(case, tag, causal=True, plain_max_abs=False, entry="paged_attention"):
+    tag = f"{entry}/{tag}"
     print(f"{tag}: seqs={len(case['q_lens'])} q={case['q_lens'][:8]} ctx={case['lens'].tolist()[:8]} "
           f"H={case['H']} HQ={case['HQ']} BS={case['BS']} causal={causal}", flush=True)
-    got, exp = run(case, causal), ref(case, causal)
+    got, exp = run(case, causal, entry=entry), ref(case, causal)
     dt = str(case["q"].dtype).replace("torch.", "")
     err, excess, cs = check_tolerance(got, exp, dt, rot_block=case["p"].blk)
     print(f"{tag}: max_abs={err:.3e} excess_over_bound={excess:.3e} cos={cs:.7f}", flush=True)
@@ -63,62 +74,62 @@ def check(case, tag, causal=True, plain_max_abs=False):
         assert err <= 2e-2, f"{tag}: max_abs={err}"
 
 
-def test_attention_chunks_after_prefixes_iso3():
+def test_attention_chunks_after_prefixes_iso3(entry):
     """Config 1 heads (32 q / 8 kv), iso fast 3-bit; ragged chunks around tile edges after prefixes."""
     q_lens = [1, 15, 16, 17, 64, 65, 130]
     ctx = [q + pre for q, pre in zip(q_lens, [0, 40, 64, 100, 0, 191, 300])]
-    check(attn_case(61, q_lens, ctx, 8, 32, Params("iso", 3, 3)), "chunks-iso3")
+    check(attn_case(61, q_lens, ctx, 8, 32, Params("iso", 3, 3)), "chunks-iso3", entry=entry)
 
 
-def test_attention_decode_batch_one_token_each():
+def test_attention_decode_batch_one_token_each(entry):
     """max_q_len = 1: one 16-position group per workgroup; contexts around tile edges and long."""
     ctx = [1, 2, 63, 64, 65, 129, 1000, 3001]
-    check(attn_case(62, [1] * len(ctx), ctx, 8, 32, Params("iso", 3, 3)), "decode-batch")
+    check(attn_case(62, [1] * len(ctx), ctx, 8, 32, Params("iso", 3, 3)), "decode-batch", entry=entry)
 
 
-def test_attention_gqa7_iso_full_mixed():
+def test_attention_gqa7_iso_full_mixed(entry):
     """Config 4 heads (28 q / 4 kv, GQA 7), iso full 3-bit; decodes and chunks in one launch."""
     q_lens = [1, 1, 200, 64]
     ctx = [500, 77, 200 + 350, 64 + 1]
-    check(attn_case(63, q_lens, ctx, 4, 28, Params("iso", 3, 3, iso_mode="full")), "gqa7-mixed")
+    check(attn_case(63, q_lens, ctx, 4, 28, Params("iso", 3, 3, iso_mode="full")), "gqa7-mixed", entry=entry)
 
 
 @pytest.mark.parametrize("H,HQ", [(2, 32), (2, 24), (1, 9), (8, 8), (4, 12)])
-def test_attention_gqa_widths(H, HQ):
+def test_attention_gqa_widths(H, HQ, entry):
     """GQA 16 / 12 / 9 split over 2 / 2 / 3 workgroups per kv head; GQA 1 and 3 take 4+ waves."""
     q_lens = [33, 1, 100]
     ctx = [33 + 20, 90, 100]
-    check(attn_case(64 + HQ, q_lens, ctx, H, HQ, Params("planar", 4, 3)), f"gqa{HQ // H}")
+    check(attn_case(64 + HQ, q_lens, ctx, H, HQ, Params("planar", 4, 3)), f"gqa{HQ // H}", entry=entry)
 
 
-def test_attention_noncausal():
+def test_attention_noncausal(entry):
     """causal = 0: every query of a sequence sees all its keys."""
     q_lens = [50, 1, 70]
     ctx = [50 + 13, 40, 70]
-    check(attn_case(65, q_lens, ctx, 8, 32, Params("iso", 4, 4)), "noncausal", causal=False)
+    check(attn_case(65, q_lens, ctx, 8, 32, Params("iso", 4, 4)), "noncausal", causal=False, entry=entry)
 
 
-def test_attention_unit_scale_fp16_planar():
+def test_attention_unit_scale_fp16_planar(entry):
     """Unit-scale K/V and fp16 q: the plain 2e-2 bound holds too."""
     q_lens = [80, 1, 40]
     ctx = [80 + 64, 300, 40]
     check(attn_case(66, q_lens, ctx, 8, 32, Params("planar", 3, 3), kv="unit", dtype=torch.float16), "unit-fp16",
-          plain_max_abs=True)
+          plain_max_abs=True, entry=entry)
 
 
 @pytest.mark.parametrize("BS", [12, 32])
-def test_attention_block_sizes(BS):
+def test_attention_block_sizes(BS, entry):
     """Block size 12 (no power of two) and 32."""
     q_lens = [20, 1, 45]
     ctx = [20 + 31, 100, 45]
-    check(attn_case(67, q_lens, ctx, 8, 32, Params("iso", 3, 3), BS=BS), f"bs{BS}")
+    check(attn_case(67, q_lens, ctx, 8, 32, Params("iso", 3, 3), BS=BS), f"bs{BS}", entry=entry)
 
 
-def test_attention_single_key_closed_form():
+def test_attention_single_key_closed_form(entry):
     """L = 1: the output is the back-rotated V row (rounded to bf16 twice), bit-exact
     up to the oracle's rounding of the same value."""
     case = attn_case(68, [1, 1], [1, 1], 2, 8, Params("iso", 4, 4))
-    got, exp = run(case), ref(case)
+    got, exp = run(case, entry=entry), ref(case)
     assert np.abs(got - exp).max() <= 1e-2 * max(1.0, float(np.abs(exp).max()))
 
 
@@ -154,3 +165,21 @@ def test_attention_graph_replay():
         eager = K.paged_attention(*args)
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager), f"replay {r}"
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_paged_prefill_equals_paged_attention(causal):
+    """Same arithmetic in both kernels (K/V rounded to the q dtype, the same fp32
+    online softmax over the same 64-key tiles): outputs equal bit for bit on a
+    mixed batch -- decodes, a chunk after a long prefix, ragged tails -- and also
+    through a view of a larger output tensor (strided rows)."""
+    q_lens = [1, 3, 17, 64, 129, 700]
+    ctx = [900, 5, 17 + 333, 64, 129 + 1, 700 + 64]
+    case = attn_case(71, q_lens, ctx, 8, 32, Params("iso", 3, 3))
+    a = run(case, causal, entry="paged_attention")
+    b = run(case, causal, entry="paged_prefill")
+    assert np.array_equal(a, b)
+    big = torch.zeros(case["q"].shape[0], 40, 128, dtype=case["q"].dtype, device="cuda")
+    c = run(case, causal, out=big[:, 4:36], entry="paged_prefill")
+    assert np.array_equal(a, c)
+    assert torch.all(big[:, :4] == 0) and torch.all(big[:, 36:] == 0)

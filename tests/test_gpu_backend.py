@@ -4,13 +4,14 @@ One prefill step (three ragged prompts) and one decode step through
 RQAttentionImpl.forward, as vLLM drives it (rq_backend.py:858-1036 in the
 reference): new K/V are compressed into the packed cache, then attention runs
 from the cache, fused (RQ_USE_FUSED_PAGED=1: rq_fused_decode / rq_int8_prefill)
-or unfused (rq_paged_attention; or paged decompress + fp32 attention on the
-device, the path kept for other head sizes).  After each step every cache
-byte must equal the oracle's store of the same K/V, and the output must match
-the oracle's attention within the parity tolerance (cos >= 0.999,
-|got - ref| <= max(2e-2, ulp(x) + 2 ulp(rotation-block max))); the
-rq_paged_attention path against the oracle of the reference's non-fused path
-(K/V decompressed to the q dtype).
+or unfused (rq_paged_attention for short queries, rq_paged_prefill for longer
+ones; or paged decompress + fp32 attention on the device, the path kept for
+other head sizes).  After each step every cache byte must equal the oracle's
+store of the same K/V, and the output must match the oracle's attention within
+the parity tolerance (cos >= 0.999, |got - ref| <= max(2e-2, ulp(x) +
+2 ulp(rotation-block max))); the rq_paged_attention / rq_paged_prefill path
+against the oracle of the reference's non-fused path (K/V decompressed to the
+q dtype).
 """
 import math
 import types
@@ -237,19 +238,32 @@ def test_backend_decode_step_graph_replay(monkeypatch):
 
 def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
     """The default (non-fused) path: a mixed batch of decodes and chunks in one forward
-    is one rq_paged_attention launch, checked against the oracle of the reference's
-    non-fused path; then a decode step on the same path captured in a HIP graph
-    replays the eager output bit for bit (no host read of the metadata, no
-    workspace)."""
+    -- the decodes through rq_paged_attention, the two chunks through one
+    rq_paged_prefill call -- checked against the oracle of the reference's non-fused
+    path; then a decode step on the same path captured in a HIP graph replays the
+    eager output bit for bit (no host read of the metadata, no workspace)."""
     ctx = [3000, 700, 5, 800, 64]
     q_lens = [1, 1, 1, 200, 64]
     impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 73, fused=False)
     assert not impl._fused_paged_available and not impl._fused_prefill_available
+    import rotorquant_vllm.vllm.rq_backend as rq_backend_module
+    seen = []
+
+    def counted(name, fn):
+        def wrapper(q, kv_cache, block_table, seq_lens, *a, **k):
+            seen.append((name, seq_lens.shape[0]))
+            return fn(q, kv_cache, block_table, seq_lens, *a, **k)
+        return wrapper
+
+    monkeypatch.setattr(rq_backend_module, "_paged_attention_fn",
+                        counted("attention", rq_backend_module._paged_attention_fn))
+    monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", counted("prefill", rq_backend_module._paged_prefill_fn))
     dev = torch.device("cuda")
     kv_cache = torch.from_numpy(c["cache0"]).to(dev)
     out = torch.empty(c["q"].shape, dtype=torch.bfloat16, device=dev)
     impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
     torch.cuda.synchronize()
+    assert seen == [("attention", 3), ("prefill", 2)], seen
     got_cache = kv_cache.cpu().numpy()
     assert np.array_equal(got_cache, c["full_cache"]), f"{int((got_cache != c['full_cache']).sum())} bytes differ"
     pn = p.np()

@@ -7,7 +7,7 @@
   nibble cache of the same tokens, bit for bit: the two layouts hold the same
   indices and norms and the kernels run the same arithmetic on them (paged
   decompress, fused decode with 8, 4 and 2 kv heads per workgroup, int8
-  prefill, rq_paged_attention);
+  prefill, rq_paged_attention, rq_paged_prefill);
 * the backend with RQ_DENSE_3BIT=1: prefill then decode through
   RQAttentionImpl.forward, cache bytes against the oracle's dense store,
   outputs against the attention oracle.
@@ -102,7 +102,7 @@ def test_fused_decode_dense_equals_nibble(H, HQ):
     assert excess <= 0 and cs >= 0.999
 
 
-def test_int8_prefill_and_paged_attention_dense_equal_nibble():
+def test_prefill_and_paged_attention_dense_equal_nibble():
     from rotorquant_vllm import kernels as K
     p = Params("planar", 3, 3)
     q_lens, ctx = [1, 70, 129], [300, 70, 129 + 40]
@@ -112,7 +112,7 @@ def test_int8_prefill_and_paged_attention_dense_equal_nibble():
     cu = _d(np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32))
     lens = _d(np.asarray(ctx, np.int32))
     print(f"dense prefill / attention: q={q_lens} ctx={ctx}", flush=True)
-    pre, att = [], []
+    pre, att, ppf = [], [], []
     for cache, dense3 in ((nib, False), (den, True)):
         c = _d(cache)
         pre.append(K.fused_paged_rq_int8_prefill(q, c, _d(bt), lens, _d(p.kc), _d(p.vc), _d(p.R), H, D, BS,
@@ -120,9 +120,12 @@ def test_int8_prefill_and_paged_attention_dense_equal_nibble():
                                                  dense3=dense3).cpu())
         att.append(K.paged_attention(q, c, _d(bt), lens, cu, max(q_lens), _d(p.kc), _d(p.vc), _d(p.R), H, D, BS,
                                      dense3=dense3).cpu())
+        ppf.append(K.paged_prefill(q, c, _d(bt), lens, cu, max(q_lens), _d(p.kc), _d(p.vc), _d(p.R), H, D, BS,
+                                   dense3=dense3).cpu())
         torch.cuda.synchronize()
     assert torch.equal(pre[0], pre[1])
     assert torch.equal(att[0], att[1])
+    assert torch.equal(ppf[0], ppf[1]) and torch.equal(ppf[0], att[0])
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])

@@ -84,7 +84,7 @@ class TestABI:
         assert set(syms) == set(_lib.EXPORTED)
 
     def test_version(self):
-        assert _lib.load().rq_abi_version() == 5
+        assert _lib.load().rq_abi_version() == 6
 
     def test_argument_validation_without_gpu(self):
         """Bad arguments are rejected before any device work, with a message."""
@@ -112,6 +112,17 @@ class TestABI:
                             (dict(il=2), b"index_layout")):
             rc = lib.rq_paged_attention(*{**base, **change}.values())
             assert rc == 1 and msg in lib.rq_last_error(), change
+        # rq_paged_prefill: the same checks, plus its workspace (none given here)
+        pre = {k: v for k, v in base.items() if k != "stream"}
+        pre = {**{k: pre[k] for k in list(pre)[:list(pre).index("sl") + 1]}, "msl": 16,
+               **{k: pre[k] for k in list(pre)[list(pre).index("sl") + 1:]}, "ws": None, "wsb": 0, "stream": None}
+        for change, msg in ((dict(d=64), b"head_dim"), (dict(hq=136), b"integer <= 16"), (dict(rb=8), b"rot_block"),
+                            (dict(nk=17), b"centroid"), (dict(dtype=2), b"dtype"), (dict(il=1, nv=16), b"dense"),
+                            (dict(il=2), b"index_layout"), (dict(msl=-1), b"bad sizes"), ({}, b"workspace")):
+            rc = lib.rq_paged_prefill(*{**pre, **change}.values())
+            assert rc == 1 and msg in lib.rq_last_error(), change
+        assert lib.rq_paged_prefill(*{**pre, "msl": 0}.values()) == 0  # nothing to attend: no launch
+        assert lib.rq_paged_prefill_workspace_bytes(3, 8, 1000) == lib.rq_int8_prefill_workspace_bytes(3, 8, 1000)
         with pytest.raises(ValueError):
             _lib.check(1, "x")
 
