@@ -12,7 +12,10 @@ each case also prints its max-abs, the number of elements above the flat
 Where the oracle would take minutes, a seeded subset is checked and stated:
 config 2 checks 32 of its 256 sequences, config 4's decode part the
 131072-token sequence and 31 of its 127 companions, config 3 and config 4's
-chunks every 32nd query row plus the last 32 of each sequence.
+chunks every 32nd query row plus the last 32 of each sequence.  Config 3 and
+config 4's chunks run through both prefill kernels: rq_int8_prefill (the fused
+path) against the prefill oracle, rq_paged_prefill (the non-fused path's long
+queries) against the non-fused oracle (K/V rounded to the q dtype).
 """
 import math
 
@@ -92,21 +95,30 @@ def test_config4_decode_part():
     torch.cuda.empty_cache()
 
 
-def _prefill_check(tag, inp, rows_of):
+def _prefill_check(tag, inp, rows_of, entry="int8"):
+    """entry "int8": rq_int8_prefill (the fused path) against oracle.prefill_attention;
+    "paged": rq_paged_prefill (the non-fused path's long queries) against
+    oracle.unfused_attention (K/V rounded to the q dtype)."""
     from rotorquant_vllm import kernels as K
     p, dev = inp["p"], inp["q"].device
     lens, q_lens = inp["lens_host"], inp["q_lens"]
+    tag = f"{entry}/{tag}"
     print(f"{tag}: seqs={len(lens)} q_tokens={sum(q_lens)} ctx={lens}", flush=True)
-    out = K.fused_paged_rq_int8_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], p.kc.to(dev),
-                                        p.vc.to(dev), p.R.to(dev), inp["H"], 128, 16, cu_seqlens_q=inp["cu"],
-                                        max_q_len=max(q_lens), max_seq_len=max(lens))
+    if entry == "int8":
+        out = K.fused_paged_rq_int8_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], p.kc.to(dev),
+                                            p.vc.to(dev), p.R.to(dev), inp["H"], 128, 16, cu_seqlens_q=inp["cu"],
+                                            max_q_len=max(q_lens), max_seq_len=max(lens))
+    else:
+        out = K.paged_prefill(inp["q"], inp["caches"][0], inp["bt"], inp["lens"], inp["cu"], max(q_lens),
+                              p.kc.to(dev), p.vc.to(dev), p.R.to(dev), inp["H"], 128, 16, max_seq_len=max(lens))
     torch.cuda.synchronize()
     cu = inp["cu"].cpu().numpy()
     rows = np.concatenate([cu[b] + rows_of(q_lens[b]) for b in range(len(lens))])
     sub, bt, sl = host_subcache(inp["caches"][0], inp["bt_host"], lens, list(range(len(lens))))
     pn = p.np()
-    ref = O.prefill_attention(inp["q"].float().cpu().numpy(), cu, sub, bt, sl, inp["H"], 128, pn["kc"], pn["vc"],
-                              pn["R"], 1 / math.sqrt(128), "bfloat16", rows=rows)
+    oracle_fn = O.prefill_attention if entry == "int8" else O.unfused_attention
+    ref = oracle_fn(inp["q"].float().cpu().numpy(), cu, sub, bt, sl, inp["H"], 128, pn["kc"], pn["vc"], pn["R"],
+                    1 / math.sqrt(128), "bfloat16", rows=rows)
     _report(tag, out.float().cpu().numpy()[rows], ref[rows], "bfloat16", p.blk)
 
 
@@ -114,22 +126,24 @@ def _sampled_rows(T):
     return np.unique(np.concatenate([np.arange(0, T, 32), np.arange(max(0, T - 32), T)]))
 
 
-def test_config3_full_size():
-    """Config 3: 8 fresh sequences x 4096 tokens, causal, 32 q / 8 kv, iso fast 4-bit, one launch."""
+@pytest.mark.parametrize("entry", ["int8", "paged"])
+def test_config3_full_size(entry):
+    """Config 3: 8 fresh sequences x 4096 tokens, causal, 32 q / 8 kv, iso fast 4-bit, one call."""
     q_lens = [4096] * 8
     inp = gpu_prefill_inputs(q_lens, q_lens, 8, 32, 3, "iso", 4)
-    _prefill_check("config3 8x4096", inp, _sampled_rows)
+    _prefill_check("config3 8x4096", inp, _sampled_rows, entry)
     del inp
     torch.cuda.empty_cache()
 
 
-def test_config4_chunks_after_prefixes():
+@pytest.mark.parametrize("entry", ["int8", "paged"])
+def test_config4_chunks_after_prefixes(entry):
     """Config 4's prefill part: 4 chunks of 2048 tokens after seeded prefixes U{0..14336},
-    28 q / 4 kv heads, iso full 3-bit, one launch."""
+    28 q / 4 kv heads, iso full 3-bit, one call."""
     pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
     q_lens = [2048] * 4
     ctx = [x + 2048 for x in pre]
     inp = gpu_prefill_inputs(q_lens, ctx, 4, 28, 4, "iso", 3, iso_mode="full")
-    _prefill_check(f"config4 chunks prefixes={pre}", inp, _sampled_rows)
+    _prefill_check(f"config4 chunks prefixes={pre}", inp, _sampled_rows, entry)
     del inp
     torch.cuda.empty_cache()
