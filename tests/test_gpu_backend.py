@@ -304,3 +304,46 @@ def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(outd, eager), f"replay {i}"
+
+
+def test_backend_unfused_prefill_groups(monkeypatch):
+    """The non-fused path with a prefill workspace that holds one 800-token sequence's
+    tile images (4 kv heads): the two chunks of a mixed batch go to rq_paged_prefill
+    in two calls, each with its own max_seq_len and its absolute query rows, and the
+    whole output matches the oracle of the reference's non-fused path."""
+    from rotorquant_vllm import _lib
+    from rotorquant_vllm import kernels as K
+    import rotorquant_vllm.vllm.rq_backend as rq_backend_module
+    ctx = [3000, 700, 5, 800, 64]
+    q_lens = [1, 1, 1, 200, 64]
+    impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 74, fused=False)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    kv_cache = torch.from_numpy(c["cache0"]).to(dev)
+    impl._init_cg_buffers(kv_cache, torch.bfloat16)
+    budget = _lib.load().rq_paged_prefill_workspace_bytes(1, 4, 800)
+    monkeypatch.setitem(K._ws_cache, (str(dev), "prefill"), torch.empty(budget, dtype=torch.uint8, device=dev))
+    seen = []
+
+    def counted(name, fn):
+        def wrapper(q, kv, block_table, seq_lens, cu, max_q, *a, **k):
+            seen.append((name, seq_lens.shape[0], int(max_q), k.get("max_seq_len")))
+            return fn(q, kv, block_table, seq_lens, cu, max_q, *a, **k)
+        return wrapper
+
+    monkeypatch.setattr(rq_backend_module, "_paged_attention_fn",
+                        counted("attention", rq_backend_module._paged_attention_fn))
+    monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", counted("prefill", rq_backend_module._paged_prefill_fn))
+    out = torch.full(c["q"].shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    print(f"unfused prefill groups: ctx={ctx} q_lens={q_lens} workspace={budget} B", flush=True)
+    impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
+    torch.cuda.synchronize()
+    assert seen == [("attention", 3, 1, None), ("prefill", 1, 200, 800), ("prefill", 1, 64, 64)], seen
+    pn = p.np()
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    ref = O.unfused_attention(c["q"].float().numpy(), cu, c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 4, D,
+                              pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), "every query row is written"
+    err, excess, cs = check_tolerance(got, ref, "bfloat16", rot_block=p.blk)
+    print(f"unfused prefill groups: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}", flush=True)
+    assert excess <= 0 and cs >= 0.999
