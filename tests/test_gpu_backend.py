@@ -347,3 +347,44 @@ def test_backend_unfused_prefill_groups(monkeypatch):
     err, excess, cs = check_tolerance(got, ref, "bfloat16", rot_block=p.blk)
     print(f"unfused prefill groups: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}", flush=True)
     assert excess <= 0 and cs >= 0.999
+
+
+def test_backend_fused_prefill_groups(monkeypatch):
+    """The fused path with an int8-prefill workspace that holds one 800-token sequence's
+    tile images (4 kv heads): the decodes go to the fused decode, the two chunks to
+    rq_int8_prefill in two calls, each with its own max_seq_len and its absolute query
+    rows, and every row matches the prefill oracle."""
+    from rotorquant_vllm import _lib
+    from rotorquant_vllm import kernels as K
+    import rotorquant_vllm.vllm.rq_backend as rq_backend_module
+    ctx = [3000, 700, 5, 800, 64]
+    q_lens = [1, 1, 1, 200, 64]
+    impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 75)
+    assert impl._fused_paged_available and impl._fused_prefill_available
+    dev = torch.device("cuda", torch.cuda.current_device())
+    kv_cache = torch.from_numpy(c["cache0"]).to(dev)
+    impl._init_cg_buffers(kv_cache, torch.bfloat16)
+    budget = _lib.load().rq_int8_prefill_workspace_bytes(1, 4, 800)
+    monkeypatch.setitem(K._ws_cache, (str(dev), "prefill"), torch.empty(budget, dtype=torch.uint8, device=dev))
+    seen = []
+    fn = rq_backend_module._fused_paged_rq_int8_prefill_fn
+
+    def counted(*a, **k):
+        seen.append((a[3].shape[0], k.get("max_q_len"), k.get("max_seq_len")))
+        return fn(*a, **k)
+
+    monkeypatch.setattr(rq_backend_module, "_fused_paged_rq_int8_prefill_fn", counted)
+    out = torch.full(c["q"].shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    print(f"fused prefill groups: ctx={ctx} q_lens={q_lens} workspace={budget} B", flush=True)
+    impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
+    torch.cuda.synchronize()
+    assert seen == [(1, 200, 800), (1, 64, 64)], seen
+    pn = p.np()
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    ref = O.prefill_attention(c["q"].float().numpy(), cu, c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 4, D,
+                              pn["kc"], pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16")
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), "every query row is written"
+    err, excess, cs = check_tolerance(got, ref, "bfloat16", rot_block=p.blk)
+    print(f"fused prefill groups: max_abs={err:.3e} excess={excess:.3e} cos={cs:.6f}", flush=True)
+    assert excess <= 0 and cs >= 0.999
