@@ -125,6 +125,14 @@ def test_attention_block_sizes(BS, entry):
     check(attn_case(67, q_lens, ctx, 8, 32, Params("iso", 3, 3), BS=BS), f"bs{BS}", entry=entry)
 
 
+def test_attention_empty_sequences(entry):
+    """Sequences without query tokens, with or without context, between ones that have
+    them: their work items exit at once, and the other sequences' rows are unaffected."""
+    q_lens = [0, 20, 0, 33, 0]
+    ctx = [0, 25, 7, 33, 0]
+    check(attn_case(72, q_lens, ctx, 8, 32, Params("iso", 3, 3)), "empty-seqs", entry=entry)
+
+
 def test_attention_single_key_closed_form(entry):
     """L = 1: the output is the back-rotated V row (rounded to bf16 twice), bit-exact
     up to the oracle's rounding of the same value."""
