@@ -23,6 +23,15 @@ void set_error(const char *fmt, ...);
         }                                  \
     } while (0)
 
+// A caller-provided workspace smaller than the call needs: RQ_ENOSPACE.
+#define RQ_CHECK_SPACE(cond, ...)          \
+    do {                                   \
+        if (!(cond)) {                     \
+            ::rq::set_error(__VA_ARGS__);  \
+            return RQ_ENOSPACE;            \
+        }                                  \
+    } while (0)
+
 int check_launch(const char *what);
 
 // ---------------------------------------------------------------------------

@@ -1233,7 +1233,7 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
     RQ_CHECK_ARG(((uintptr_t)k_centroids % 16) == 0 && ((uintptr_t)v_centroids % 16) == 0 && ((uintptr_t)rotation % 16) == 0,
                  "centroids and rotation must be 16-byte aligned");
     if (num_seqs == 0) return RQ_OK;
-    RQ_CHECK_ARG(workspace_bytes >= rq_fused_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_seq_len),
+    RQ_CHECK_SPACE(workspace_bytes >= rq_fused_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_seq_len),
                  "workspace too small");
     RQ_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;

@@ -236,7 +236,7 @@ extern "C" int rq_paged_decompress(const uint8_t *kv_cache, int64_t num_blocks, 
     if (lrc) return lrc;
     RQ_CHECK_ARG(out_dtype == RQ_DTYPE_F16 || out_dtype == RQ_DTYPE_BF16 || out_dtype == RQ_DTYPE_F32,
                  "bad out_dtype %d", out_dtype);
-    RQ_CHECK_ARG(workspace_bytes >= rq_paged_decompress_workspace_bytes(num_blocks), "workspace too small");
+    RQ_CHECK_SPACE(workspace_bytes >= rq_paged_decompress_workspace_bytes(num_blocks), "workspace too small");
     RQ_CHECK_ARG(((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
     RQ_CHECK_ARG(stride_token % 4 == 0 && stride_block % 4 == 0 && ((uintptr_t)kv_cache % 4) == 0,
                  "cache must be 4-byte aligned");

@@ -555,9 +555,9 @@ int prefill_call(int kq, int causal, const void *q, int32_t dtype, int64_t total
     RQ_CHECK_ARG(((uintptr_t)rotation % 16) == 0, "rotation must be 16-byte aligned");
     if (num_seqs == 0 || max_q_len == 0 || num_blocks == 0 || max_seq_len == 0) return RQ_OK;
     const int64_t need = rq_int8_prefill_workspace_bytes(num_seqs, num_kv_heads, max_seq_len);
-    RQ_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace % 16) == 0,
-                 "workspace must be 16-byte aligned and hold %lld bytes (got %lld)", (long long)need,
-                 (long long)workspace_bytes);
+    RQ_CHECK_SPACE(workspace_bytes >= need, "workspace too small: the call needs %lld bytes (got %lld)",
+                   (long long)need, (long long)workspace_bytes);
+    RQ_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace % 16) == 0, "workspace must be 16-byte aligned");
     PrefillArgs a{};
     a.q = q;
     a.q_st = q_stride_tok;

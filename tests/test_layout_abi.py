@@ -118,9 +118,15 @@ class TestABI:
                **{k: pre[k] for k in list(pre)[list(pre).index("sl") + 1:]}, "ws": None, "wsb": 0, "stream": None}
         for change, msg in ((dict(d=64), b"head_dim"), (dict(hq=136), b"integer <= 16"), (dict(rb=8), b"rot_block"),
                             (dict(nk=17), b"centroid"), (dict(dtype=2), b"dtype"), (dict(il=1, nv=16), b"dense"),
-                            (dict(il=2), b"index_layout"), (dict(msl=-1), b"bad sizes"), ({}, b"workspace")):
+                            (dict(il=2), b"index_layout"), (dict(msl=-1), b"bad sizes")):
             rc = lib.rq_paged_prefill(*{**pre, **change}.values())
             assert rc == 1 and msg in lib.rq_last_error(), change
+        # a workspace smaller than the call needs: RQ_ENOSPACE (2); a missing one: RQ_EINVAL
+        assert lib.rq_paged_prefill(*pre.values()) == 2 and b"workspace too small" in lib.rq_last_error()
+        assert lib.rq_paged_prefill(*{**pre, "wsb": 1 << 30}.values()) == 1 and b"aligned" in lib.rq_last_error()
+        rc = lib.rq_fused_decode(None, 1, 1, 32, 0, 0, None, 1, 16, 0, 0, 8, 128, 0, None, 1, 1, None, 16, None, 8,
+                                 None, 8, None, 4, 0.1, None, 0, 0, None, 0, None)
+        assert rc == 2 and b"workspace too small" in lib.rq_last_error()
         assert lib.rq_paged_prefill(*{**pre, "msl": 0}.values()) == 0  # nothing to attend: no launch
         assert lib.rq_paged_prefill_workspace_bytes(3, 8, 1000) == lib.rq_int8_prefill_workspace_bytes(3, 8, 1000)
         with pytest.raises(ValueError):
