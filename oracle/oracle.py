@@ -18,9 +18,11 @@ Restates the reference (tpurtell/rotorquant-vllm) on the CPU:
   compress_store ............... rq_backend.py:585-657
   paged_decompress ............. rq_backend.py:737-852
   decode_attention ............. src/rotorquant_vllm/triton/fused_paged_rq_decode.py:252-312
-                                 (math of the kernel :76-206 in fp64)
+                                 (math of the kernel :76-206 in fp64; K and V are
+                                 centroid * norm rounded to the q dtype, :146-147, :190-191)
   prefill_attention ............ src/rotorquant_vllm/triton/fused_paged_rq_int8_prefill.py:296-363
-                                 (math in fp64; causal position offset L - T + i)
+                                 (math in fp64; K and V rounded to the q dtype, :172, :224;
+                                 causal position offset L - T + i)
   unfused_attention ............ src/rotorquant_vllm/vllm/rq_backend.py:937-1036 (the
                                  non-fused path: K/V decompressed to the q dtype,
                                  flash attention's math in fp64, causal or not)
@@ -39,7 +41,8 @@ Pins (what each function is checked against, besides the product):
     keys -> logistic weight of sm_scale * (s1 - s0)); prefill rows equal
     decode over the visible prefix; the q / out roundings against torch's
     own casts.  Mistakes planted through _kv_head, _visible and _scores
-    (GQA map, mask offset, missing scale) fail these checks.
+    (GQA map, mask offset, missing scale) and K/V left unrounded fail these
+    checks.
   dense3_pack: a bit permutation (each of the 3 x 32 input bits of a group lands
     on its own output bit, checked bit by bit) and unpack inverts it, on all
     index values at every position (tests/test_oracle_golden.py).
@@ -371,6 +374,14 @@ def paged_decompress(cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb,
 # Attention references (float64 over the exact dequantized K/V)
 # ---------------------------------------------------------------------------
 
+def _kv_rounding(kv_dtype, dtype):
+    """The dtype K/V are rounded to: "q" (the default of the attention oracles) is the
+    q dtype, as both reference kernels cast centroid * norm to it
+    (fused_paged_rq_decode.py:146-147, :190-191; fused_paged_rq_int8_prefill.py:172,
+    :224); None keeps the fp32 products (no rounding)."""
+    return dtype if kv_dtype == "q" else kv_dtype
+
+
 def gather_seq(cache, block_table_row, L, num_kv_heads, head_dim, k_cb, v_cb, kv_dtype=None):
     """K, V (L, H, D) fp64 dequantized (centroid * norm in fp32) for one sequence;
     with kv_dtype, rounded to that dtype as decompress() writes them (the pages
@@ -442,10 +453,11 @@ def _scores(qr: np.ndarray, K: np.ndarray, sm_scale: float) -> np.ndarray:
 
 
 def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype,
-                         kv_dtype=None):
+                         kv_dtype="q"):
     """Rotated-space decode output in float64, before the output rounding:
-    (B, HQ, D).  q: (B, HQ, D) fp32 values of the dtype-rounded query; kv_dtype as
-    for gather_seq."""
+    (B, HQ, D).  q: (B, HQ, D) fp32 values of the dtype-rounded query; K/V rounded
+    to _kv_rounding(kv_dtype, dtype) (default: the q dtype, as the reference)."""
+    kv_dtype = _kv_rounding(kv_dtype, dtype)
     B, HQ, D = q.shape
     G = HQ // num_kv_heads
     out = np.zeros((B, HQ, D))
@@ -467,7 +479,7 @@ def decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim
 
 
 def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale, dtype,
-                     kv_dtype=None):
+                     kv_dtype="q"):
     """q: (B, HQ, D) fp32 values of the dtype-rounded query.  Returns (B, HQ, D) fp32 values."""
     o_rot = decode_attention_rot(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R, sm_scale,
                                  dtype, kv_dtype)
@@ -476,13 +488,15 @@ def decode_attention(q, cache, block_table, seq_lens, num_kv_heads, head_dim, k_
 
 
 def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
-                          sm_scale, dtype, rows=None, causal=True, kv_dtype=None):
+                          sm_scale, dtype, rows=None, causal=True, kv_dtype="q"):
     """Rotated-space prefill output in float64, before the output rounding: (T, HQ, D).
 
     Query i of sequence b sits at position seq_lens[b] - q_len_b + i; causal: it
     sees the keys at positions <= its own, else all seq_lens[b] keys.  rows
     (optional, sorted global query rows) restricts the work to those rows;
-    the others stay zero.  kv_dtype as for gather_seq."""
+    the others stay zero.  K/V rounded to _kv_rounding(kv_dtype, dtype) (default:
+    the q dtype, as the reference)."""
+    kv_dtype = _kv_rounding(kv_dtype, dtype)
     T, HQ, D = q.shape
     G = HQ // num_kv_heads
     out = np.zeros((T, HQ, D))
@@ -513,7 +527,7 @@ def prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_he
 
 
 def prefill_attention(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb, R,
-                      sm_scale, dtype, rows=None, causal=True, kv_dtype=None):
+                      sm_scale, dtype, rows=None, causal=True, kv_dtype="q"):
     """Attention of new tokens; query i of sequence b sits at position seq_lens[b] - q_len_b + i.
     Returns (T, HQ, D) fp32 values (rows outside `rows`, when given, are zero)."""
     o_rot = prefill_attention_rot(q, cu_seqlens, cache, block_table, seq_lens, num_kv_heads, head_dim, k_cb, v_cb,

@@ -128,24 +128,25 @@ __device__ __forceinline__ float rows_sum(float x) {
 // Direct global -> LDS copies, issued as inline assembly so that the compiler
 // neither waits for them before unrelated LDS accesses nor counts them: the
 // kernel waits for them itself with s_waitcnt vmcnt.  Lane l writes its bytes
-// at LDS address m0 + l * size (m0 = wave-uniform destination).
+// at LDS address m0 + l * size (m0 = wave-uniform destination).  The destination
+// is an operand bound to m0 (the compiler writes m0); the s_nop is the one wait
+// state an SALU write of m0 needs before a load with LDS = 1, which the compiler
+// does not insert for an asm statement.
 //   copy16:  16 bytes from the uniform base `src` + per-lane 32-bit offset.
 //   copy16v: 16 bytes from a per-lane address.
 //   copy4s:  4 bytes from the uniform base `src` + per-lane 32-bit offset.
 //   copy4:   4 bytes from a per-lane address.
 __device__ __forceinline__ void copy16(const uint8_t *src, uint32_t voff, uint32_t dst) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "s"(dst)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(src), "{m0}"(dst) : "memory");
 }
 __device__ __forceinline__ void copy16v(const uint8_t *src, uint32_t dst) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(dst) : "memory");
 }
 __device__ __forceinline__ void copy4s(const uint8_t *src, uint32_t voff, uint32_t dst) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(src), "s"(dst)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(src), "{m0}"(dst) : "memory");
 }
 __device__ __forceinline__ void copy4(const uint8_t *src, uint32_t dst) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(dst) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_copies() {

@@ -1,35 +1,43 @@
 // Fused paged decode attention over the packed RotorQuant cache (gfx950).
 //
 // Replaces fused_paged_rq_decode (src/rotorquant_vllm/triton/fused_paged_rq_decode.py:214-312,
-// kernel :32-206).  Same mathematics -- attention in the rotated space, with
-// q_rot = bf16(q R^T), K/V = centroid[idx] * norm, exp2 online softmax, and
-// out = bf16(bf16(out_rot) R) -- organised for CDNA4 in three launches:
+// kernel :32-206).  Same mathematics -- attention in the rotated space with
+// q_rot = dtype(q R^T) (:271), K = dtype(centroid[idx] * norm) (:146-147) and V
+// likewise (:190-191), exp2 online softmax, out = dtype(dtype(out_rot) R) (:201-206,
+// :308) -- organised for CDNA4 in three launches:
 //
-//   * decode_prep_kernel: per sequence, the fp16 Q^T MFMA operand of every kv
-//     head and one descriptor per 32-token tile (slot offsets from the block
-//     table);
+//   * decode_prep_kernel: per sequence, the Q^T MFMA operand (q_rot in the q dtype)
+//     of every kv head and one descriptor per 32-token tile (slot offsets from the
+//     block table);
 //   * decode_kernel: persistent; the tiles of the whole batch are split into
-//     equal contiguous ranges, one per resident workgroup.  A workgroup holds
-//     one wave per kv head, so each token's K/V bytes are read once and shared
-//     by all GQA query heads.  Tiles are copied global -> LDS two ahead;
-//     Q K^T and P V run on v_mfma_f32_16x16x32_f16 with the GQA group
-//     (<= 16 query heads) as the 16-wide N side; nibble -> fp16 centroid
-//     lookups are register v_perm_b32 table lookups and the K/V norms are
-//     applied to the scores and to P.  Each sequence segment of a range ends
-//     in an (m, l, acc) partial;
-//   * decode_merge_kernel: log-sum-exp over a sequence's partials, rounding
-//     and the rotation back by R.
+//     contiguous ranges, one per resident workgroup.  A workgroup holds one wave
+//     per kv head, so each token's K/V bytes are read once and shared by all GQA
+//     query heads.  Tiles are copied global -> LDS two ahead.  Per tile, each lane
+//     builds half of one token's K and V codebook tables -- the 8 (16) values
+//     dtype(c_j * norm) of that token -- in LDS; the lanes holding the token's
+//     indices look them up with v_perm_b32.  Q K^T runs on the q-dtype MFMA (exact
+//     products, fp32 sums), P V on the fp16 MFMA with V as an fp16 image of its
+//     q-dtype value.  Each sequence segment of a range ends in an (m, l, acc)
+//     partial;
+//   * decode_merge_kernel: log-sum-exp over a sequence's partials, rounding and
+//     the rotation back by R.
 //
 // MFMA operand layout used below (16x16x32, wave64, lane l, g = l / 16):
 //   A (16 x 32): lane holds row l % 16, k = 8g .. 8g+7   (4 dwords of 2 x 16-bit)
 //   B (32 x 16): lane holds col l % 16, k = 8g .. 8g+7
 //   C (16 x 16): lane holds col l % 16, rows 4g .. 4g+3  (4 floats)
 //
-// S^T = K Q^T per 16-token group j (A = K: row = token 16j + l%16, k = head
-// dims; B = Q^T: col = query head).  Lane (g, q) then holds scores of tokens
-// {4g + i} (j = 0) and {16 + 4g + i} (j = 1) for query head q, which is
-// exactly the k-group order used for O^T = V^T P^T (A = V^T: row = a head dim,
-// k = those 8 tokens; B = P^T: col = query head): no cross-lane movement of P.
+// S^T = K Q^T per 16-token group j (A = K: row = token 16j + l%16, k = head dims;
+// B = Q^T: col = query head).  Lane (g, col) then holds the scores of tokens
+// 4g + i (j = 0) and 16 + 4g + i (j = 1) for its query head.
+// O^T = V^T P^T with one row per *pair* of head dims of a nibble dword (row r:
+// dims 8r .. 8r+7, pairs (e0,e2) (e1,e3) (e4,e6) (e5,e7) in four MFMAs): k slots
+// 8g + 2i and 8g + 2i + 1 hold the two dims of the pair for token 16kb + 4g + i,
+// so a lane's V operand is one token's table lookups (no transpose), and the P^T
+// column picks the dim.  With at most 8 query heads per kv head, columns c < 8
+// carry (p, 0) for head c and columns c >= 8 carry (0, p) for head c - 8 (the S^T
+// columns repeat the heads likewise): one MFMA yields both dims of the pair.
+// With more heads (WIDE), two MFMAs per pair, (p, 0) and (0, p).
 #include <algorithm>
 #include <mutex>
 
@@ -58,36 +66,18 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                       0, 0, 0);
 }
 
-// Centroids (fp32, 16-byte aligned, n = 8 or 16): uniform vector loads issued
-// together (entries past n read as zero).
-struct Centroids {
-    float4 v4[4];
-};
-__device__ __forceinline__ Centroids load_centroids(const float *c, int n) {
-    const float4 *c4 = reinterpret_cast<const float4 *>(c);
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    return Centroids{{c4[0], c4[1], n > 8 ? c4[2] : z, n > 8 ? c4[3] : z}};
-}
-
-// Centroids -> 16-bit table split in low / high bytes.
+// Two fp32 values rounded to the 16-bit dtype, packed a | b << 16 (one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
 template <int DT>
-__device__ __forceinline__ Table16 make_table(const Centroids &cv) {
-    const float4 *v4 = cv.v4;
-    Table16 t;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const float e[4] = {v4[w].x, v4[w].y, v4[w].z, v4[w].w};
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t bits = Elem<DT>::from_f32(e[i]);
-            lo |= (bits & 0xffu) << (8 * i);
-            hi |= (bits >> 8) << (8 * i);
-        }
-        t.lo[w] = lo;
-        t.hi[w] = hi;
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) float f32x2;
+    if constexpr (DT == RQ_DTYPE_BF16) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    } else {
+        typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
     }
-    return t;
 }
 
 // One packed dword (8 nibbles, coordinates e0..e7 of one token) -> MFMA
@@ -102,13 +92,60 @@ __device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
     return decode_row8_sel<BITS>(t, (x >> 4) & 0x0f0f0f0fu, x & 0x0f0f0f0fu);  // e0 e2 e4 e6 | e1 e3 e5 e7
 }
 
-typedef __attribute__((ext_vector_type(2))) int i32x2;
-// ds_read_b64_tr_b8 (gfx950): per 16 lanes, lanes 2i and 2i + 1 name the two 8-byte
-// halves of row i of an 8 x 16 byte block, and lane c receives byte c of rows 0..7
-// (row i in byte i).  p: an LDS address, 8-byte aligned.
-__device__ __forceinline__ i32x2 ds_read_tr8(const uint8_t *p) {
-    typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2 *)(p));
+// ---------------------------------------------------------------------------
+// Per-token codebook tables in LDS.  A table holds the 16-bit values of a
+// token's 2^BITS codebook entries as low-byte / high-byte dwords (Table16):
+//   8 entries  (16 bytes): lo0 hi0 lo1 hi1          (lo0: low bytes of entries 0-3)
+//   16 entries (32 bytes): lo0 hi0 lo1 hi1 lo2 hi2 lo3 hi3
+// Half hh (entries [NE/2 hh, NE/2 (hh + 1))) is written by one lane: 8 bytes at
+// 8 hh, or 16 bytes at 16 hh.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint2 planes4(uint32_t p01, uint32_t p23) {  // 4 values as pairs -> (lo, hi) dwords
+    return make_uint2(perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u));
+}
+
+// Half hh of the table of dtype(c_j * m) for the codebook cb (16 floats in LDS,
+// zero-padded), written at dst.  F16_IMAGE: the values are then stored as fp16
+// (for a bf16 dtype: the bf16 value converted to fp16, exact while it is at least
+// 2^-17 and below 65504).  The product is rounded to fp32 before the 16-bit
+// rounding, as the reference's fp32 multiply followed by .to(dtype).
+template <int DT, int BITS, bool F16_IMAGE>
+__device__ __forceinline__ void table_half(const float *cb, float m, int hh, uint8_t *dst) {
+    constexpr int NH = (1 << BITS) / 2;  // entries per half
+    const float4 *c4 = reinterpret_cast<const float4 *>(cb + NH * hh);
+    uint32_t pr[NH / 2];
+#pragma unroll
+    for (int q = 0; q < NH / 4; ++q) {
+        const float4 c = c4[q];
+        const float e[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t v = pack2<DT>(opaque(e[2 * j] * m), opaque(e[2 * j + 1] * m));
+            if constexpr (F16_IMAGE && DT == RQ_DTYPE_BF16)
+                v = pack2<RQ_DTYPE_F16>(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u));
+            pr[2 * q + j] = v;
+        }
+    }
+    if constexpr (NH == 4) {
+        *reinterpret_cast<uint2 *>(dst + 8 * hh) = planes4(pr[0], pr[1]);
+    } else {
+        const uint2 x = planes4(pr[0], pr[1]), y = planes4(pr[2], pr[3]);
+        *reinterpret_cast<u32x4 *>(dst + 16 * hh) = u32x4{x.x, x.y, y.x, y.y};
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ Table16 read_table(const uint8_t *p) {
+    Table16 t;
+    const u32x4 r = *reinterpret_cast<const u32x4 *>(p);
+    t.lo[0] = r.x, t.hi[0] = r.y, t.lo[1] = r.z, t.hi[1] = r.w;
+    if constexpr (BITS == 4) {
+        const u32x4 s = *reinterpret_cast<const u32x4 *>(p + 16);
+        t.lo[2] = s.x, t.hi[2] = s.y, t.lo[3] = s.z, t.hi[3] = s.w;
+    } else {
+        t.lo[2] = t.lo[3] = t.hi[2] = t.hi[3] = 0u;
+    }
+    return t;
 }
 
 // Value of lane (l & ~3) + perm[l & 3] of the lane's quad (DPP quad_perm, ctrl =
@@ -150,26 +187,12 @@ struct DecodeArgs {
     int *tile_prefix;   // [seq][2]: first workgroup whose range covers the sequence, number of such workgroups
     int *n_tiles_total;
     uint64_t *split_m;  // M of the range split (prep kernel)
-    uint32_t *qops;     // [seq][H][16 cols][4 g][4 chunks][4 dwords]: fp16 query operands (cols < G written)
-    float *qscale;      // [seq][H][16] score scales
+    uint32_t *qops;     // [seq][H][16 cols][4 g][4 chunks][4 dwords]: q-dtype query operands (cols < G written)
     float *part_acc;    // [slot][HQ][D], slot = workgroup + seq
     float *part_ml;     // [slot][HQ][2]
     void *out;
     int64_t o_ss, o_sh;
 };
-
-template <int DT>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    if constexpr (DT == RQ_DTYPE_BF16) {
-        typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-        bf16x2 v = {(__bf16)a, (__bf16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    } else {
-        typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
-        f16x2 v = {(_Float16)a, (_Float16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-}
 
 // The lane index, recomputed where it is used (two VALU ops, no input register).
 // Lane-derived values needed only at segment boundaries or by the copy issue are
@@ -189,14 +212,12 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
 }
 
 // q_rot = q R^T of the G query heads of (seq, kv head h), rounded to the query
-// dtype, as the fp16 Q^T MFMA operand: lane (g, col) holds for dim chunk c the
-// dims 32g + 8c + {0,2,4,6,1,3,5,7} of query head col (zero for col >= G).  The
-// rounded q_rot is scaled by 2^qexp (exact) so its largest element sits in
-// [2^14, 2^15); sc = score_scale * 2^-qexp undoes it on the scores.
+// dtype (fused_paged_rq_decode.py:271), as the Q^T MFMA operand in that dtype:
+// lane (g, col) holds for dim chunk c the dims 32g + 8c + {0,2,4,6,1,3,5,7} of
+// query head col (zero for col >= G).
 // wq: this wave's LDS scratch of G * 128 16-bit values.
 template <int DT>
-__device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, int h, uint16_t *wq, u32x4 (&qop)[4],
-                                              float &sc) {
+__device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, int h, uint16_t *wq, u32x4 (&qop)[4]) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, col = lane & 15;
     {
@@ -244,32 +265,13 @@ __device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, 
         }
     }
     __builtin_amdgcn_wave_barrier();
-    float qv[4][8];
-    float qmax = 0.f;
     #pragma unroll
     for (int c = 0; c < 4; ++c) {
+        // w: dims 8c' .. 8c'+7 (c' = 4g + c) as 16-bit pairs (d0 d1) (d2 d3) (d4 d5) (d6 d7)
         const uint4 w = col < a.G ? *reinterpret_cast<const uint4 *>(wq + col * kD + 32 * g + 8 * c)
                                   : make_uint4(0, 0, 0, 0);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            qv[c][2 * i] = Elem<DT>::to_f32(ws[i] & 0xffffu);
-            qv[c][2 * i + 1] = Elem<DT>::to_f32(ws[i] >> 16);
-            qmax = fmaxf(qmax, fmaxf(fabsf(qv[c][2 * i]), fabsf(qv[c][2 * i + 1])));
-        }
-    }
-    qmax = rows_max(qmax);
-    const int qexp = qmax > 0.f ? 141 - (int)((__float_as_uint(qmax) >> 23) & 0xffu) : 0;  // 14 - floor(log2 qmax)
-    sc = a.score_scale * ldexpf(1.f, -qexp);
-    #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        float e[8];
-    #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = ldexpf(qv[c][i], qexp);
-        qop[c].x = pack2<RQ_DTYPE_F16>(e[0], e[2]);
-        qop[c].y = pack2<RQ_DTYPE_F16>(e[4], e[6]);
-        qop[c].z = pack2<RQ_DTYPE_F16>(e[1], e[3]);
-        qop[c].w = pack2<RQ_DTYPE_F16>(e[5], e[7]);
+        qop[c] = u32x4{perm(w.y, w.x, 0x05040100u), perm(w.w, w.z, 0x05040100u),   // (d0 d2) (d4 d6)
+                       perm(w.y, w.x, 0x07060302u), perm(w.w, w.z, 0x07060302u)};  // (d1 d3) (d5 d7)
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -337,9 +339,9 @@ __device__ __forceinline__ int seq_tiles(const DecodeArgs &a, int64_t b) {
 }
 
 // Per-call preparation; workgroup (seq, y):
-//   * y == 0: the fp16 query operands (and score scales) of every kv head of the
-//     sequence, stored per query-head column (256 bytes each, in the order the
-//     decode lanes (g, col) read them) so one copy moves a kv head's G columns;
+//   * y == 0: the query operands of every kv head of the sequence, stored per
+//     query-head column (256 bytes each, in the order the decode lanes (g, col)
+//     read them) so one copy moves a kv head's G columns;
 //   * y >= 1: the tile descriptors of the sequence's tokens, four per thread and
 //     step, placed after the tiles of the sequences before it (the tiles of all
 //     sequences, in order, form the work the decode kernel splits by range);
@@ -360,15 +362,13 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     if (y == 0) {
         for (int h = wave; h < a.H; h += nw) {
             u32x4 qop[4];
-            float sc;
-            query_operand<DT>(a, seq, h, reinterpret_cast<uint16_t *>(prep_lds) + wave * 16 * kD, qop, sc);
+            query_operand<DT>(a, seq, h, reinterpret_cast<uint16_t *>(prep_lds) + wave * 16 * kD, qop);
             const int g = lane >> 4, col = lane & 15;
             uint4 *dst = reinterpret_cast<uint4 *>(a.qops + ((seq * a.H + h) * 16 + col) * 64 + g * 16);
             if (col < a.G) {
     #pragma unroll
                 for (int c = 0; c < 4; ++c) dst[c] = make_uint4(qop[c].x, qop[c].y, qop[c].z, qop[c].w);
             }
-            if (lane < 16) a.qscale[(seq * a.H + h) * 16 + lane] = sc;
         }
     }
     // tiles before this sequence (prefix) and in all sequences (NT)
@@ -452,9 +452,9 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
     }
 }
 
-// Decode.  The tiles of all sequences, in order, are split into gridDim.x equal
-// contiguous ranges; workgroup w (with blockIdx.z selecting a group of hpw kv
-// heads, one wave per head) takes range w, so every workgroup gets the same work
+// Decode.  The tiles of all sequences, in order, are split into contiguous ranges
+// (see RangeSplit); workgroup w (with blockIdx.z selecting a group of hpw kv heads,
+// one wave per head) takes range w, so every workgroup gets about the same work
 // whatever the sequence lengths.  A range covers one or more sequence segments;
 // each segment ends in a partial (m, l, acc) at slot w + seq, which is unique
 // because ranges are contiguous and ordered.
@@ -462,16 +462,19 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
 // Data movement: tile descriptors are copied into an LDS ring four tiles ahead
 // and each tile's K/V index runs and norms two tiles ahead, into two stages:
 //   stage layout: token t at t * tok_stride: [K idx of the hpw heads | V idx]
-//                 then norm rows (2*hpw x 32 fp32): K norms of each head, V norms.
+//                 then the norms (2 * hpw x 32 fp32).
 // One copy instruction moves a whole token's K+V index run (8*hpw x 16 B), so
 // every request covers whole cache lines.  Iteration t: wait for tile t (tile
-// t+1 stays in flight), barrier, read this wave's operands into registers,
-// barrier, copy descriptor t+4 and tile t+2, compute tile t from registers.
+// t+1 stays in flight), barrier, read this wave's index bytes and norms, build
+// the codebook tables into the wave's own K index bytes (read already), read the
+// tables and look the V operands up, barrier, copy descriptor t+4 and tile t+2,
+// compute tile t from registers.
 // Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
 constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
 
 // D3: the cache holds the dense 3-bit index layout (48 index bytes per head).
-template <int DT, int KB, int VB, int HPW, bool D3>
+// WIDE: more than 8 query heads per kv head.
+template <int DT, int KB, int VB, int HPW, bool D3, bool WIDE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(KB, VB, HPW)))) void decode_kernel(DecodeArgs a) {
     const int w = blockIdx.x;
     const int NT = *a.n_tiles_total;
@@ -487,24 +490,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int g = lane >> 4;    // k-group / row-group
     const int col = lane & 15;  // MFMA column (query head inside the GQA group) / row
     const int h0 = blockIdx.z * hpw;
-    const int h = h0 + wave;
     const SlotLayout SL(a.H, kD, D3);
-    constexpr int IB = D3 ? 48 : 64;  // index bytes per head
-    constexpr bool kTrV = !D3 && HPW > 0;  // V index bytes by transposing LDS reads
+    constexpr int IB = D3 ? 48 : 64;   // index bytes per head
+    constexpr int TV = D3 ? 16 : 32;   // V table offset in a token's K index bytes (K table at 0)
+    constexpr bool kScaleV = DT == RQ_DTYPE_BF16;  // V fp16 image carries 2^-e_run (bf16 range)
     const int TS = HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride;
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
-    const int tl = lane & 31;  // token of this lane in a tile (slot base, norm copy)
+    const int tl = lane & 31;  // token of this lane's codebook tables (and slot base, norm copy)
+    const int hh = lane >> 5;  // the half of those tables this lane builds
 
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *const stage0 = lds;
     uint8_t *const stage1 = lds + stage_bytes;
     const TileDesc *const ring = reinterpret_cast<const TileDesc *>(lds + 2 * stage_bytes);
-    // Query operand slot: per wave, its kv head's G columns (256 bytes each), then
-    // the score scales of the hpw kv heads (16 floats each).
+    // Query operand slot: per wave, its kv head's G columns (256 bytes each); then
+    // the K and V codebooks (16 floats each, zero-padded).
     const int G = a.G;
     uint8_t *const qarea = lds + 2 * stage_bytes + kRing * sizeof(TileDesc);
-    const float *const scarea = reinterpret_cast<const float *>(qarea + hpw * G * 256);
+    float *const cbarea = reinterpret_cast<float *>(qarea + hpw * G * 256);
 
     // Descriptor of local tile i -> ring slot i % kRing (wave 0, one copy).
     auto issue_desc = [&](int i) {
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * lane, lds_addr(reinterpret_cast<const uint8_t *>(ring + i % kRing)));
     };
     // Copies of local tile i into stage sb.  Per wave and full tile: kTile / hpw
-    // token copies and one norm copy.
+    // token copies and, on waves < hpw / 4, one norm copy.
     auto issue = [&](int i, const uint8_t *sb) {
         const TileDesc &d = ring[i % kRing];
         const int valid = __builtin_amdgcn_readfirstlane(d.valid);
@@ -526,20 +530,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             if (lane < 2 * PH * hpw) copy16(tok, kv_src, dst + tt * TS);
         }
         if constexpr (HPW > 0) {
-            // Norms in 16-byte pieces: a token's K norms and V norms of the hpw heads
-            // are NP pieces; one copy covers TPI tokens (waves 0 .. kTile/TPI - 1).
-            // Lane l takes token slot q' = l / NP, piece l % NP, where slot q' holds
-            // token 4 (q' % (TPI/4)) + q' / (TPI/4) of the copy's token range: the
-            // norms of tokens 4g + i (fixed i) then land 16 NP g bytes apart (distinct
-            // banks) and tokens i, i+1, ... 256 bytes apart.
-            constexpr int NP = HPW / 2, TPI = 64 / NP;
-            if (wave < kTile / TPI) {
+            // Norms in 16-byte pieces (4 heads' K or V norms of one token): piece p =
+            // kind * NPH + sub (kind 0: K, 1: V; sub: heads 4 sub .. 4 sub + 3) of token t
+            // lands at slot 32 p + t.  Copy c (wave c) moves pieces 2c and 2c + 1 of all
+            // tokens: lane l takes token l & 31, piece 2c + (l >> 5).
+            constexpr int NPH = HPW / 4;
+            if (wave < NPH) {
                 const uint32_t l = lane_now();  // lane-derived values rebuilt here, not kept live
-                const int qs = l / NP, p = l % NP;
-                const int tt = wave * TPI + 4 * (qs % (TPI / 4)) + qs / (TPI / 4);
-                const uint32_t src = p < NP / 2 ? (uint32_t)(SL.k_norm + 4 * h0 + 16 * p)
-                                                : (uint32_t)(SL.v_norm + 4 * h0 + 16 * (p - NP / 2));
-                if (tt < valid) copy16v(a.cache + d.off[tt] + src, dst + norm_off + 1024 * wave);
+                const int t = l & 31, p = 2 * wave + (int)(l >> 5);
+                const int kind = p / NPH, sub = p % NPH;
+                const uint32_t src = (kind ? (uint32_t)SL.v_norm : (uint32_t)SL.k_norm) + 4 * h0 + 16 * sub;
+                if (t < valid) copy16v(a.cache + d.off[t] + src, dst + norm_off + 1024 * wave);
             }
         } else {
             // norm rows 2*wave, 2*wave+1 (row j < hpw: K norm of head h0+j, else V norm of head h0+j-hpw)
@@ -549,30 +550,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
         }
     };
+    // This wave's K (kind 0) or V (kind 1) norm of token t in stage sb.
+    auto norm_at = [&](const uint8_t *sb, int kind, int t) {
+        if constexpr (HPW > 0) {
+            constexpr int NPH = HPW / 4;
+            return *reinterpret_cast<const float *>(sb + norm_off + 16 * ((kind * NPH + (wave >> 2)) * 32 + t) +
+                                                    4 * (wave & 3));
+        } else {
+            return *reinterpret_cast<const float *>(sb + norm_off + 128 * (kind * hpw + wave) + 4 * t);
+        }
+    };
 
-    // Query operand and score scales of sequence s -> the query slot (each wave its
-    // own kv head): ceil(G / 4) 16-byte copies and one 4-byte copy per wave.
+    // Query operand of sequence s -> the query slot (each wave its own kv head):
+    // ceil(G / 4) 16-byte copies per wave.
     auto issue_q = [&](int s) {
-        const uint8_t *src = reinterpret_cast<const uint8_t *>(a.qops) + ((int64_t)s * a.H + h) * 16 * 256;
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(a.qops) + ((int64_t)s * a.H + h0 + wave) * 16 * 256;
         const uint32_t dst = lds_addr(qarea + wave * G * 256);
         const uint32_t l16 = 16u * lane_now();
         for (int j = 0; j < G * 256; j += 1024)
             if (j + l16 < (uint32_t)(G * 256)) copy16(src, j + l16, dst + j);
-        if (l16 < 256)
-            copy4s(reinterpret_cast<const uint8_t *>(a.qscale + ((int64_t)s * a.H + h) * 16), l16 >> 2,
-                   lds_addr(reinterpret_cast<const uint8_t *>(scarea + wave * 16)));
     };
 
-    // The centroid loads are compiler-visible: issued before the descriptor copies
+    // The codebook loads are compiler-visible: issued before the descriptor copies
     // and covered by their wait, so no wait of the compiler's for them lands after
     // the first tile copies (it would wait for those too).
-    const Centroids ck = load_centroids(a.kc, a.nkc), cv = load_centroids(a.vc, a.nvc);
+    float cbv = 0.f;
+    if (threadIdx.x < 32) {
+        const int e = threadIdx.x & 15;
+        cbv = threadIdx.x < 16 ? (e < a.nkc ? a.kc[e] : 0.f) : (e < a.nvc ? a.vc[e] : 0.f);
+    }
     for (int i = 0; i < min(nt, kRing); ++i) issue_desc(i);
     wait_copies<0>();
+    if (threadIdx.x < 32) cbarea[threadIdx.x] = cbv;
     __syncthreads();
-
-    const Table16 tk = make_table<RQ_DTYPE_F16>(ck);
-    const Table16 tv = make_table<RQ_DTYPE_F16>(cv);
 
     // Per-segment state.  No compiler-visible global load is issued inside the tile
     // loop: the compiler does not count the copies, so a wait it inserted for a load
@@ -580,62 +590,57 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     // query operand therefore arrives by copy, in the same stream as the tiles.
     int seq = -1;
     u32x4 qop[4];
-    float sc;
-    f32x4 acc[8];
+    constexpr int NACC = WIDE ? 8 : 4;
+    f32x4 acc[NACC];  // [rb] (dims (first | second) of pair rb), WIDE: [rb] first dims, [4 + rb] second dims
     float m_run, l_run;
-    int e_run;      // every V norm of the segment so far is < 2^e_run
+    int e_run;      // bf16: every V norm of the segment so far is < 2^e_run; acc carries 2^-e_run
     float lim;      // 2^e_run
+    const float sc = a.score_scale;
     auto begin_segment = [&]() {
         const uint32_t ln = lane_now(), lc = ln & 15;  // rebuilt here, not kept live across the loop
-        const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + lc * 256 + (ln >> 4) * 64);
+        const uint32_t qc = WIDE ? lc : (lc & 7);      // query head of this lane's column
+        const uint4 *src = reinterpret_cast<const uint4 *>(qarea + wave * G * 256 + qc * 256 + (ln >> 4) * 64);
     #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const uint4 v = (int)lc < G ? src[c] : make_uint4(0, 0, 0, 0);
+            const uint4 v = (int)qc < G ? src[c] : make_uint4(0, 0, 0, 0);
             qop[c] = u32x4{v.x, v.y, v.z, v.w};
         }
-        sc = (int)lc < G ? scarea[wave * 16 + lc] : 1.f;  // columns >= G: zero queries, any positive scale
     #pragma unroll
-        for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        m_run = -INFINITY;  // running max (log2 domain) for query head `col`
-        l_run = 0.f;        // this lane's partial sum of p' = p * 2^-e_run
-        // P operand = p' * v_norm = p * v_norm * 2^-e_run <= 2^8 (fp16).  acc and l_run
-        // carry the factor 2^-e_run, so the partial is (m_run + e_run, l_run, acc).
-        // Starting at 2^-64 keeps p' <= 2^72 and l_run finite for tiny norms.
-        e_run = -64;
-        lim = 0x1p-64f;
+        for (int m = 0; m < NACC; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m_run = -INFINITY;  // running max (log2 domain) for this lane's query head
+        l_run = 0.f;        // this lane's partial sum of p
+        // bf16: the V operand is V * 2^-e_run <= max|c| (fp16); starting at 2^-64 keeps
+        // tiny norms representable until the first tile raises it.
+        e_run = kScaleV ? -64 : 0;
+        lim = kScaleV ? 0x1p-64f : INFINITY;
     };
-    // Partial of the current segment -> slot w + seq.  Addresses are a uniform
-    // 64-bit base plus a 32-bit lane offset computed here (a hoisted 64-bit per-lane
-    // address would be spilled, and its reload would wait for the copies in flight).
+    // Partial of the current segment -> slot w + seq: (m_run + e_run, l_run 2^-e_run, acc),
+    // acc in head-dim order.  Addresses are a uniform 64-bit base plus a 32-bit lane
+    // offset computed here (a hoisted 64-bit per-lane address would be spilled, and its
+    // reload would wait for the copies in flight).
     auto end_segment = [&]() {
         const float lsum = rows_sum(l_run);
-        if (col < a.G) {
-            const int64_t slot = (int64_t)(w + seq) * a.HQ + h * a.G;  // uniform: query head h*G of the slot
+        const uint32_t ln = lane_now(), lc = ln & 15, lg = ln >> 4;
+        const uint32_t qc = WIDE ? lc : (lc & 7);
+        if ((int)qc < a.G) {
+            const int64_t slot = (int64_t)(w + seq) * a.HQ + (h0 + wave) * a.G;  // uniform: query head h*G of the slot
             uint8_t *pa = reinterpret_cast<uint8_t *>(a.part_acc + slot * kD);
             uint8_t *pm = reinterpret_cast<uint8_t *>(a.part_ml + slot * 2);
-            const uint32_t ln = lane_now();
-            if constexpr (!kTrV) {
-                // acc[m][i] = O[col][8 * (4g + i) + m] relative to 2^(m_run + e_run)
-                const uint32_t lo_off = ((ln & 15) * kD + 32 * (ln >> 4)) * 4;
+            const uint32_t hoff = qc * kD * 4;
     #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float4 lo = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
-                    float4 hi = make_float4(acc[4][i], acc[5][i], acc[6][i], acc[7][i]);
-                    float4 *dst = reinterpret_cast<float4 *>(pa + lo_off + 32 * i);
-                    dst[0] = lo;
-                    dst[1] = hi;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t r8 = 8 * (4 * lg + i);  // nibble dword 4g + i: dims 8r .. 8r+7
+                if constexpr (WIDE) {
+                    *reinterpret_cast<float4 *>(pa + hoff + 4 * r8) = make_float4(acc[0][i], acc[1][i], acc[4][i], acc[5][i]);
+                    *reinterpret_cast<float4 *>(pa + hoff + 4 * (r8 + 4)) = make_float4(acc[2][i], acc[3][i], acc[6][i], acc[7][i]);
+                } else {
+                    const uint32_t d0 = r8 + (lc >= 8 ? 2 : 0);  // columns >= 8: the second dims of the pairs
+                    *reinterpret_cast<float2 *>(pa + hoff + 4 * d0) = make_float2(acc[0][i], acc[1][i]);
+                    *reinterpret_cast<float2 *>(pa + hoff + 4 * (d0 + 4)) = make_float2(acc[2][i], acc[3][i]);
                 }
-            } else {
-                // acc[2r + e][i] = O[col][32r + 8g + 2i + e] relative to 2^(m_run + e_run)
-                const uint32_t lo_off = ((ln & 15) * kD + 8 * (ln >> 4)) * 4;
-    #pragma unroll
-                for (int i = 0; i < 4; ++i)
-    #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        *reinterpret_cast<float2 *>(pa + lo_off + 4 * (32 * r + 2 * i)) =
-                            make_float2(acc[2 * r][i], acc[2 * r + 1][i]);
             }
-            if (g == 0) *reinterpret_cast<float2 *>(pm + 8u * (lane_now() & 15)) = make_float2(m_run + (float)e_run, lsum);
+            if (lg == 0 && (WIDE || lc < 8))
+                *reinterpret_cast<float2 *>(pm + 8u * qc) = make_float2(m_run + (float)e_run, ldexpf(lsum, -e_run));
         }
     };
     // The query slot holds the operand of the segment starting at local tile q_upto;
@@ -648,17 +653,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     if (nt > 1) issue(1, stage1);
 
     for (int t = 0; t < nt; ++t) {
-        const uint8_t *const sb = (t & 1) ? stage1 : stage0;
+        uint8_t *const sb = (t & 1) ? stage1 : stage0;
         // Tile t landed?  Issued after its copies, and allowed to stay in flight:
         // this wave's copies of tile t+1 (iteration t-1) and descriptor t+3 (wave 0,
         // iteration t-1; the prologue issues descriptors 0..3 before tile 0).  The
         // query operand copies of an iteration precede both.
         if (HPW > 0 && t + 1 < nt) {
-            constexpr int HP = HPW > 0 ? HPW : 8, TPI = 128 / HP;
+            constexpr int HP = HPW > 0 ? HPW : 8, NPH = HP / 4;
             const int v1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid);
-            // token copies tt = wave, wave + HPW, ... < v1; a norm copy on the waves
-            // whose token range [wave * TPI, +TPI) starts below v1
-            const int n = (v1 > wave ? (v1 - wave + HP - 1) / HP : 0) + (wave < kTile / TPI && wave * TPI < v1 ? 1 : 0) +
+            // token copies tt = wave, wave + HPW, ... < v1; a norm copy on the waves < NPH
+            const int n = (v1 > wave ? (v1 - wave + HP - 1) / HP : 0) + (wave < NPH ? 1 : 0) +
                           (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
             wait_copies_n<kTile / HP + 2>(n);
         } else {
@@ -674,21 +678,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             begin_segment();
         }
         // ---- this wave's operands of the tile ------------------------------------
-        // token col, K dims 32g .. 32g+31 (16 nibble bytes, or the 12-byte dense group g)
+        // K: token col (and 16 + col), dims 32g .. 32g+31 (16 nibble bytes, or the
+        // 12-byte dense group g)
         const uint8_t *kb = sb + col * TS + IB * wave + (D3 ? 12 : 16) * g;
-        // V index bytes of the lane's 8 tokens 4g + k, 16 + 4g + k (k < 4), transposed:
-        // Ga[r] = byte j of tokens 4g .. 4g+3 (byte k = token 4g + k), Gb[r] = byte j of
-        // tokens 16+4g .. 16+4g+3.
-        //   nibbles, 8 or 4 heads per workgroup: j = 16r + col (dims 32r + 2 col, +1) by
-        //     ds_read_b64_tr_b8, which transposes, per 16 lanes, an 8 x 16 byte block:
-        //     lanes 2i and 2i + 1 give the two 8-byte halves of row i (token i of the lane
-        //     group), and lane c gets byte c of every row;
-        //   otherwise j = r of the nibble dword col (dims 8 col + 2r, +1), or dense: of
-        //     dword min(col % 4, 2) of group col / 4 (position 3 is assembled from the
-        //     quad's other three lanes), read per token and byte-transposed in registers
-        //     (the generic-head variant has no VGPRs to spare for the other form).
-        uint32_t vw[8], Ga[4], Gb[4];
-        const uint8_t *nb = sb + norm_off + 128 * wave + 16 * g;               // K norms of tokens 4g..4g+3
         uint4 kw0, kw1;
         if constexpr (D3) {
             const uint32_t *k0p = reinterpret_cast<const uint32_t *>(kb);
@@ -699,42 +691,92 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             kw0 = *reinterpret_cast<const uint4 *>(kb);
             kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
         }
-        if constexpr (!kTrV) {
+        // V: nibble dword col (dims 8 col .. 8 col + 7) of the lane's 8 tokens 4g + i and
+        // 16 + 4g + i, or dense: dword min(col % 4, 2) of group col / 4 (position 3 is
+        // assembled from the quad's other lanes below)
+        uint32_t vw[8];
+        {
             const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave +
                                 (D3 ? 12 * (col >> 2) + 4 * min(col & 3, 2) : 4 * col);
     #pragma unroll
             for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
-        } else {
-            const int row = col >> 1;  // token 4g + row (row < 4) or 12 + 4g + row
-            const uint8_t *vr = sb + (row < 4 ? 4 * g + row : 12 + 4 * g + row) * TS + IB * hpw + IB * wave + 8 * (col & 1);
+        }
+        // the K and V norms of token tl (this lane's tables)
+        float nk = norm_at(sb, 0, tl), nv = norm_at(sb, 1, tl);
+
+        // ---- tokens past the end were not copied: their stage bytes are stale.  Zero
+        // their norms (their tables are then zero) and V index dwords (a stale nibble
+        // >= 8 would look up a non-zero byte pattern, and NaN * 0 would reach the
+        // accumulator); their scores are masked below.
+        if (valid < kTile) {
+            // (each masking block takes `valid` through an empty asm, so that its
+            // compares stay inside the block instead of running for every full tile)
+            const int vv = opaque_s(valid);
+            const uint32_t ln = lane_now();
+            const int g4 = 4 * (int)(ln >> 4);  // 4g, rebuilt here (not kept live)
+            const int t32 = (int)(ln & 31);
+            nk = t32 < vv ? nk : 0.f;
+            nv = t32 < vv ? nv : 0.f;
     #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const i32x2 t = ds_read_tr8(vr + 16 * r);
-                Ga[r] = (uint32_t)t.x;
-                Gb[r] = (uint32_t)t.y;
+            for (int i = 0; i < 8; ++i) {
+                const int tt = i < 4 ? g4 + i : 12 + g4 + i;
+                vw[i] = tt < vv ? vw[i] : 0u;
             }
         }
-        float4 nk0, nk1, nv0, nv1;
-        if constexpr (HPW > 0) {
-            // token 4g + i at 256 i + 16 NP q (+1024 for tokens 16.. when TPI = 16),
-            // q = g (tokens < 16) or 4 + g (tokens >= 16 when TPI = 32)
-            constexpr int NP = HPW / 2, TPI = 64 / NP;
-            const float *n0 = reinterpret_cast<const float *>(sb + norm_off + 16 * NP * g + 16 * (wave / 4) + 4 * (wave % 4));
-            const int hi = TPI == 16 ? 1024 : 16 * NP * 4;  // tokens 16..31
-            const int vo = 16 * (NP / 2);                     // V norms after the K pieces
-            auto ld4 = [&](int o) {
-                const float *p = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(n0) + o);
-                return make_float4(p[0], p[64], p[128], p[192]);
-            };
-            nk0 = ld4(0);
-            nk1 = ld4(hi);
-            nv0 = ld4(vo);
-            nv1 = ld4(vo + hi);
-        } else {
-            nk0 = *reinterpret_cast<const float4 *>(nb);
-            nk1 = *reinterpret_cast<const float4 *>(nb + 64);
-            nv0 = *reinterpret_cast<const float4 *>(nb + 128 * hpw);
-            nv1 = *reinterpret_cast<const float4 *>(nb + 128 * hpw + 64);
+        // bf16: a V norm at or above 2^e_run (rare after the first tile): raise e_run to
+        // the tile's largest norm and rescale acc, which carries 2^-e_run.
+        if constexpr (kScaleV) {
+            if (__any(nv >= lim)) {
+                float nvm = rows_max(nv);
+    #pragma unroll
+                for (int o = 1; o < 16; o <<= 1) nvm = fmaxf(nvm, __shfl_xor(nvm, o));
+                const int e_tile = (int)((__float_as_uint(nvm) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
+                if (e_tile > e_run) {
+                    const float f = ldexpf(1.f, e_run - e_tile);
+    #pragma unroll
+                    for (int m = 0; m < NACC; ++m) acc[m] *= f;
+                    e_run = e_tile;
+                    lim = ldexpf(1.f, e_run);
+                }
+            }
+        }
+        // ---- codebook tables of token tl: this lane's half of the K table (q dtype) and
+        // of the V table (fp16 image), written over the wave's own K index bytes of the
+        // token, which were read above (LDS instructions of a wave complete in order)
+        {
+            uint8_t *tab = sb + tl * TS + IB * wave;
+            table_half<DT, KB, false>(cbarea, nk, hh, tab);
+            table_half<DT, VB, true>(cbarea + 16, kScaleV ? ldexpf(nv, -e_run) : nv, hh, tab + TV);
+        }
+        __builtin_amdgcn_wave_barrier();
+        const Table16 tk0 = read_table<KB>(sb + col * TS + IB * wave);
+        const Table16 tk1 = read_table<KB>(sb + (16 + col) * TS + IB * wave);
+        // ---- V operands: token i's dims of the lane's nibble dword, by pair:
+        //   av[i] = (e0 e2) (e1 e3) (e4 e6) (e5 e7)
+        // Index selectors (one index per byte) of the even and the odd dims.  Dense:
+        // lanes of positions 0..2 mask their own bytes; the position-3 lane takes the
+        // top bits of its quad's A, B and C lanes (same token): one form for all lanes,
+        // (x >> s1) & m1 | (y >> s2) & m2, with per-lane shifts and masks.
+        auto sel = [&](uint32_t x, uint32_t &ev, uint32_t &od) {
+            if constexpr (D3) {
+                const bool p3 = (col & 3) == 3;
+                const uint32_t xe = quad_pick<0x24>(x), xo = quad_pick<0x64>(x), y = quad_pick<0xa4>(x);
+                const uint32_t m1 = p3 ? 0x03030303u : 0x07070707u, m2 = p3 ? 0x04040404u : 0u;
+                ev = ((xe >> (p3 ? 6 : 0)) & m1) | ((y >> 4) & m2);
+                od = ((xo >> (p3 ? 6 : 3)) & m1) | ((y >> 5) & m2);
+            } else {
+                ev = (x >> 4) & 0x0f0f0f0fu;
+                od = x & 0x0f0f0f0fu;
+            }
+        };
+        u32x4 av[8];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const Table16 tv = read_table<VB>(sb + (i < 4 ? 4 * g + i : 12 + 4 * g + i) * TS + IB * wave + TV);
+            uint32_t ev, od;
+            sel(vw[i], ev, od);
+            const uint2 e = lookup4<VB>(tv, ev), o = lookup4<VB>(tv, od);
+            av[i] = u32x4{e.x, o.x, e.y, o.y};
         }
         __syncthreads();  // the stage and descriptor slot t are free once every wave holds its operands
 
@@ -755,56 +797,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         if (t + kRing < nt) issue_desc(t + kRing);
         if (t + 2 < nt) issue(t + 2, sb);
 
-        // ---- tokens past the end were not copied: their stage bytes are stale.  Zero
-        // their norms and V indices (a stale nibble >= 8 would look up a NaN in an
-        // 8-entry table, and NaN * 0 would reach the accumulator); their scores are
-        // masked below.
-        float nk[8] = {nk0.x, nk0.y, nk0.z, nk0.w, nk1.x, nk1.y, nk1.z, nk1.w};
-        float nv[8] = {nv0.x, nv0.y, nv0.z, nv0.w, nv1.x, nv1.y, nv1.z, nv1.w};
-        if (valid < kTile) {
-            // (each masking block takes `valid` through an empty asm, so that its
-            // compares stay inside the block instead of running for every full tile)
-            const int vv = opaque_s(valid);
-            const int g4 = 4 * (int)(lane_now() >> 4);  // 4g, rebuilt here (not kept live)
-    #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int tt = i < 4 ? g4 + i : 12 + g4 + i;
-                nk[i] = tt < vv ? nk[i] : 0.f;
-                nv[i] = tt < vv ? nv[i] : 0.f;
-                if constexpr (!kTrV) vw[i] = tt < vv ? vw[i] : 0u;
-            }
-            if constexpr (kTrV) {
-                uint32_t ma = 0, mb = 0;  // bytes of the tokens 4g + k and 16 + 4g + k below valid
-    #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    ma |= (g4 + k < vv ? 0xffu : 0u) << (8 * k);
-                    mb |= (16 + g4 + k < vv ? 0xffu : 0u) << (8 * k);
-                }
-    #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    Ga[r] &= ma;
-                    Gb[r] &= mb;
-                }
-            }
-        }
-        // A V norm at or above 2^e_run (rare after the first tile): raise e_run to the
-        // tile's largest norm (over all 32 tokens: the four row groups of the wave)
-        // and rescale what carries 2^-e_run.
-        const float nvl = fmaxf(fmaxf(fmaxf(nv[0], nv[1]), fmaxf(nv[2], nv[3])), fmaxf(fmaxf(nv[4], nv[5]), fmaxf(nv[6], nv[7])));
-        if (__any(nvl >= lim)) {
-            const float nvm = rows_max(nvl);
-            const int e_tile = (int)((__float_as_uint(nvm) >> 23) & 0xffu) - 126;  // 2^e_tile > max norm
-            if (e_tile > e_run) {
-                const float f = ldexpf(1.f, e_run - e_tile);
-    #pragma unroll
-                for (int m = 0; m < 8; ++m) acc[m] *= f;
-                l_run *= f;
-                e_run = e_tile;
-                lim = ldexpf(1.f, e_run);
-            }
-        }
-
-        // ---- S^T = K Q^T ----------------------------------------------------
+        // ---- S^T = K Q^T (exact products of the q-dtype values, fp32 sums) -----------
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
         if constexpr (D3) {
             // dense group (A, B, C): positions 0..2 from their own dword, 3 from the top bits
@@ -815,23 +808,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                 const uint32_t o0 = c < 3 ? d3_odd(a0[c]) : d3_odd3(a0[1], a0[2]);
                 const uint32_t e1 = c < 3 ? d3_even(a1[c]) : d3_even3(a1[0], a1[2]);
                 const uint32_t o1 = c < 3 ? d3_odd(a1[c]) : d3_odd3(a1[1], a1[2]);
-                s0 = mfma<RQ_DTYPE_F16>(decode_row8_sel<KB>(tk, e0, o0), qop[c], s0);
-                s1 = mfma<RQ_DTYPE_F16>(decode_row8_sel<KB>(tk, e1, o1), qop[c], s1);
+                s0 = mfma<DT>(decode_row8_sel<KB>(tk0, e0, o0), qop[c], s0);
+                s1 = mfma<DT>(decode_row8_sel<KB>(tk1, e1, o1), qop[c], s1);
             }
         } else {
             const uint32_t k0w[4] = {kw0.x, kw0.y, kw0.z, kw0.w};
             const uint32_t k1w[4] = {kw1.x, kw1.y, kw1.z, kw1.w};
     #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                s0 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k0w[c]), qop[c], s0);
-                s1 = mfma<RQ_DTYPE_F16>(decode_row8<KB>(tk, k1w[c]), qop[c], s1);
+                s0 = mfma<DT>(decode_row8<KB>(tk0, k0w[c]), qop[c], s0);
+                s1 = mfma<DT>(decode_row8<KB>(tk1, k1w[c]), qop[c], s1);
             }
         }
-        // ---- scale by K norm, mask, online softmax ---------------------------
-        // s = score / sc; the score scale sc > 0 enters the exponent's fma (and the
-        // max, which it commutes with).
-        float s[8] = {s0.x * nk[0], s0.y * nk[1], s0.z * nk[2], s0.w * nk[3],
-                      s1.x * nk[4], s1.y * nk[5], s1.z * nk[6], s1.w * nk[7]};
+        // ---- mask, online softmax ------------------------------------------------------
+        // The score scale sc > 0 enters the exponent's fma (and the max, which it
+        // commutes with).
+        float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
         if (valid < kTile) {
             const int vv = opaque_s(valid);
             const int g4 = 4 * (int)(lane_now() >> 4);
@@ -844,73 +836,54 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
         tmax = rows_max(tmax) * sc;
         // Lazy running max: rescale only when a column's max exceeds m_run by more
-        // than 8 (log2 units).  In between, p = 2^(score - m_run) <= 2^8, so the
-        // fp16 P operand (p * v_norm * 2^-e_run <= 2^8) stays in range; acc and l_run
-        // are relative to the same m_run, so the result does not depend on when the
-        // rescale happens.  The exponent's fma also applies 2^-e_run.
+        // than 8 (log2 units).  In between, p = 2^(score - m_run) <= 2^8, so the fp16
+        // P operand stays in range; acc and l_run are relative to the same m_run, so
+        // the result does not depend on when the rescale happens.
         if (__any(tmax > m_run + 8.f)) {
             const float m_new = fmaxf(m_run, tmax);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
     #pragma unroll
-            for (int m = 0; m < 8; ++m) acc[m] *= alpha;
+            for (int m = 0; m < NACC; ++m) acc[m] *= alpha;
             l_run *= alpha;
             m_run = m_new;
         }
-        const float mb = -(m_run + (float)e_run);
         float p[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sc, mb));  // p * 2^-e_run
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sc, -m_run));
             l_run += p[i];
         }
-        u32x4 pop;
-        pop.x = pack2<RQ_DTYPE_F16>(p[0] * nv[0], p[1] * nv[1]);
-        pop.y = pack2<RQ_DTYPE_F16>(p[2] * nv[2], p[3] * nv[3]);
-        pop.z = pack2<RQ_DTYPE_F16>(p[4] * nv[4], p[5] * nv[5]);
-        pop.w = pack2<RQ_DTYPE_F16>(p[6] * nv[6], p[7] * nv[7]);
 
         // ---- O^T += V^T P^T ---------------------------------------------------
-        // Ga[j], Gb[j]: byte j of the lane's tokens (read transposed above, or here
-        // byte-transposed from the tokens' dwords); split nibbles per head dim.
-        if constexpr (!kTrV) {
-            const uint32_t A01 = perm(vw[1], vw[0], 0x05010400u), B01 = perm(vw[1], vw[0], 0x07030602u);
-            const uint32_t A23 = perm(vw[3], vw[2], 0x05010400u), B23 = perm(vw[3], vw[2], 0x07030602u);
-            const uint32_t A45 = perm(vw[5], vw[4], 0x05010400u), B45 = perm(vw[5], vw[4], 0x07030602u);
-            const uint32_t A67 = perm(vw[7], vw[6], 0x05010400u), B67 = perm(vw[7], vw[6], 0x07030602u);
-            Ga[0] = perm(A23, A01, 0x05040100u);
-            Ga[1] = perm(A23, A01, 0x07060302u);
-            Ga[2] = perm(B23, B01, 0x05040100u);
-            Ga[3] = perm(B23, B01, 0x07060302u);
-            Gb[0] = perm(A67, A45, 0x05040100u);
-            Gb[1] = perm(A67, A45, 0x07060302u);
-            Gb[2] = perm(B67, B45, 0x05040100u);
-            Gb[3] = perm(B67, B45, 0x07060302u);
-        }
-        // Index selectors (one index per byte) of the even and the odd dim of byte j.
-        // Dense: lanes of positions 0..2 mask their own bytes; the position-3 lane takes
-        // the top bits of its quad's A, B and C lanes (same tokens): one form for all
-        // lanes, (x >> s1) & m1 | (y >> s2) & m2, with per-lane shifts and masks.
-        auto sel = [&](uint32_t G, uint32_t &ev, uint32_t &od) {
-            if constexpr (D3) {
-                const bool p3 = (col & 3) == 3;
-                const uint32_t xe = quad_pick<0x24>(G), xo = quad_pick<0x64>(G), y = quad_pick<0xa4>(G);
-                const uint32_t m1 = p3 ? 0x03030303u : 0x07070707u, m2 = p3 ? 0x04040404u : 0u;
-                ev = ((xe >> (p3 ? 6 : 0)) & m1) | ((y >> 4) & m2);
-                od = ((xo >> (p3 ? 6 : 3)) & m1) | ((y >> 5) & m2);
-            } else {
-                ev = (G >> 4) & 0x0f0f0f0fu;
-                od = G & 0x0f0f0f0fu;
-            }
-        };
+        // P^T k slots 8g + 2i, +1 (token 16kb + 4g + i; the two dims of a pair):
+        // (p, 0) in columns < 8 and (0, p) in columns >= 8, or (WIDE) both.
+        const uint32_t x01 = pack2<RQ_DTYPE_F16>(p[0], p[1]), x23 = pack2<RQ_DTYPE_F16>(p[2], p[3]);
+        const uint32_t x45 = pack2<RQ_DTYPE_F16>(p[4], p[5]), x67 = pack2<RQ_DTYPE_F16>(p[6], p[7]);
+        if constexpr (!WIDE) {
+            const bool hi_col = (lane_now() & 8) != 0;
+            const uint32_t se = hi_col ? 0x01000c0cu : 0x0c0c0100u;  // element 0 -> (x, 0) or (0, x)
+            const uint32_t so = hi_col ? 0x03020c0cu : 0x0c0c0302u;  // element 1
+            const u32x4 b0 = u32x4{perm(x01, x01, se), perm(x01, x01, so), perm(x23, x23, se), perm(x23, x23, so)};
+            const u32x4 b1 = u32x4{perm(x45, x45, se), perm(x45, x45, so), perm(x67, x67, se), perm(x67, x67, so)};
     #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t ea, oa, eb, ob;
-            sel(Ga[j], ea, oa);
-            sel(Gb[j], eb, ob);
-            uint2 ha = lookup4<VB>(tv, ea), hb = lookup4<VB>(tv, eb);
-            uint2 la = lookup4<VB>(tv, oa), lb = lookup4<VB>(tv, ob);
-            acc[2 * j] = mfma<RQ_DTYPE_F16>(u32x4{ha.x, ha.y, hb.x, hb.y}, pop, acc[2 * j]);          // even dims
-            acc[2 * j + 1] = mfma<RQ_DTYPE_F16>(u32x4{la.x, la.y, lb.x, lb.y}, pop, acc[2 * j + 1]);  // odd dims
+            for (int rb = 0; rb < 4; ++rb) {
+                acc[rb] = mfma<RQ_DTYPE_F16>(u32x4{av[0][rb], av[1][rb], av[2][rb], av[3][rb]}, b0, acc[rb]);
+                acc[rb] = mfma<RQ_DTYPE_F16>(u32x4{av[4][rb], av[5][rb], av[6][rb], av[7][rb]}, b1, acc[rb]);
+            }
+        } else {
+            const u32x4 b0e = u32x4{x01 & 0xffffu, x01 >> 16, x23 & 0xffffu, x23 >> 16};
+            const u32x4 b1e = u32x4{x45 & 0xffffu, x45 >> 16, x67 & 0xffffu, x67 >> 16};
+            const u32x4 b0o = u32x4{x01 << 16, x01 & 0xffff0000u, x23 << 16, x23 & 0xffff0000u};
+            const u32x4 b1o = u32x4{x45 << 16, x45 & 0xffff0000u, x67 << 16, x67 & 0xffff0000u};
+    #pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const u32x4 a0 = u32x4{av[0][rb], av[1][rb], av[2][rb], av[3][rb]};
+                const u32x4 a1 = u32x4{av[4][rb], av[5][rb], av[6][rb], av[7][rb]};
+                acc[rb] = mfma<RQ_DTYPE_F16>(a0, b0e, acc[rb]);
+                acc[rb] = mfma<RQ_DTYPE_F16>(a1, b1e, acc[rb]);
+                acc[4 + rb] = mfma<RQ_DTYPE_F16>(a0, b0o, acc[4 + rb]);
+                acc[4 + rb] = mfma<RQ_DTYPE_F16>(a1, b1o, acc[4 + rb]);
+            }
         }
     }
 
@@ -1011,40 +984,51 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
 
-// Resident decode workgroups per CU for an LDS size (cached per device and size).
-template <int DT, int KB, int VB, int HPW, bool D3>
+// Resident decode workgroups per CU for an LDS size (cached per device and size;
+// the cache of each kernel instance is guarded by a mutex, so concurrent callers
+// see whole entries).
+template <int DT, int KB, int VB, int HPW, bool D3, bool WIDE>
 static int decode_per_cu(const DecodeArgs &a, size_t lds) {
     static int cache[64][8][2] = {};  // [device][entry] = {lds, workgroups per CU}
+    static std::mutex mu;
     int dev = 0;
     (void)hipGetDevice(&dev);
     dev = dev < 0 || dev >= 64 ? 0 : dev;
-    for (auto &e : cache[dev])
-        if (e[0] == (int)lds && e[1] > 0) return e[1];
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (auto &e : cache[dev])
+            if (e[0] == (int)lds && e[1] > 0) return e[1];
+    }
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW, D3>),
-                                                      64 * a.hpw, lds) != hipSuccess || nb <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nb, reinterpret_cast<const void *>(&decode_kernel<DT, KB, VB, HPW, D3, WIDE>), 64 * a.hpw, lds) !=
+            hipSuccess ||
+        nb <= 0)
         nb = 1;
     nb = std::min(nb, kMaxWgPerCu);
-    for (auto &e : cache[dev])
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto &e : cache[dev]) {
+        if (e[0] == (int)lds && e[1] > 0) break;  // another caller stored it meanwhile
         if (e[1] == 0) {
             e[0] = (int)lds;
             e[1] = nb;
             break;
         }
+    }
     return nb;
 }
 
 // configure: set the grid and range split only (before the prep kernel, which
 // needs them); otherwise launch.
-template <int DT, int KB, int VB, int HPW, bool D3>
+template <int DT, int KB, int VB, int HPW, bool D3, bool WIDE>
 static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
     if (!configure) {
-        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw), dim3(64 * a.hpw),
-                           lds, st, a);
+        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3, WIDE>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw),
+                           dim3(64 * a.hpw), lds, st, a);
         return;
     }
     // as many workgroups per kv-head group as are resident at once
-    const int per_cu = decode_per_cu<DT, KB, VB, HPW, D3>(a, lds);
+    const int per_cu = decode_per_cu<DT, KB, VB, HPW, D3, WIDE>(a, lds);
     const int groups = a.H / a.hpw;
     a.grid_w = std::max(1, per_cu * device_cus() / groups);
     // rank weights by workgroups per CU (workgroups [r CUs, (r+1) CUs) are
@@ -1061,11 +1045,17 @@ static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool conf
     a.split_r = UINT64_MAX / tot;
 }
 
+template <int DT, int KB, int VB, bool D3, bool WIDE>
+static void launch_decode_w(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3, WIDE>(a, lds, st, configure);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3, WIDE>(a, lds, st, configure);
+    else launch_decode_h<DT, KB, VB, 0, D3, WIDE>(a, lds, st, configure);
+}
+
 template <int DT, int KB, int VB, bool D3 = false>
 static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
-    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3>(a, lds, st, configure);
-    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3>(a, lds, st, configure);
-    else launch_decode_h<DT, KB, VB, 0, D3>(a, lds, st, configure);
+    if (a.G > 8) launch_decode_w<DT, KB, VB, D3, true>(a, lds, st, configure);
+    else launch_decode_w<DT, KB, VB, D3, false>(a, lds, st, configure);
 }
 
 template <int DT>
@@ -1080,7 +1070,7 @@ static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, bool d
 
 // Workspace layout (256-byte aligned regions).
 struct DecodeWorkspace {
-    int64_t part_acc, part_ml, qops, qscale, descs, tile_prefix, n_tiles, total;
+    int64_t part_acc, part_ml, qops, descs, tile_prefix, n_tiles, total;
     DecodeWorkspace(int64_t num_seqs, int64_t num_q_heads, int64_t max_seq_len) {
         auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
         const int64_t slots = (int64_t)kMaxWgPerCu * device_cus() + num_seqs;
@@ -1088,8 +1078,7 @@ struct DecodeWorkspace {
         part_acc = 0;
         part_ml = al(part_acc + slots * num_q_heads * kD * 4);
         qops = al(part_ml + slots * num_q_heads * 2 * 4);
-        qscale = al(qops + num_seqs * num_q_heads * 64 * 16 * 4);  // kv heads <= query heads
-        descs = al(qscale + num_seqs * num_q_heads * 16 * 4);
+        descs = al(qops + num_seqs * num_q_heads * 64 * 16 * 4);  // kv heads <= query heads
         tile_prefix = al(descs + max_tiles * (int64_t)sizeof(TileDesc));
         n_tiles = al(tile_prefix + num_seqs * 8);  // NT (int) at +0, range-split multiplier (uint64) at +8
         total = al(n_tiles + 16);
@@ -1265,7 +1254,6 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
         a.part_acc = reinterpret_cast<float *>(base + W.part_acc);
         a.part_ml = reinterpret_cast<float *>(base + W.part_ml);
         a.qops = reinterpret_cast<uint32_t *>(base + W.qops);
-        a.qscale = reinterpret_cast<float *>(base + W.qscale);
         a.descs = reinterpret_cast<TileDesc *>(base + W.descs);
         a.tile_prefix = reinterpret_cast<int *>(base + W.tile_prefix);
         a.n_tiles_total = reinterpret_cast<int *>(base + W.n_tiles);
@@ -1289,7 +1277,8 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
     a.split_c = 1;
     a.wt[0] = a.wt[1] = a.wt[2] = a.wt[3] = 1;
     a.split_r = UINT64_MAX;
-    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * (a.G * 256 + 64);
+    // two stages, the descriptor ring, the query slot and the two codebooks
+    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * a.G * 256 + 128;
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, true);

@@ -11,14 +11,15 @@
 //   * int8 operands are rounded to nearest and carry a second int8 "low" part,
 //     one int8 being too coarse for the 2e-2 output tolerance:
 //       Q K^T = s_q s_k [q_hi.k_hi + (q_hi.k_lo + q_lo.k_hi) / 128]   (3 int8 MFMAs)
-//     q per query row (absmax / 127); k from a per-codebook index -> int8 byte
-//     table (centroid * 127 / max|centroid| and the residual * 128) with the
-//     per-token scale norm / (largest k norm of the 64-key tile).
+//     q per query row (absmax / 127); k per 64-key tile: the reference's K,
+//     centroid * norm rounded to the q dtype (:172), in units of s_tile / 127,
+//     s_tile = dtype(max|centroid| * largest k norm of the tile) >= every |k|.
 //   P V runs on the fp16 MFMA, as the reference's 16-bit product (:217-227) but
-//   with 11-bit operands on both sides: V' = (centroid * norm) * 2^-e_tile in
-//   fp16, with 2^e_tile above the 64-key tile's largest v norm, and
-//   P' = p * 2^(e_tile - e_run) in fp16, e_run the largest e_tile so far (acc
-//   is rescaled when it grows); the row sum is a 17th MFMA row of 2^-e_tile.
+//   with 11-bit operands on both sides: V' = V * 2^-e_tile in fp16, V the
+//   reference's centroid * norm rounded to the q dtype (:224), 2^e_tile above the
+//   64-key tile's largest v norm, and P' = p * 2^(e_tile - e_run) in fp16, e_run
+//   the largest e_tile so far (acc is rescaled when it grows); the row sum is a
+//   17th MFMA row of 2^-e_tile.
 //
 // Two kernels per call:
 //   * prefill_pack_kernel decodes every 64-key tile of every (sequence, kv head)
@@ -107,7 +108,7 @@ constexpr int kImKlo = kImKhi + kKT * kKP;          // same, low parts
 constexpr int kImVt = kImKlo + kKT * kKP;          // [128 dims][64 keys] fp16 V', keys in MFMA k order
 __host__ __device__ constexpr int k_piece(int r, int c) { return r * kKP + 16 * (c ^ (r & 7)); }
 // V^T row d (128 bytes: 8 pieces of 8 keys) uses the K row swizzle: piece c at k_piece(d, c).
-constexpr int kImSk = kImVt + kPD * kKT * 2;        // float: score unit = tile k scale * kmax/127 * score_scale / 128
+constexpr int kImSk = kImVt + kPD * kKT * 2;        // float: score unit = s_tile / 127 * score_scale / 128 (int8 K)
 constexpr int kImVe = kImSk + 4;                    // int: e_tile, 2^e_tile > the tile's largest v norm
 constexpr int kImOnes = kImSk + 16;                 // row-sum operand: 4 dwords of 2^-e_tile (fp16 pair), 4 zero dwords
 constexpr int kImBytes = (kImOnes + 32 + 1023) / 1024 * 1024;  // whole 1 KB copies
@@ -142,14 +143,16 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     __shared__ uint64_t toff[kKT];
     const float kmax = codebook_max(a.kc, a.nkc);
 
-    // K codebook in int8 units; each K element is c * 127 / kmax * (k norm / tile k scale),
-    // so the key norms are part of the K operand and the score unit is one per tile.
-    // Likewise V: c * 127 / vmax * (v norm / tile v scale).
+    // K and V are the reference's values, dtype(centroid * norm), in both modes.  int8
+    // K: in units of s_tile / 127 (s_tile = dtype(kmax * largest k norm of the tile),
+    // the largest |k| the tile can hold, as rounding is monotone), so the key norms
+    // are part of the K operand and the score unit is one per tile.
     __shared__ float ktab[16], vtab[16];
-    __shared__ float krho[kKT], vnorm[kKT];
+    __shared__ float knorm[kKT], vnorm[kKT];
     __shared__ float vscale;  // 2^-e_v
+    __shared__ float kinv;    // 127 / s_tile (int8 K)
     if (tid < 16) {
-        ktab[tid] = tid < a.nkc ? (KQ == kKqInt8 ? a.kc[tid] * (127.f / kmax) : a.kc[tid]) : 0.f;
+        ktab[tid] = tid < a.nkc ? a.kc[tid] : 0.f;
         vtab[tid] = tid < a.nvc ? a.vc[tid] : 0.f;
     }
     if (tid < kKT) {
@@ -180,16 +183,18 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
             kx = fmaxf(kx, __shfl_xor(kx, o));
             vx = fmaxf(vx, __shfl_xor(vx, o));
         }
-        const float s_k = kx > 0.f ? kx : 1.f;
+        const float s_raw = Elem<DT>::to_f32(Elem<DT>::from_f32(opaque(kmax * kx)));
+        const float s_tile = s_raw > 0.f ? s_raw : 1.f;
         // 2^e_v > vx, clamped to [-14, 24] so that 2^-e_v is an fp16 (normal or denormal)
         // value: the attention kernel's row-sum MFMA reads it.  Norms above 2^24 would
         // overflow v' in fp16.
         const int e_v = min(24, max(-14, (int)((__float_as_uint(vx) >> 23) & 0xffu) - 126));
-        krho[tid] = KQ == kKqInt8 ? nkv / s_k : nkv;  // q-dtype K: the norm itself
+        knorm[tid] = nkv;
         vnorm[tid] = nvv;
         if (tid == 0) {
             *reinterpret_cast<float *>(img + kImSk) =
-                KQ == kKqInt8 ? s_k * (kmax / 127.f * a.score_scale * (1.f / 128.f)) : a.score_scale;
+                KQ == kKqInt8 ? s_tile * (1.f / 127.f) * a.score_scale * (1.f / 128.f) : a.score_scale;
+            kinv = 127.f / s_tile;
             *reinterpret_cast<int *>(img + kImVe) = e_v;
             const uint32_t w = pack_f16(ldexpf(1.f, -e_v), ldexpf(1.f, -e_v));
             *reinterpret_cast<u32x4 *>(img + kImOnes) = u32x4{w, w, w, w};
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         for (int w = tid; w < kKT * 16; w += 256) {
             const int tk = w >> 4, dw = w & 15;
             const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
-            const float nrm = krho[tk];
+            const float nrm = knorm[tk];
             uint32_t pr[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {  // byte j: dim 8 dw + 2j in the high nibble, + 1 in the low one
@@ -219,14 +224,16 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     for (int w = tid; w < kKT * 16; w += 256) {
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
         const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
-        const float rho = krho[tk];
+        const float nrm = knorm[tk], inv = kinv;
         uint32_t hw[2], lw[2];  // [0]: even dims (high nibbles), [1]: odd dims (low nibbles)
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
             uint32_t hv = 0, lv = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float t = ktab[(x >> (8 * j + (par ? 0 : 4))) & 15u] * rho;  // |t| <= 127
+                // the reference's K, dtype(c * n) (|k| <= s_tile), in units of s_tile / 127
+                const float kr = Elem<DT>::to_f32(Elem<DT>::from_f32(opaque(ktab[(x >> (8 * j + (par ? 0 : 4))) & 15u] * nrm)));
+                const float t = kr * inv;  // |t| <= 127
                 const int hi = sat_i8(t);
                 const int lo = sat_i8((t - (float)hi) * 128.f);
                 hv |= (uint32_t)(hi & 0xff) << (8 * j);
@@ -239,8 +246,8 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         *reinterpret_cast<uint2 *>(img + kImKhi + ko) = make_uint2(hw[0], hw[1]);
         *reinterpret_cast<uint2 *>(img + kImKlo + ko) = make_uint2(lw[0], lw[1]);
     }
-    // V'^T rows: v' = (centroid * norm, rounded to fp32) * 2^-e_v (exact), rounded to
-    // fp16 (|v'| < max|centroid|).  Key t = 16b + 4gg + i sits in piece
+    // V'^T rows: v' = dtype(centroid * norm) * 2^-e_v (exact), rounded to fp16 (exact
+    // unless below fp16's normal range; |v'| < max|centroid|).  Key t = 16b + 4gg + i sits in piece
     // 4 (b >> 1) + gg of its dim row, element 4 (b & 1) + i: thread (key quad,
     // dword) writes 4 consecutive keys = 8 bytes.
     {
@@ -265,9 +272,8 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t idx = (x[i] >> (8 * j + (par ? 0 : 4))) & 15u;
-                    // q-dtype K: V rounded to the q dtype first (exact in fp16 after the scale)
-                    const float v = KQ == kKqInt8 ? opaque(vtab[idx] * nv[i])
-                                                  : Elem<DT>::to_f32(Elem<DT>::from_f32(opaque(vtab[idx] * nv[i])));
+                    // V rounded to the q dtype first, as the reference (fused_paged_rq_int8_prefill.py:224)
+                    const float v = Elem<DT>::to_f32(Elem<DT>::from_f32(opaque(vtab[idx] * nv[i])));
                     e[i] = f32_to_f16_bits(v * vs);
                 }
                 *reinterpret_cast<uint2 *>(img + kImVt + k_piece(d, piece) + elem_off) =

@@ -742,9 +742,11 @@ class RQAttentionImpl(_ImplBase):
         does not take (head sizes other than 128, GQA groups above 16, fp32 models).
 
         K/V of the referenced blocks are decompressed once (rq_paged_decompress) to
-        fp32; each sequence attends over its blocks, one kv head (its GQA group of
-        query heads) and at most ~32 M scores at a time.  Host lengths come from the
-        metadata's host copies when present (one device read otherwise)."""
+        the q dtype, as the reference's _decompress_cache_paged(..., query.dtype)
+        (reference rq_backend.py:988-994); each sequence attends over its blocks in
+        fp32, one kv head (its GQA group of query heads) and at most ~32 M scores at
+        a time.  Host lengths come from the metadata's host copies when present
+        (one device read otherwise)."""
         BS = kv_cache.shape[1]
         H, D = self.num_kv_heads, self.head_size
         q = query[:num_actual_tokens]
@@ -761,9 +763,9 @@ class RQAttentionImpl(_ImplBase):
         starts = qsl.tolist()
         # capacity: every referenced block once (fewer when sequences share blocks)
         cap = max(1, sum((L + BS - 1) // BS for L in lens))
-        out_k = torch.empty(cap, BS, H, D, dtype=torch.float32, device=q.device)
+        out_k = torch.empty(cap, BS, H, D, dtype=q.dtype, device=q.device)
         k_cache, v_cache, bt, _ = _paged_decompress_fn(kv_cache, md.block_table, md.seq_lens, H, D, self._dev_kc,
-                                                       self._dev_vc, torch.float32, out_k=out_k,
+                                                       self._dev_vc, q.dtype, out_k=out_k,
                                                        out_v=torch.empty_like(out_k), **self._layout_kw())
         out_rot = torch.zeros(num_actual_tokens, HQ, D, dtype=torch.float32, device=q.device)
         for b, L in enumerate(lens):
@@ -772,8 +774,8 @@ class RQAttentionImpl(_ImplBase):
             if T <= 0 or L == 0:
                 continue
             ids = bt[b, :(L + BS - 1) // BS].long()
-            K = k_cache[ids].reshape(-1, H, D)[:L]
-            V = v_cache[ids].reshape(-1, H, D)[:L]
+            K = k_cache[ids].reshape(-1, H, D)[:L].float()
+            V = v_cache[ids].reshape(-1, H, D)[:L].float()
             rows = max(1, min(T, (32 << 20) // max(1, G * L)))
             for r0 in range(0, T, rows):
                 r1 = min(T, r0 + rows)

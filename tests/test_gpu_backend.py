@@ -88,8 +88,9 @@ def test_backend_prefill_then_decode(monkeypatch, path, mode, bits):
     got_cache = kv_cache.cpu().numpy()
     assert np.array_equal(got_cache, ref_cache), f"prefill store: {int((got_cache != ref_cache).sum())} bytes differ"
     cu = np.concatenate([[0], np.cumsum(prompts)]).astype(np.int32)
-    # rq_paged_attention follows the reference's non-fused path: K/V decompressed to the q dtype
-    kv_dtype = "bfloat16" if path == "unfused" else None
+    # both paths round K/V to the q dtype, as the reference's fused kernels
+    # (fused_paged_rq_decode.py:146-147, :190-191) and its non-fused pages do
+    kv_dtype = "bfloat16"
     ref = O.prefill_attention(q.float().numpy(), cu, ref_cache, bt, np.asarray(prompts, np.int32), H, D, pn["kc"],
                               pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16", kv_dtype=kv_dtype)
     err, excess, cs = check_tolerance(out.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)

@@ -175,7 +175,7 @@ def test_backend_dense3_prefill_then_decode(monkeypatch, fused):
     got = kv_cache.cpu().numpy()
     assert np.array_equal(got, ref_cache), f"{int((got != ref_cache).sum())} bytes differ"
     nib = O.dense3_cache_to_nibbles(ref_cache, H, D)
-    kv_dtype = None if fused else "bfloat16"
+    kv_dtype = "bfloat16"  # fused or not: K/V rounded to the q dtype, as the reference
     ref = O.prefill_attention(q.float().numpy(), cu, nib, bt, np.asarray(prompts, np.int32), H, D, pn["kc"],
                               pn["vc"], pn["R"], 1.0 / math.sqrt(D), "bfloat16", kv_dtype=kv_dtype)
     err, excess, cs = check_tolerance(out.float().cpu().numpy(), ref, "bfloat16", rot_block=p.blk)

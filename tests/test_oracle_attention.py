@@ -6,8 +6,10 @@ without the kernels, against:
 
   * torch.nn.functional.scaled_dot_product_attention in float64, over K/V
     dequantized here with torch ops from the cache bytes (block-table walk,
-    nibble split, centroid * norm in fp32), GQA by repeat_interleave and an
-    explicit causal mask at positions L - T + i;
+    nibble split, centroid * norm in fp32) and cast by torch to the q dtype as
+    both reference kernels cast them (fused_paged_rq_decode.py:146-147,
+    :190-191; fused_paged_rq_int8_prefill.py:172, :224), GQA by
+    repeat_interleave and an explicit causal mask at positions L - T + i;
   * closed forms: zero context -> zeros, L = 1 -> the V row, identical keys ->
     the mean of V, two keys -> the logistic weight of sm_scale * (s1 - s0);
   * consistency: prefill row i of a chunk equals decode over the first
@@ -16,8 +18,9 @@ without the kernels, against:
     (fused_paged_rq_decode.py:271, :201-206, :308).
 
 Planted mistakes (GQA map h % H instead of h // G, the causal mask one
-position off either way, the score scale dropped) go into the oracle through
-its helpers _kv_head / _visible / _scores, and each must fail a check here.
+position off either way, the score scale dropped, K/V left as unrounded fp32
+products) go into the oracle through its helpers _kv_head / _visible /
+_scores / decompress, and each must fail a check here.
 
 Reference kernel math: src/rotorquant_vllm/triton/fused_paged_rq_decode.py:76-206,
 fused_paged_rq_int8_prefill.py:187-189.
@@ -39,8 +42,9 @@ D = 128
 # Independent pieces (torch)
 # ---------------------------------------------------------------------------
 
-def torch_dequant(cache: np.ndarray, bt_row, L: int, H: int, kc, vc):
-    """K, V (L, H, D) float64 from the cache bytes, with torch ops only.
+def torch_dequant(cache: np.ndarray, bt_row, L: int, H: int, kc, vc, cast=None):
+    """K, V (L, H, D) float64 from the cache bytes, with torch ops only; with cast
+    (a torch dtype), the fp32 products are cast to it as the reference kernels do.
 
     Slot layout: [K idx H x 64 | K norms H x f32 | V idx | V norms | pad];
     byte j of a head holds dim 2j in its high nibble and dim 2j + 1 in its low one."""
@@ -56,7 +60,7 @@ def torch_dequant(cache: np.ndarray, bt_row, L: int, H: int, kc, vc):
         idx = torch.stack([b >> 4, b & 15], dim=-1).reshape(L, H, D)
         nrm = slot[:, norm_off:norm_off + 4 * H].contiguous().view(torch.float32).reshape(L, H, 1)
         vals = torch.as_tensor(np.asarray(cb), dtype=torch.float32)[idx] * nrm  # one fp32 product
-        return vals.double()
+        return (vals if cast is None else vals.to(cast)).double()
 
     K = part(0, H * half, kc)
     V = part(H * half + 4 * H, 2 * H * half + 4 * H, vc)
@@ -105,7 +109,7 @@ def check_decode_vs_sdpa(case) -> float:
         if L == 0:
             err = max(err, float(np.abs(got[b]).max()))
             continue
-        K, V = torch_dequant(case["cache"], case["bt"][b], L, case["H"], pn["kc"], pn["vc"])
+        K, V = torch_dequant(case["cache"], case["bt"][b], L, case["H"], pn["kc"], pn["vc"], cast=torch.bfloat16)
         qr = torch_q_rot(case["q"][b:b + 1], p.R)
         exp = sdpa_rot(qr, K, V, G, [L - 1], case["sm_scale"])[0].numpy()
         err = max(err, rel_err(got[b], exp))
@@ -134,7 +138,7 @@ def check_prefill_vs_sdpa(case) -> float:
     G = case["HQ"] // case["H"]
     for b in range(len(case["lens"])):
         s0, s1, L = int(case["cu"][b]), int(case["cu"][b + 1]), int(case["lens"][b])
-        K, V = torch_dequant(case["cache"], case["bt"][b], L, case["H"], pn["kc"], pn["vc"])
+        K, V = torch_dequant(case["cache"], case["bt"][b], L, case["H"], pn["kc"], pn["vc"], cast=torch.bfloat16)
         qr = torch_q_rot(case["q"][s0:s1], p.R)
         T = s1 - s0
         exp = sdpa_rot(qr, K, V, G, [L - T + i for i in range(T)], case["sm_scale"]).numpy()
@@ -167,7 +171,7 @@ def check_two_keys(sm_scale=1 / math.sqrt(D)) -> float:
     pn = p.np()
     got = O.decode_attention_rot(case["q"].float().numpy(), case["cache"], case["bt"], case["lens"], 1, D, pn["kc"],
                                  pn["vc"], pn["R"], sm_scale, "bfloat16")[0]
-    K, V = torch_dequant(case["cache"], case["bt"][0], 2, 1, pn["kc"], pn["vc"])
+    K, V = torch_dequant(case["cache"], case["bt"][0], 2, 1, pn["kc"], pn["vc"], cast=torch.bfloat16)
     qr = torch_q_rot(case["q"][0], p.R).numpy()  # (2, D)
     err = 0.0
     for h in range(2):
@@ -200,13 +204,13 @@ def test_two_key_closed_form():
 
 
 def test_zero_context_and_single_key():
-    """L = 0 -> zeros; L = 1 -> the dequantized V row of the query head's kv head."""
+    """L = 0 -> zeros; L = 1 -> the dequantized V row (cast to the q dtype) of the query head's kv head."""
     case = decode_case(44, 2, 2, 8, [0, 1])
     pn = case["p"].np()
     got = O.decode_attention_rot(case["q"].float().numpy(), case["cache"], case["bt"], case["lens"], 2, D, pn["kc"],
                                  pn["vc"], pn["R"], case["sm_scale"], "bfloat16")
     assert np.all(got[0] == 0)
-    _, V = torch_dequant(case["cache"], case["bt"][1], 1, 2, pn["kc"], pn["vc"])
+    _, V = torch_dequant(case["cache"], case["bt"][1], 1, 2, pn["kc"], pn["vc"], cast=torch.bfloat16)
     for h in range(8):
         assert np.array_equal(got[1, h], V[0, h // 4].numpy())
     full = O.decode_attention(case["q"].float().numpy(), case["cache"], case["bt"], case["lens"], 2, D, pn["kc"],
@@ -219,7 +223,7 @@ def test_identical_keys_give_mean_of_values():
     pn = case["p"].np()
     got = O.decode_attention_rot(case["q"].float().numpy(), case["cache"], case["bt"], case["lens"], 2, D, pn["kc"],
                                  pn["vc"], pn["R"], case["sm_scale"], "bfloat16")[0]
-    K, V = torch_dequant(case["cache"], case["bt"][0], 333, 2, pn["kc"], pn["vc"])
+    K, V = torch_dequant(case["cache"], case["bt"][0], 333, 2, pn["kc"], pn["vc"], cast=torch.bfloat16)
     assert torch.equal(K, K[0:1].expand_as(K))
     mean = V.mean(dim=0).numpy()  # (H, D)
     for h in range(8):
@@ -263,6 +267,24 @@ def test_planted_missing_scale_is_caught(monkeypatch):
     monkeypatch.setattr(O, "_scores", lambda qr, K, sm_scale: qr @ K.T)
     assert check_two_keys() > 1e-3
     assert check_decode_vs_sdpa(_decode_case()) > 1e-3
+
+
+def test_planted_unrounded_kv_is_caught(monkeypatch):
+    """K/V left as fp32 products (no cast to the q dtype) fail the decode and prefill checks."""
+    monkeypatch.setattr(O, "decompress", lambda p, n, c, dt: O.decompress_f32(p, n, c))
+    assert check_decode_vs_sdpa(_decode_case()) > 1e-4
+    assert check_prefill_vs_sdpa(_prefill_case()) > 1e-4
+    assert check_two_keys() > 1e-4
+
+
+def test_fp32_kv_option_differs_from_the_default():
+    """kv_dtype=None (no rounding) is an explicit option; the default rounds to the q dtype."""
+    case = _decode_case()
+    pn = case["p"].np()
+    args = (case["q"].float().numpy(), case["cache"], case["bt"], case["lens"], case["H"], D, pn["kc"], pn["vc"],
+            pn["R"], case["sm_scale"], "bfloat16")
+    assert np.array_equal(O.decode_attention_rot(*args), O.decode_attention_rot(*args, kv_dtype="bfloat16"))
+    assert not np.array_equal(O.decode_attention_rot(*args), O.decode_attention_rot(*args, kv_dtype=None))
 
 
 # ---------------------------------------------------------------------------
