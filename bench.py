@@ -287,10 +287,12 @@ def decode_config1_tp8_slice(steps=20):
     return out
 
 
-def unfused_call(inp, q, cu, max_q):
-    """The backend's non-fused path over a prepared cache, as it dispatches: queries of
-    at most 16 tokens -> one rq_paged_attention call; longer ones -> one rq_paged_prefill
-    call (its workspace allocated here, outside the timed calls)."""
+def unfused_call(inp, q, cu, max_q, paged_attention=False):
+    """The backend's non-fused path over a prepared cache, as it dispatches: single-token
+    decodes -> one rq_fused_decode call (max_seq_len = the block table's capacity, as the
+    backend launches it); other queries of at most 16 tokens -> one rq_paged_attention
+    call; longer ones -> one rq_paged_prefill call (workspaces allocated here, outside the
+    timed calls).  paged_attention=True: rq_paged_attention for the decodes too."""
     import torch
 
     from rotorquant_vllm import _lib
@@ -299,6 +301,17 @@ def unfused_call(inp, q, cu, max_q):
     kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
     out = torch.empty_like(q)
     args = (q, inp["caches"][0], inp["bt"], inp["lens"], cu, max_q, kc, vc, R, inp["H"], 128, inp["BS"])
+    if max_q == 1 and not paged_attention:
+        cap = inp["bt"].shape[1] * inp["BS"]
+        B = inp["lens"].shape[0]
+        ws = torch.empty(_lib.load().rq_fused_decode_workspace_bytes(B, q.shape[1], 128, cap), dtype=torch.uint8,
+                         device=dev)
+        launch = K.fused_paged_rq_decode_launcher(q, inp["caches"][0], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
+                                                  128, inp["BS"], out=out, max_seq_len=cap, workspace=ws)
+
+        def fn():
+            launch()
+        return fn
     if max_q <= 16:
         def fn():
             K.paged_attention(*args, out=out)
@@ -313,20 +326,23 @@ def unfused_call(inp, q, cu, max_q):
 
 
 def time_unfused(cfg, steps=5):
-    """The non-fused path (K/V rounded to bf16, 16-bit MFMA) on config 1's decode batch
-    (rq_paged_attention; bytes as the fused decode's roofline) or config 3's causal
-    prefill (rq_paged_prefill; algorithmic bf16 flops = 2 x the causal Q K^T + P V
-    multiply-adds)."""
+    """The non-fused path (K/V rounded to bf16) on config 1's decode batch as the backend
+    dispatches it (rq_fused_decode; bytes as the fused decode's roofline; also
+    rq_paged_attention on the same batch) or config 3's causal prefill (rq_paged_prefill;
+    algorithmic bf16 flops = 2 x the causal Q K^T + P V multiply-adds)."""
     import torch
     if cfg == 1:
         lens = config1_lens()
         inp = build_decode_inputs(lens, copies=1)
         B = len(lens)
         cu = torch.arange(B + 1, dtype=torch.int32, device="cuda")
-        ms = time_events(unfused_call(inp, inp["q"], cu, 1), steps)
+        ms = time_events(unfused_call(inp, inp["q"], cu, 1), max(steps, 20))
+        ms_pa = time_events(unfused_call(inp, inp["q"], cu, 1, paged_attention=True), steps)
         nb = decode_bytes(lens, 8, 32, 128, 16)
         gbs = nb / (ms * 1e-3) / 1e9
-        out = dict(batch=B, us=round(ms * 1e3, 1), GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2))
+        out = dict(batch=B, us=round(ms * 1e3, 1), GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2),
+                   kernel="rq_fused_decode (the backend's dispatch of single-token decodes)",
+                   paged_attention_us=round(ms_pa * 1e3, 1))
     else:
         q_lens = [4096] * 8
         inp = prefill_inputs(q_lens, q_lens, 8, 32, 3, "iso", 4)
@@ -475,9 +491,11 @@ def config0_roundtrip(budget_s=10.0):
 
 
 def cpu_baseline(inp, gpu_out, budget_s=15.0):
-    """CPU path on a bounded sample: oracle decompress of each sequence's blocks + torch fp32
-    attention (the reference has no CPU decode path).  Its outputs, rounded as the reference
-    rounds (bf16 out_rot, back-rotation, bf16), are also compared with the GPU's output."""
+    """CPU path on a bounded sample: oracle decompress of each sequence's blocks to bf16 (K and V
+    rounded to the q dtype as the reference's kernel rounds them, fused_paged_rq_decode.py:146-147,
+    :190-191) + torch fp32 attention (the reference has no CPU decode path).  Its outputs, rounded
+    as the reference rounds (bf16 out_rot, back-rotation, bf16), are also compared with the GPU's
+    output."""
     import numpy as np
     import torch
 
@@ -497,7 +515,7 @@ def cpu_baseline(inp, gpu_out, budget_s=15.0):
     outs = []
     t0 = time.perf_counter()
     for b, L in enumerate(lens):
-        K_, V_ = O.gather_seq(cache, inp["bt_host"][b], L, H, D, p.kc.numpy(), p.vc.numpy())
+        K_, V_ = O.gather_seq(cache, inp["bt_host"][b], L, H, D, p.kc.numpy(), p.vc.numpy(), kv_dtype="bfloat16")
         Kt = torch.from_numpy(K_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
         Vt = torch.from_numpy(V_.astype(np.float32)).repeat_interleave(G, dim=1).transpose(0, 1)
         qr = torch.from_numpy(O.rotate_q(q[b].numpy(), R, "bfloat16"))
@@ -514,7 +532,8 @@ def cpu_baseline(inp, gpu_out, budget_s=15.0):
     err, excess, cs = check_tolerance(got, ref, "bfloat16", rot_block=p.blk)
     return dict(value=done_bytes / el / 1e9, unit="GB/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"{n_seq} of {len(lens)} config-1 sequences ({sum(lens[:n_seq])} tokens): oracle C "
-                       f"decompress + torch fp32 attention, {el:.1f} s", cpu=cpu_model(), os_cpu_count=os.cpu_count(),
+                       f"decompress to bf16 + torch fp32 attention, {el:.1f} s", cpu=cpu_model(),
+                os_cpu_count=os.cpu_count(),
                 gpu_vs_cpu={"max_abs": err, "cos": round(cs, 7), "within_tolerance": bool(excess <= 0 and cs >= 0.999),
                             "tolerance": "cos >= 0.999, |d| <= max(2e-2, ulp(x) + 2 ulp(rotation-block max))"})
 
@@ -659,8 +678,12 @@ def main():
         print("bench.py: graph replay differs from eager results; timing eager launches", file=sys.stderr)
         t, gpu_out = time_decode(inp, args.steps, args.warmup, graphs=False)
     nbytes = decode_bytes(lens, 8, 32, 128, 16)
-    step_s = t["avg_ms"] * 1e-3
+    # Headline: the median of the per-step event times (each step bracketed by events);
+    # the back-to-back mean (two events around all timed steps) is the roofline's
+    # average launch duration.
+    step_s = t["median_ms"] * 1e-3
     gbs = nbytes / step_s / 1e9
+    gbs_mean = nbytes / (t["avg_ms"] * 1e-3) / 1e9
     result = {
         "metric": "fused paged decode HBM GB/s (Llama-3-8B layer, iso fast 3-bit, B=64, L~U[1024,8192])",
         "value": round(gbs, 1),
@@ -681,11 +704,15 @@ def main():
         "decode_tok_per_s": round(64 / step_s, 1),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "step_ms": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in t.items() if k != "wall_s"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+        "value_basis": "algorithmic bytes / median per-step time (HIP events around each step on the launch "
+                       "stream, %d steps)" % args.steps,
+        "GBps_back_to_back_mean": round(gbs_mean, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs_mean, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs_mean / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "one rq_fused_decode call (decode_prep_kernel + decode_kernel + decode_merge_kernel), "
-                               "HIP events around each call on its stream; traffic = HBM bytes per call from "
-                               "profiles/decode_cfg1_traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated)"},
+                               "average duration from two HIP events around the back-to-back timed calls on their "
+                               "stream; traffic = HBM bytes per call from profiles/decode_cfg1_traffic.json "
+                               "(rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated)"},
     }
     if not args.no_compress:
         result["compress"] = time_compress()

@@ -115,6 +115,7 @@ _compress_store_fn = None
 _paged_decompress_fn = None
 _paged_attention_fn = None
 _paged_prefill_fn = None
+_unfused_decode_fn = None
 _shared_workspace = None
 try:
     from rotorquant_vllm import _lib as _rq_lib
@@ -123,6 +124,8 @@ try:
     from rotorquant_vllm.kernels import fused_paged_rq_int8_prefill as _fused_paged_rq_int8_prefill_fn
     from rotorquant_vllm.kernels import paged_attention as _paged_attention_fn
     from rotorquant_vllm.kernels import paged_prefill as _paged_prefill_fn
+    # The non-fused path's single-token decodes (a separate hook from the fused path's)
+    from rotorquant_vllm.kernels import fused_paged_rq_decode as _unfused_decode_fn
     from rotorquant_vllm.kernels import paged_decompress as _paged_decompress_fn
     from rotorquant_vllm.kernels import shared_workspace as _shared_workspace
 
@@ -429,10 +432,27 @@ class RQMetadataBuilder(_BuilderBase):
 
     @classmethod
     def get_cudagraph_support(cls, vllm_config: object, kv_cache_spec: object):
+        """UNIFORM_SINGLE_TOKEN_DECODE when the layer's decodes run a HIP kernel whose
+        launch does not depend on host data (the fused decode, or rq_paged_attention):
+        the library loads, head_size 128, a GQA group the kernels take and an f16 /
+        bf16 model.  Otherwise NEVER: such decodes run the torch fallback, whose loop
+        over host lengths cannot be captured."""
         if not _fused_paged_kernel_available:
             return AttentionCGSupport.NEVER
         head_size = getattr(kv_cache_spec, "head_size", RQ_FUSED_HEAD_DIM)
         if head_size != RQ_FUSED_HEAD_DIM:
+            return AttentionCGSupport.NEVER
+        model_config = getattr(vllm_config, "model_config", None)
+        dtype = getattr(model_config, "dtype", None)
+        if isinstance(dtype, torch.dtype) and dtype not in (torch.float16, torch.bfloat16):
+            return AttentionCGSupport.NEVER
+        num_kv = getattr(kv_cache_spec, "num_kv_heads", None)
+        num_heads = None
+        try:
+            num_heads = model_config.get_num_attention_heads(vllm_config.parallel_config)
+        except Exception:  # no model config (tests) or an older vLLM: decided by head_size alone
+            pass
+        if num_kv and num_heads and _fused_shape_ok(num_heads, num_kv, head_size) is not None:
             return AttentionCGSupport.NEVER
         return AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE
 
@@ -583,7 +603,8 @@ class RQAttentionImpl(_ImplBase):
         if dev.type == "cuda" and _shared_workspace is not None:
             lib = _rq_lib.load()
             cap = -(-self._max_model_len // kv_cache.shape[1]) * kv_cache.shape[1]
-            if self._fused_paged_available:
+            unfused_decode = _unfused_decode_fn is not None and self._unfused_kernel_ok(compute_dtype, self.num_heads)
+            if self._fused_paged_available or unfused_decode:
                 _shared_workspace(dev, "decode", lib.rq_fused_decode_workspace_bytes(
                     self._max_num_seqs, self.num_heads, self.head_size, cap))
             if self._fused_prefill_available or self._unfused_kernel_ok(compute_dtype, self.num_heads):
@@ -614,12 +635,14 @@ class RQAttentionImpl(_ImplBase):
 
     # -- fused paths -----------------------------------------------------------
 
-    def _fused_decode(self, query, kv_cache, block_table, seq_lens, output, n):
-        """Fused decode of sequences [0, n) (one query token each) into output[:n].
+    def _fused_decode(self, query, kv_cache, block_table, seq_lens, output, n, fn=None):
+        """Fused decode of sequences [0, n) (one query token each) into output[:n], through
+        fn (default: the fused path's hook _fused_paged_rq_decode_fn).
 
         max_seq_len is the block table's capacity, not the batch's longest
         sequence: a captured HIP graph replays with longer sequences than it was
         captured with, so the launch must not depend on the lengths."""
+        fn = _fused_paged_rq_decode_fn if fn is None else fn
         kc, vc, R = self._launch_operands()
         BS = kv_cache.shape[1]
         cap = block_table.shape[1] * BS
@@ -627,7 +650,7 @@ class RQAttentionImpl(_ImplBase):
         if _shared_workspace is not None and query.device.type == "cuda":
             ws = _shared_workspace(query.device, "decode", _rq_lib.load().rq_fused_decode_workspace_bytes(
                 n, query.shape[1], self.head_size, cap))
-        _call_hook(_fused_paged_rq_decode_fn, query[:n], kv_cache, block_table, seq_lens, kc, vc, R,
+        _call_hook(fn, query[:n], kv_cache, block_table, seq_lens, kc, vc, R,
                    self.num_kv_heads, self.head_size, BS, sm_scale=self.scale, out=output[:n], max_seq_len=cap,
                    workspace=ws, **self._layout_kw())
 
@@ -653,7 +676,10 @@ class RQAttentionImpl(_ImplBase):
     def _fused_batch(self, query, kv_cache, md, output, num_actual_tokens):
         """A batch with multi-token sequences through the fused kernels: the leading
         single-token sequences (vLLM orders decodes first) go to the fused decode,
-        the rest to the int8 prefill in groups that fit its workspace."""
+        the rest to the int8 prefill in groups that fit its workspace.  A prefill hook
+        with the reference's signature (one sequence per call, no cu_seqlens_q:
+        fused_paged_rq_int8_prefill.py:247-260, :305-309) is called once per sequence
+        with that sequence's own query and output rows."""
         qsl_cpu = getattr(md, "rq_query_start_loc_cpu", None)
         sl_cpu = getattr(md, "rq_seq_lens_cpu", None)
         qsl_cpu = (qsl_cpu if qsl_cpu is not None else md.query_start_loc.cpu()).tolist()
@@ -671,6 +697,15 @@ class RQAttentionImpl(_ImplBase):
         kc, vc, R = self._launch_operands()
         BS = kv_cache.shape[1]
         bt = md.block_table
+        names = _accepted_keywords(_fused_paged_rq_int8_prefill_fn)
+        if names is not None and "cu_seqlens_q" not in names:
+            for b in range(nd, B):
+                s0, s1 = qsl_cpu[b], qsl_cpu[b + 1]
+                if s1 > s0:
+                    _call_hook(_fused_paged_rq_int8_prefill_fn, query[s0:s1], kv_cache, bt[b:b + 1],
+                               md.seq_lens[b:b + 1], kc, vc, R, self.num_kv_heads, self.head_size, BS,
+                               sm_scale=self.scale, out=output[s0:s1], **self._layout_kw())
+            return output
         for g0, g1, mx, mq in self._prefill_groups(lens, q_lens, nd, BS, bt.shape[1], query.device):
             _call_hook(_fused_paged_rq_int8_prefill_fn, query[:num_actual_tokens], kv_cache, bt[g0:g1],
                        md.seq_lens[g0:g1], kc, vc, R, self.num_kv_heads, self.head_size, BS, sm_scale=self.scale,
@@ -689,14 +724,18 @@ class RQAttentionImpl(_ImplBase):
         """Non-fused path (replaces :937-1036: q pre-rotation, paged decompress to the q
         dtype, flash_attn_varlen_func, back-rotation).
 
-        head_size 128, f16/bf16: queries of at most RQ_UNFUSED_SHORT_Q tokens (decodes)
-        take one rq_paged_attention launch over the whole batch (K/V tiles dequantized
-        to the q dtype in LDS; no workspace, no host read of the metadata, capturable
-        in a HIP graph).  A batch with longer queries sends its leading short ones
-        (vLLM orders decodes first) to rq_paged_attention and the rest to
-        rq_paged_prefill (same arithmetic; each 64-key tile decoded once into the
-        prefill workspace, in groups that fit it).  Other shapes: the device path
-        _forward_unfused_torch."""
+        head_size 128, f16/bf16: a batch of single-token decodes takes the decode kernel
+        (rq_fused_decode: its arithmetic is this path's -- K/V rounded to the q dtype,
+        exact Q K^T products, fp32 sums -- and a decode sees its whole context, causal
+        or not; the batch's tiles are split over the whole GPU, and the launch is
+        capturable in a HIP graph).  Other queries of at most RQ_UNFUSED_SHORT_Q tokens
+        take one rq_paged_attention launch (K/V tiles dequantized to the q dtype in
+        LDS; no workspace, no host read of the metadata, capturable).  A batch with
+        longer queries sends its leading single-token decodes (vLLM orders decodes
+        first) to the decode kernel, the following short ones to rq_paged_attention
+        and the rest to rq_paged_prefill (same arithmetic; each 64-key tile decoded
+        once into the prefill workspace, in groups that fit it).  Other shapes: the
+        device path _forward_unfused_torch."""
         q = query[:num_actual_tokens]
         if not self._unfused_kernel_ok(q.dtype, q.shape[1]):
             return self._forward_unfused_torch(query, kv_cache, md, output, num_actual_tokens)
@@ -706,6 +745,11 @@ class RQAttentionImpl(_ImplBase):
             qsl_cpu = getattr(md, "rq_query_start_loc_cpu", None)
             qsl_cpu = qsl_cpu if qsl_cpu is not None else md.query_start_loc.cpu()
             max_q = int((qsl_cpu[1:] - qsl_cpu[:-1]).max()) if qsl_cpu.numel() > 1 else 0
+        decode_ok = _unfused_decode_fn is not None and _shared_workspace is not None
+        if int(max_q) == 1 and decode_ok:
+            self._fused_decode(query, kv_cache, md.block_table, md.seq_lens, output, num_actual_tokens,
+                               fn=_unfused_decode_fn)
+            return output
         kc, vc, R = self._launch_operands()
         BS = kv_cache.shape[1]
         causal = bool(getattr(md, "causal", True))
@@ -723,13 +767,19 @@ class RQAttentionImpl(_ImplBase):
         lens = (sl_cpu if sl_cpu is not None else md.seq_lens.cpu()).tolist()
         B = len(lens)
         q_lens = [qsl[b + 1] - qsl[b] for b in range(B)]
-        ns = 0
+        nd = 0
+        if decode_ok:
+            while nd < B and q_lens[nd] == 1:
+                nd += 1
+        bt = md.block_table
+        if nd:
+            self._fused_decode(query, kv_cache, bt[:nd], md.seq_lens[:nd], output, nd, fn=_unfused_decode_fn)
+        ns = nd
         while ns < B and q_lens[ns] <= RQ_UNFUSED_SHORT_Q:
             ns += 1
-        bt = md.block_table
-        if ns:
-            _paged_attention_fn(q, kv_cache, bt[:ns], md.seq_lens[:ns], md.query_start_loc[:ns + 1],
-                                max(q_lens[:ns]), kc, vc, R, self.num_kv_heads, self.head_size, BS,
+        if ns > nd:
+            _paged_attention_fn(q, kv_cache, bt[nd:ns], md.seq_lens[nd:ns], md.query_start_loc[nd:ns + 1],
+                                max(q_lens[nd:ns]), kc, vc, R, self.num_kv_heads, self.head_size, BS,
                                 sm_scale=self.scale, causal=causal, out=out, **self._layout_kw())
         for g0, g1, mx, mq in self._prefill_groups(lens, q_lens, ns, BS, bt.shape[1], query.device):
             _paged_prefill_fn(q, kv_cache, bt[g0:g1], md.seq_lens[g0:g1], md.query_start_loc[g0:g1 + 1], mq, kc, vc,
@@ -747,6 +797,9 @@ class RQAttentionImpl(_ImplBase):
         fp32, one kv head (its GQA group of query heads) and at most ~32 M scores at
         a time.  Host lengths come from the metadata's host copies when present
         (one device read otherwise)."""
+        if query.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("RotorQuant: this layer's shape or dtype runs the torch fallback (a loop over host "
+                               "sequence lengths), which cannot be captured in a graph")
         BS = kv_cache.shape[1]
         H, D = self.num_kv_heads, self.head_size
         q = query[:num_actual_tokens]

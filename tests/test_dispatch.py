@@ -153,6 +153,40 @@ def test_mixed_batch_splits_decodes_and_prefill_groups(monkeypatch, host_copies)
     assert torch.all(output == 1.0)
 
 
+def test_mixed_batch_with_reference_signature_prefill_hook(monkeypatch):
+    """A prefill hook with the reference's signature (one sequence, no cu_seqlens_q) on a
+    mixed batch [1, 1, 1, 40 | 7]: it is called once per multi-token sequence with that
+    sequence's own query / output rows, block-table row and length; the decode rows are
+    written only by the decode hook."""
+    impl = _bare_impl(True, True)
+    calls = []
+
+    def fake_decode(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads, head_dim,
+                    block_size, sm_scale=None, out=None):
+        calls.append(("decode", tuple(q.shape), seq_lens.tolist()))
+        out.fill_(1.0)
+        return out
+
+    def fake_prefill(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads, head_dim,
+                     block_size, sm_scale=None, out=None):
+        if seq_lens.numel() != 1:
+            raise ValueError("single sequence only")
+        calls.append(("prefill", tuple(q.shape), seq_lens.tolist(), block_table[0, 0].item()))
+        out.fill_(7.0)
+        return out
+
+    monkeypatch.setattr(rq_backend_module, "_fused_paged_rq_decode_fn", fake_decode)
+    monkeypatch.setattr(rq_backend_module, "_fused_paged_rq_int8_prefill_fn", fake_prefill)
+    q_lens, seq_lens = [1, 1, 1, 40, 7], [300, 30, 9, 300, 107]
+    md = _mixed_metadata(q_lens, seq_lens)
+    query = torch.randn(md.num_actual_tokens, 8, 128)
+    output = torch.zeros_like(query)
+    impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
+    assert calls == [("decode", (3, 8, 128), [300, 30, 9]), ("prefill", (40, 8, 128), [300], 3 * 64),
+                     ("prefill", (7, 8, 128), [107], 4 * 64)]
+    assert torch.all(output[:3] == 1.0) and torch.all(output[3:] == 7.0)
+
+
 def test_single_token_batch_goes_to_decode_only(monkeypatch):
     impl = _bare_impl(True, True)
     seen = []
@@ -183,6 +217,14 @@ def test_fused_flags_follow_the_kernel_shapes(monkeypatch):
     spec = SimpleNamespace(head_size=128)
     assert (rq_backend_module.RQMetadataBuilder.get_cudagraph_support(None, spec)
             == rq_backend_module.AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE)
+    # shapes or dtypes whose decodes run the torch fallback (not capturable): NEVER
+    for num_heads, dtype, exp in ((32, torch.bfloat16, "UNIFORM_SINGLE_TOKEN_DECODE"), (32, torch.float32, "NEVER"),
+                                  (8 * 17, torch.float16, "NEVER")):
+        mc = SimpleNamespace(dtype=dtype, get_num_attention_heads=lambda pc, n=num_heads: n)
+        cfg = SimpleNamespace(model_config=mc, parallel_config=None)
+        spec = SimpleNamespace(head_size=128, num_kv_heads=8)
+        got = rq_backend_module.RQMetadataBuilder.get_cudagraph_support(cfg, spec)
+        assert got == getattr(rq_backend_module.AttentionCGSupport, exp), (num_heads, dtype)
 
 
 def test_triton_import_path_is_the_hip_op():
@@ -244,15 +286,22 @@ def test_unfused_short_queries_are_one_paged_attention_call(monkeypatch, causal)
 
 @pytest.mark.parametrize("causal", [True, False])
 def test_unfused_long_queries_split_to_paged_prefill(monkeypatch, causal):
-    """A non-fused batch with a query longer than RQ_UNFUSED_SHORT_Q: its leading short
-    queries (sequences 0..1) are one rq_paged_attention call, the rest go to
-    rq_paged_prefill in contiguous groups whose tile images fit the prefill workspace
-    (sized here for 2 x 320 keys x 8 kv heads), each with its own max_seq_len and
-    max_q_len; every query row is written exactly once."""
+    """A non-fused batch with a query longer than RQ_UNFUSED_SHORT_Q: its leading
+    single-token decode (sequence 0) goes to the decode kernel, the following short
+    query (sequence 1) to one rq_paged_attention call, the rest to rq_paged_prefill in
+    contiguous groups whose tile images fit the prefill workspace (sized here for 2 x
+    320 keys x 8 kv heads), each with its own max_seq_len and max_q_len; every query
+    row is written exactly once."""
     from rotorquant_vllm import _lib
     from rotorquant_vllm import kernels as K
     impl = _bare_impl(False, False)
     calls = []
+
+    def fake_decode(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads, head_dim,
+                    block_size, sm_scale=None, out=None, max_seq_len=None, workspace=None):
+        calls.append(("decode", tuple(q.shape), seq_lens.tolist(), tuple(block_table.shape), max_seq_len))
+        out += 1.0
+        return out
 
     def fake_attn(q, kv_cache, block_table, seq_lens, cu_seqlens_q, max_q_len, kc, vc, R, num_kv_heads, head_dim,
                   block_size, sm_scale=None, causal=True, out=None):
@@ -270,6 +319,7 @@ def test_unfused_long_queries_split_to_paged_prefill(monkeypatch, causal):
 
     monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", fake_attn)
     monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", fake_prefill)
+    monkeypatch.setattr(rq_backend_module, "_unfused_decode_fn", fake_decode)
     budget = _lib.load().rq_paged_prefill_workspace_bytes(2, 8, 320)
     monkeypatch.setitem(K._ws_cache, ("cpu", "prefill"), torch.empty(budget, dtype=torch.uint8))
     q_lens, seq_lens = [1, 3, 40, 7, 100], [500, 30, 300, 107, 320]
@@ -278,7 +328,40 @@ def test_unfused_long_queries_split_to_paged_prefill(monkeypatch, causal):
     query = torch.randn(md.num_actual_tokens, 32, 128, dtype=torch.float16)
     output = torch.zeros_like(query)
     impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
-    assert calls == [("attn", [500, 30], [0, 1, 4], (2, 64), 3, causal),
+    assert calls == [("decode", (1, 32, 128), [500], (1, 64), 64 * 16),
+                     ("attn", [30], [1, 4], (1, 64), 3, causal),
                      ("prefill", [300, 107], [4, 44, 51], 40, 300, causal),
                      ("prefill", [320], [51, 151], 100, 320, causal)]
     assert torch.all(output == 1.0)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_unfused_decode_batch_takes_the_decode_kernel(monkeypatch, causal):
+    """Without RQ_USE_FUSED_PAGED a uniform batch of single-token decodes
+    (max_query_len 1) is one decode-kernel call (rq_fused_decode: the same K/V
+    rounding and exact products as rq_paged_attention) with the block table's
+    capacity as max_seq_len and no host read of the metadata; the fused path's hook
+    _fused_paged_rq_decode_fn is not used."""
+    impl = _bare_impl(False, False)
+    calls = []
+
+    def fake_decode(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation, num_kv_heads, head_dim,
+                    block_size, sm_scale=None, out=None, max_seq_len=None, workspace=None):
+        calls.append((tuple(q.shape), block_table is md.block_table, seq_lens is md.seq_lens, max_seq_len, sm_scale))
+        out.fill_(4.0)
+        return out
+
+    def unused(*a, **k):
+        raise AssertionError("a decode batch must not reach this kernel")
+
+    monkeypatch.setattr(rq_backend_module, "_unfused_decode_fn", fake_decode)
+    monkeypatch.setattr(rq_backend_module, "_fused_paged_rq_decode_fn", unused)
+    monkeypatch.setattr(rq_backend_module, "_paged_attention_fn", unused)
+    monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", unused)
+    md = _mixed_metadata([1, 1, 1, 1], [500, 30, 300, 107], host_copies=False)
+    md.causal = causal
+    query = torch.randn(4 + 2, 32, 128, dtype=torch.bfloat16)  # 2 padding rows
+    output = torch.zeros_like(query)
+    impl.forward(None, query, None, None, torch.zeros(40, 16, 2048, dtype=torch.uint8), md, output=output)
+    assert calls == [((4, 32, 128), True, True, 64 * 16, 0.125)]
+    assert torch.all(output[:4] == 4.0) and torch.all(output[4:] == 0.0)

@@ -239,10 +239,11 @@ def test_backend_decode_step_graph_replay(monkeypatch):
 
 def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
     """The default (non-fused) path: a mixed batch of decodes and chunks in one forward
-    -- the decodes through rq_paged_attention, the two chunks through one
+    -- the decodes through the decode kernel, the two chunks through one
     rq_paged_prefill call -- checked against the oracle of the reference's non-fused
     path; then a decode step on the same path captured in a HIP graph replays the
-    eager output bit for bit (no host read of the metadata, no workspace)."""
+    eager output bit for bit (no host read of the metadata; the decode workspace was
+    allocated at the first forward)."""
     ctx = [3000, 700, 5, 800, 64]
     q_lens = [1, 1, 1, 200, 64]
     impl, p, c = _mixed_setup(monkeypatch, 4, 28, "iso", 3, "full", ctx, q_lens, 73, fused=False)
@@ -259,12 +260,13 @@ def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
     monkeypatch.setattr(rq_backend_module, "_paged_attention_fn",
                         counted("attention", rq_backend_module._paged_attention_fn))
     monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", counted("prefill", rq_backend_module._paged_prefill_fn))
+    monkeypatch.setattr(rq_backend_module, "_unfused_decode_fn", counted("decode", rq_backend_module._unfused_decode_fn))
     dev = torch.device("cuda")
     kv_cache = torch.from_numpy(c["cache0"]).to(dev)
     out = torch.empty(c["q"].shape, dtype=torch.bfloat16, device=dev)
     impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
     torch.cuda.synchronize()
-    assert seen == [("attention", 3), ("prefill", 2)], seen
+    assert seen == [("decode", 3), ("prefill", 2)], seen
     got_cache = kv_cache.cpu().numpy()
     assert np.array_equal(got_cache, c["full_cache"]), f"{int((got_cache != c['full_cache']).sum())} bytes differ"
     pn = p.np()
@@ -309,9 +311,10 @@ def test_backend_unfused_mixed_batch_and_decode_graph(monkeypatch):
 
 def test_backend_unfused_prefill_groups(monkeypatch):
     """The non-fused path with a prefill workspace that holds one 800-token sequence's
-    tile images (4 kv heads): the two chunks of a mixed batch go to rq_paged_prefill
-    in two calls, each with its own max_seq_len and its absolute query rows, and the
-    whole output matches the oracle of the reference's non-fused path."""
+    tile images (4 kv heads): the three decodes of a mixed batch go to the decode
+    kernel, its two chunks to rq_paged_prefill in two calls, each with its own
+    max_seq_len and its absolute query rows, and the whole output matches the oracle
+    of the reference's non-fused path."""
     from rotorquant_vllm import _lib
     from rotorquant_vllm import kernels as K
     import rotorquant_vllm.vllm.rq_backend as rq_backend_module
@@ -331,14 +334,22 @@ def test_backend_unfused_prefill_groups(monkeypatch):
             return fn(q, kv, block_table, seq_lens, cu, max_q, *a, **k)
         return wrapper
 
+    def counted_decode(fn):
+        def wrapper(q, kv, block_table, seq_lens, *a, **k):
+            seen.append(("decode", seq_lens.shape[0], q.shape[0], k.get("max_seq_len")))
+            return fn(q, kv, block_table, seq_lens, *a, **k)
+        return wrapper
+
     monkeypatch.setattr(rq_backend_module, "_paged_attention_fn",
                         counted("attention", rq_backend_module._paged_attention_fn))
     monkeypatch.setattr(rq_backend_module, "_paged_prefill_fn", counted("prefill", rq_backend_module._paged_prefill_fn))
+    monkeypatch.setattr(rq_backend_module, "_unfused_decode_fn", counted_decode(rq_backend_module._unfused_decode_fn))
     out = torch.full(c["q"].shape, float("nan"), dtype=torch.bfloat16, device=dev)
     print(f"unfused prefill groups: ctx={ctx} q_lens={q_lens} workspace={budget} B", flush=True)
     impl.forward(None, c["q"].to(dev), c["k_new"].to(dev), c["v_new"].to(dev), kv_cache, c["md"], output=out)
     torch.cuda.synchronize()
-    assert seen == [("attention", 3, 1, None), ("prefill", 1, 200, 800), ("prefill", 1, 64, 64)], seen
+    cap = c["md"].block_table.shape[1] * BS
+    assert seen == [("decode", 3, 3, cap), ("prefill", 1, 200, 800), ("prefill", 1, 64, 64)], seen
     pn = p.np()
     cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     ref = O.unfused_attention(c["q"].float().numpy(), cu, c["full_cache"], c["bt"], np.asarray(ctx, np.int32), 4, D,

@@ -147,3 +147,94 @@ def test_config4_chunks_after_prefixes(entry):
     _prefill_check(f"config4 chunks prefixes={pre}", inp, _sampled_rows, entry)
     del inp
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_config4_one_forward(monkeypatch, path):
+    """Config 4 as ONE RQAttentionImpl.forward: 128 decodes (1 x 131072 + 127 x U[512, 16384]
+    context) then 4 chunks of 2048 tokens after prefixes U{0..14336}, 28 q / 4 kv heads, iso
+    full 3-bit, bf16 (reference anchor: the mixed batch of rq_backend.py:957-976).  fused:
+    RQ_USE_FUSED_PAGED=1 (decode kernel + rq_int8_prefill); unfused: the default path
+    (decode kernel + rq_paged_prefill).  The forward first stores the 8324 new tokens' K/V:
+    their slots must equal the oracle's compress-store of them byte for byte.  Then the
+    131072-token decode, a seeded 31 of the other decodes and every 32nd row plus the last
+    32 of each chunk are checked against the oracle over the cache as the forward left it."""
+    import types
+
+    from rq_testlib import Params
+
+    monkeypatch.setenv("RQ_MODE", "iso")
+    monkeypatch.setenv("RQ_BITS", "3")
+    monkeypatch.setenv("RQ_ISO_MODE", "full")
+    monkeypatch.delenv("RQ_K_BITS", raising=False)
+    monkeypatch.delenv("RQ_V_BITS", raising=False)
+    if path == "fused":
+        monkeypatch.setenv("RQ_USE_FUSED_PAGED", "1")
+    else:
+        monkeypatch.delenv("RQ_USE_FUSED_PAGED", raising=False)
+    from rotorquant_vllm.vllm.rq_backend import RQAttentionImpl
+
+    dec = [131072] + torch.randint(512, 16384 + 1, (127,), generator=torch.Generator().manual_seed(4004)).tolist()
+    pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
+    ctx = dec + [x + 2048 for x in pre]
+    q_lens = [1] * len(dec) + [2048] * 4
+    inp = gpu_decode_inputs(ctx, H=4, HQ=28, cfg=4, mode="iso", iso_mode="full", copies=1, kv="kscale",
+                            kv_dtype="bfloat16")
+    dev = inp["q"].device
+    impl = RQAttentionImpl(28, 128, 128 ** -0.5, num_kv_heads=4)
+    impl._max_model_len = 131072
+    assert impl._fused_paged_available == (path == "fused")
+    T = int(sum(q_lens))
+    g = torch.Generator(device=dev).manual_seed(4006)
+    q = torch.randn(T, 28, 128, generator=g, device=dev).to(torch.bfloat16)
+    k_new = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    v_new = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    bt_host = inp["bt_host"]
+    slots = np.concatenate([bt_host[b, np.arange(L - ql, L) // 16].astype(np.int64) * 16 + np.arange(L - ql, L) % 16
+                            for b, (L, ql) in enumerate(zip(ctx, q_lens))])
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    md = types.SimpleNamespace(num_actual_tokens=T, max_query_len=2048, use_cascade=False, causal=True,
+                               slot_mapping=torch.from_numpy(slots).to(dev), block_table=inp["bt"],
+                               seq_lens=inp["lens"], query_start_loc=torch.from_numpy(cu).to(dev),
+                               max_seq_len=max(ctx))
+    md.rq_query_start_loc_cpu, md.rq_seq_lens_cpu = torch.from_numpy(cu), torch.tensor(ctx, dtype=torch.int32)
+    out = torch.full_like(q, float("nan"))
+    print(f"config4 one forward ({path}): {len(dec)} decodes (sum L {sum(dec)}), chunk prefixes {pre}", flush=True)
+    impl.forward(None, q, k_new, v_new, inp["caches"][0], md, output=out)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), "every query row is written"
+
+    # the stored new tokens, byte for byte
+    p = Params("iso", 3, 3, iso_mode="full")
+    pn = p.np()
+    TB = inp["caches"][0].shape[2]
+    ref_rows = np.zeros((T, 1, TB), np.uint8)
+    kb_, _ = O.to_bits(k_new.cpu())
+    vb_, _ = O.to_bits(v_new.cpu())
+    kp, kn = O.compress(kb_, "bfloat16", pn["rte"], pn["rto"], pn["kb"], p.blk)
+    vp, vn = O.compress(vb_, "bfloat16", pn["rte"], pn["rto"], pn["vb"], p.blk)
+    O.compress_store(ref_rows, np.arange(T), kp, kn, vp, vn)
+    flat = inp["caches"][0].view(-1, TB)
+    got_rows = flat.index_select(0, torch.from_numpy(slots).to(dev)).cpu().numpy()
+    assert np.array_equal(got_rows, ref_rows[:, 0]), f"{int((got_rows != ref_rows[:, 0]).sum())} stored bytes differ"
+
+    # decodes: the long one and a seeded 31 of the others
+    others = sorted(1 + torch.randperm(127, generator=torch.Generator().manual_seed(4008))[:31].numpy())
+    dseq = [0] + [int(x) for x in others]
+    sub, bt, sl = host_subcache(inp["caches"][0], bt_host, ctx, dseq)
+    ref = O.decode_attention(q.float().cpu().numpy()[dseq], sub, bt, sl, 4, 128, pn["kc"], pn["vc"], pn["R"],
+                             1 / math.sqrt(128), "bfloat16")
+    _report(f"config4 one forward ({path}): decodes", got[dseq], ref, "bfloat16", p.blk)
+
+    # chunks: sampled rows of each
+    cseq = list(range(128, 132))
+    sub, bt, sl = host_subcache(inp["caches"][0], bt_host, ctx, cseq)
+    ccu = cu[128:] - cu[128]
+    rows = np.concatenate([ccu[i] + _sampled_rows(2048) for i in range(4)])
+    oracle_fn = O.prefill_attention if path == "fused" else O.unfused_attention
+    ref = oracle_fn(q.float().cpu().numpy()[cu[128]:], ccu, sub, bt, sl, 4, 128, pn["kc"], pn["vc"], pn["R"],
+                    1 / math.sqrt(128), "bfloat16", rows=rows)
+    _report(f"config4 one forward ({path}): chunks", got[cu[128]:][rows], ref[rows], "bfloat16", p.blk)
+    del inp
+    torch.cuda.empty_cache()
