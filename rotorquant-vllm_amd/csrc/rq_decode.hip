@@ -98,7 +98,8 @@ __device__ __forceinline__ u32x4 decode_row8(const Table16 &t, uint32_t x) {
 //   8 entries  (16 bytes): lo0 hi0 lo1 hi1          (lo0: low bytes of entries 0-3)
 //   16 entries (32 bytes): lo0 hi0 lo1 hi1 lo2 hi2 lo3 hi3
 // Half hh (entries [NE/2 hh, NE/2 (hh + 1))) is written by one lane: 8 bytes at
-// 8 hh, or 16 bytes at 16 hh.
+// 8 hh of the first 16-byte piece, or the 16-byte piece hh (the two pieces of a
+// 32-byte table need not be adjacent).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint2 planes4(uint32_t p01, uint32_t p23) {  // 4 values as pairs -> (lo, hi) dwords
     return make_uint2(perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u));
@@ -110,7 +111,7 @@ __device__ __forceinline__ uint2 planes4(uint32_t p01, uint32_t p23) {  // 4 val
 // 2^-17 and below 65504).  The product is rounded to fp32 before the 16-bit
 // rounding, as the reference's fp32 multiply followed by .to(dtype).
 template <int DT, int BITS, bool F16_IMAGE>
-__device__ __forceinline__ void table_half(const float *cb, float m, int hh, uint8_t *dst) {
+__device__ __forceinline__ void table_half(const float *cb, float m, int hh, uint8_t *dst0, uint8_t *dst1) {
     constexpr int NH = (1 << BITS) / 2;  // entries per half
     const float4 *c4 = reinterpret_cast<const float4 *>(cb + NH * hh);
     uint32_t pr[NH / 2];
@@ -127,20 +128,20 @@ __device__ __forceinline__ void table_half(const float *cb, float m, int hh, uin
         }
     }
     if constexpr (NH == 4) {
-        *reinterpret_cast<uint2 *>(dst + 8 * hh) = planes4(pr[0], pr[1]);
+        *reinterpret_cast<uint2 *>(dst0 + 8 * hh) = planes4(pr[0], pr[1]);
     } else {
         const uint2 x = planes4(pr[0], pr[1]), y = planes4(pr[2], pr[3]);
-        *reinterpret_cast<u32x4 *>(dst + 16 * hh) = u32x4{x.x, x.y, y.x, y.y};
+        *reinterpret_cast<u32x4 *>(hh ? dst1 : dst0) = u32x4{x.x, x.y, y.x, y.y};
     }
 }
 
 template <int BITS>
-__device__ __forceinline__ Table16 read_table(const uint8_t *p) {
+__device__ __forceinline__ Table16 read_table(const uint8_t *p0, const uint8_t *p1) {
     Table16 t;
-    const u32x4 r = *reinterpret_cast<const u32x4 *>(p);
+    const u32x4 r = *reinterpret_cast<const u32x4 *>(p0);
     t.lo[0] = r.x, t.hi[0] = r.y, t.lo[1] = r.z, t.hi[1] = r.w;
     if constexpr (BITS == 4) {
-        const u32x4 s = *reinterpret_cast<const u32x4 *>(p + 16);
+        const u32x4 s = *reinterpret_cast<const u32x4 *>(p1);
         t.lo[2] = s.x, t.hi[2] = s.y, t.lo[3] = s.z, t.hi[3] = s.w;
     } else {
         t.lo[2] = t.lo[3] = t.hi[2] = t.hi[3] = 0u;
@@ -399,16 +400,24 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
         // the owner of tile t is the number of w in [1, G) with range_start(w) <= t
         // (range_start is non-decreasing and range_start(0) = 0).
         const RangeSplit r{a.split_c, a.grid_w, NT, a.wt[0], a.wt[1], a.wt[2], a.wt[3], split_multiplier(a, NT)};
-        int c_lo = 0, c_hi = 0;
-        for (int w = 1 + lane; w < r.G; w += 64) {
-            const int rs = range_start(r, w);
-            c_lo += rs <= prefix ? 1 : 0;
-            c_hi += rs <= prefix + n - 1 ? 1 : 0;
-        }
-        for (int o = 32; o >= 1; o >>= 1) {
-            c_lo += __shfl_xor(c_lo, o);
-            c_hi += __shfl_xor(c_hi, o);
-        }
+        // c(t) = #{w in [1, G): range_start(w) <= t}, in two rounds of 64 evaluations:
+        // lane k tests w = 1 + k * step (a ballot brackets the answer), then w = 1 + base
+        // + k within the bracket (step <= 64 while G <= 4097; beyond that a lane loop).
+        const int step = (r.G - 1 + 63) / 64;
+        auto count_le = [&](int tk) {
+            const int w1 = 1 + lane * step;
+            const uint64_t m1 = __ballot(w1 < r.G && range_start(r, w1) <= tk);
+            const int k = m1 ? 63 - __clzll(m1) : -1;  // last coarse point at or below tk
+            if (k < 0) return 0;
+            int c = k * step + 1;  // w = 1 .. 1 + k * step all count
+            for (int j0 = 1; j0 < step; j0 += 64) {
+                const int w2 = 1 + k * step + j0 + lane;
+                const uint64_t m2 = __ballot(j0 + lane < step && w2 < r.G && range_start(r, w2) <= tk);
+                c += __popcll(m2);
+            }
+            return c;
+        };
+        const int c_lo = count_le(prefix), c_hi = count_le(prefix + n - 1);
         if (lane == 0) {
             a.tile_prefix[2 * seq] = n > 0 ? c_lo : 0;
             a.tile_prefix[2 * seq + 1] = n > 0 ? c_hi - c_lo + 1 : 0;
@@ -487,18 +496,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int hpw = HPW > 0 ? HPW : a.hpw;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;    // k-group / row-group
-    const int col = lane & 15;  // MFMA column (query head inside the GQA group) / row
     const int h0 = blockIdx.z * hpw;
     const SlotLayout SL(a.H, kD, D3);
     constexpr int IB = D3 ? 48 : 64;   // index bytes per head
-    constexpr int TV = D3 ? 16 : 32;   // V table offset in a token's K index bytes (K table at 0)
     constexpr bool kScaleV = DT == RQ_DTYPE_BF16;  // V fp16 image carries 2^-e_run (bf16 range)
-    const int TS = HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride;
+    // One or two kv heads per workgroup (tensor-parallel slices): a token's K and V index
+    // runs are only 128 * HPW bytes, so copies use all 64 lanes with per-lane addresses
+    // (8 / HPW tokens per instruction) into tokens of 128 * HPW bytes whose 16-byte
+    // pieces are XOR-swizzled (piece p of token t at 16 (p ^ swz(t))), which keeps the
+    // operand reads free of bank conflicts.  Otherwise one instruction per token and a
+    // 16-byte skew per token.
+    constexpr bool kLine = (HPW == 1 || HPW == 2) && !D3;
+    const int TS = kLine ? 128 * HPW : (HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride);
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
-    const int tl = lane & 31;  // token of this lane's codebook tables (and slot base, norm copy)
-    const int hh = lane >> 5;  // the half of those tables this lane builds
+    const int tl_copy = lane & 31;  // token of this lane's norm copy (rows layout)
 
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *const stage0 = lds;
@@ -509,6 +521,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     const int G = a.G;
     uint8_t *const qarea = lds + 2 * stage_bytes + kRing * sizeof(TileDesc);
     float *const cbarea = reinterpret_cast<float *>(qarea + hpw * G * 256);
+
+    // Byte offset in a stage of byte b of 16-byte piece p of token t (pieces: K indices
+    // of the hpw heads, 4 per head, then V indices; nibble layouts).  swz(t) = (t >> 1) & 7
+    // gives the 8 even (odd) tokens of 16 consecutive ones distinct pieces, and is equal
+    // for tokens t, t + 1 and t + 16, so most operand addresses differ by immediates.
+    auto swz = [](int t) { return (t >> 1) & 7; };
+    auto at = [&](int t, int p, int b) { return t * TS + 16 * (kLine ? (p ^ swz(t)) : p) + b; };
 
     // Descriptor of local tile i -> ring slot i % kRing (wave 0, one copy).
     auto issue_desc = [&](int i) {
@@ -525,11 +544,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         constexpr int PH = IB / 16;  // 16-byte pieces per head
         const uint32_t kv_src = lane < PH * hpw ? (uint32_t)(SL.k_idx + IB * h0 + 16 * lane)
                                                 : (uint32_t)(SL.v_idx + IB * h0 + 16 * (lane - PH * hpw));
-        for (int tt = wave; tt < valid; tt += hpw) {
-            const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
-            if (lane < 2 * PH * hpw) copy16(tok, kv_src, dst + tt * TS);
+        if constexpr (kLine) {
+            // 64 lanes = TPI tokens x PPT pieces; wave w issues instructions 4w .. 4w + 3
+            constexpr int PPT = 8 * HPW, TPI = 64 / PPT;
+            const uint32_t l = lane_now();
+    #pragma unroll
+            for (int j = 4 * wave; j < 4 * wave + 4; ++j) {
+                if (j * TPI >= valid) break;
+                const int t = j * TPI + (int)(l / PPT);
+                const int p = (int)(l % PPT) ^ swz(t);
+                const uint32_t src = p < 4 * HPW ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * p)
+                                                 : (uint32_t)(SL.v_idx + 64 * h0 + 16 * (p - 4 * HPW));
+                if (t < valid) copy16v(a.cache + d.off[t] + src, dst + j * 1024);
+            }
+        } else {
+            for (int tt = wave; tt < valid; tt += hpw) {
+                const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
+                if (lane < 2 * PH * hpw) copy16(tok, kv_src, dst + tt * TS);
+            }
         }
-        if constexpr (HPW > 0) {
+        if constexpr (HPW >= 4) {
             // Norms in 16-byte pieces (4 heads' K or V norms of one token): piece p =
             // kind * NPH + sub (kind 0: K, 1: V; sub: heads 4 sub .. 4 sub + 3) of token t
             // lands at slot 32 p + t.  Copy c (wave c) moves pieces 2c and 2c + 1 of all
@@ -547,12 +581,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             const int nrow = 2 * wave + (lane >> 5);
             const uint32_t norm_src = nrow < hpw ? (uint32_t)(SL.k_norm + 4 * (h0 + nrow))
                                                  : (uint32_t)(SL.v_norm + 4 * (h0 + nrow - hpw));
-            if (tl < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
+            if (tl_copy < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
         }
     };
     // This wave's K (kind 0) or V (kind 1) norm of token t in stage sb.
     auto norm_at = [&](const uint8_t *sb, int kind, int t) {
-        if constexpr (HPW > 0) {
+        if constexpr (HPW >= 4) {
             constexpr int NPH = HPW / 4;
             return *reinterpret_cast<const float *>(sb + norm_off + 16 * ((kind * NPH + (wave >> 2)) * 32 + t) +
                                                     4 * (wave & 3));
@@ -662,9 +696,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             constexpr int HP = HPW > 0 ? HPW : 8, NPH = HP / 4;
             const int v1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid);
             // token copies tt = wave, wave + HPW, ... < v1; a norm copy on the waves < NPH
-            const int n = (v1 > wave ? (v1 - wave + HP - 1) / HP : 0) + (wave < NPH ? 1 : 0) +
-                          (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
-            wait_copies_n<kTile / HP + 2>(n);
+            // (16-byte pieces, HPW >= 4) or on every wave (4-byte rows, HPW < 4; its lane
+            // of token 0 always copies)
+            // (line copies: instructions 4 wave + j, j < 4, whose first token is below v1)
+            constexpr int TPI = 8 / HP;
+            const int n_tok = kLine ? min(4, max(0, (v1 + TPI - 1) / TPI - 4 * wave))
+                                    : (v1 > wave ? (v1 - wave + HP - 1) / HP : 0);
+            const int n = n_tok + (HP >= 4 ? (wave < NPH ? 1 : 0) : 1) + (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
+            wait_copies_n<(kLine ? 4 : kTile / HP) + 2>(n);
         } else {
             wait_copies<0>();
         }
@@ -678,28 +717,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             begin_segment();
         }
         // ---- this wave's operands of the tile ------------------------------------
+        // (lane-derived values of this section are rebuilt from the lane id here, so
+        // that their addresses are not loop-invariant registers: under pressure those
+        // are spilled, and a spill reload waits for every copy in flight)
+        const uint32_t lnow = lane_now();
+        const int col = (int)(lnow & 15), g = (int)(lnow >> 4), tl = (int)(lnow & 31), hh = (int)(lnow >> 5);
         // K: token col (and 16 + col), dims 32g .. 32g+31 (16 nibble bytes, or the
         // 12-byte dense group g)
-        const uint8_t *kb = sb + col * TS + IB * wave + (D3 ? 12 : 16) * g;
         uint4 kw0, kw1;
         if constexpr (D3) {
+            const uint8_t *kb = sb + col * TS + IB * wave + 12 * g;
             const uint32_t *k0p = reinterpret_cast<const uint32_t *>(kb);
             const uint32_t *k1p = reinterpret_cast<const uint32_t *>(kb + 16 * TS);
             kw0 = make_uint4(k0p[0], k0p[1], k0p[2], 0u);
             kw1 = make_uint4(k1p[0], k1p[1], k1p[2], 0u);
         } else {
-            kw0 = *reinterpret_cast<const uint4 *>(kb);
-            kw1 = *reinterpret_cast<const uint4 *>(kb + 16 * TS);
+            kw0 = *reinterpret_cast<const uint4 *>(sb + at(col, 4 * wave + g, 0));
+            kw1 = *reinterpret_cast<const uint4 *>(sb + at(16 + col, 4 * wave + g, 0));
         }
         // V: nibble dword col (dims 8 col .. 8 col + 7) of the lane's 8 tokens 4g + i and
         // 16 + 4g + i, or dense: dword min(col % 4, 2) of group col / 4 (position 3 is
         // assembled from the quad's other lanes below)
         uint32_t vw[8];
-        {
-            const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave +
-                                (D3 ? 12 * (col >> 2) + 4 * min(col & 3, 2) : 4 * col);
+        if constexpr (D3) {
+            const uint8_t *vb = sb + 4 * g * TS + IB * hpw + IB * wave + 12 * (col >> 2) + 4 * min(col & 3, 2);
     #pragma unroll
             for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t *>(vb + (i < 4 ? i : 12 + i) * TS);
+        } else {
+    #pragma unroll
+            for (int i = 0; i < 8; ++i)
+                vw[i] = *reinterpret_cast<const uint32_t *>(
+                    sb + at(i < 4 ? 4 * g + i : 12 + 4 * g + i, 4 * hpw + 4 * wave + (col >> 2), 4 * (col & 3)));
         }
         // the K and V norms of token tl (this lane's tables)
         float nk = norm_at(sb, 0, tl), nv = norm_at(sb, 1, tl);
@@ -743,14 +791,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         // ---- codebook tables of token tl: this lane's half of the K table (q dtype) and
         // of the V table (fp16 image), written over the wave's own K index bytes of the
         // token, which were read above (LDS instructions of a wave complete in order)
-        {
-            uint8_t *tab = sb + tl * TS + IB * wave;
-            table_half<DT, KB, false>(cbarea, nk, hh, tab);
-            table_half<DT, VB, true>(cbarea + 16, kScaleV ? ldexpf(nv, -e_run) : nv, hh, tab + TV);
-        }
+        // Tables of token t: K in K index pieces 0 (and 1) of the wave's head, V in pieces
+        // 2 (and 3); dense layout: K at byte 0, V at byte 16 of the head's 48 bytes.
+        auto tab_k = [&](int t, int q) { return sb + (D3 ? t * TS + IB * wave + 16 * q : at(t, 4 * wave + q, 0)); };
+        auto tab_v = [&](int t, int q) { return sb + (D3 ? t * TS + IB * wave + 16 + 16 * q : at(t, 4 * wave + 2 + q, 0)); };
+        table_half<DT, KB, false>(cbarea, nk, hh, tab_k(tl, 0), tab_k(tl, 1));
+        table_half<DT, VB, true>(cbarea + 16, kScaleV ? ldexpf(nv, -e_run) : nv, hh, tab_v(tl, 0), tab_v(tl, 1));
         __builtin_amdgcn_wave_barrier();
-        const Table16 tk0 = read_table<KB>(sb + col * TS + IB * wave);
-        const Table16 tk1 = read_table<KB>(sb + (16 + col) * TS + IB * wave);
+        const Table16 tk0 = read_table<KB>(tab_k(col, 0), tab_k(col, 1));
+        const Table16 tk1 = read_table<KB>(tab_k(16 + col, 0), tab_k(16 + col, 1));
         // ---- V operands: token i's dims of the lane's nibble dword, by pair:
         //   av[i] = (e0 e2) (e1 e3) (e4 e6) (e5 e7)
         // Index selectors (one index per byte) of the even and the odd dims.  Dense:
@@ -772,7 +821,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         u32x4 av[8];
     #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const Table16 tv = read_table<VB>(sb + (i < 4 ? 4 * g + i : 12 + 4 * g + i) * TS + IB * wave + TV);
+            const int ti = i < 4 ? 4 * g + i : 12 + 4 * g + i;
+            const Table16 tv = read_table<VB>(tab_v(ti, 0), tab_v(ti, 1));
             uint32_t ev, od;
             sel(vw[i], ev, od);
             const uint2 e = lookup4<VB>(tv, ev), o = lookup4<VB>(tv, od);
@@ -904,7 +954,7 @@ template <int DT, int kMergePass>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int64_t seq = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hq = blockIdx.x * 4 + wave;
+    const int hq = blockIdx.x * (blockDim.x >> 6) + wave;
     __shared__ float orot_all[4][kD];
     float *orot = orot_all[wave];
     if (hq >= a.HQ) return;
@@ -982,7 +1032,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     reinterpret_cast<uint32_t *>(dst)[lane] = packed;
 }
 
-constexpr int kMaxWgPerCu = 4;  // bound on decode workgroups per CU (sizes the partial slots)
+// Bound on decode workgroups per CU (sizes the partial slots).  One-wave workgroups
+// (one kv head: a tensor-parallel slice) timed the same at 4, 8 and 16 per CU.
+constexpr int kMaxWgPerCu = 4;
 
 // Resident decode workgroups per CU for an LDS size (cached per device and size;
 // the cache of each kernel instance is guarded by a mutex, so concurrent callers
@@ -1049,6 +1101,8 @@ template <int DT, int KB, int VB, bool D3, bool WIDE>
 static void launch_decode_w(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
     if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3, WIDE>(a, lds, st, configure);
     else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3, WIDE>(a, lds, st, configure);
+    else if (a.hpw == 2) launch_decode_h<DT, KB, VB, 2, D3, WIDE>(a, lds, st, configure);
+    else if (a.hpw == 1) launch_decode_h<DT, KB, VB, 1, D3, WIDE>(a, lds, st, configure);
     else launch_decode_h<DT, KB, VB, 0, D3, WIDE>(a, lds, st, configure);
 }
 
@@ -1267,7 +1321,9 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
             a.hpw = d;
             break;
         }
-    a.tok_stride = 2 * SlotLayout(num_kv_heads, head_dim, dense3).ib * a.hpw + 16;
+    // token stride in a stage: 128 bytes per head, unpadded (swizzled) for one or two heads
+    // per workgroup in the nibble layout; else the index runs plus a 16-byte skew
+    a.tok_stride = (a.hpw <= 2 && !dense3) ? 128 * a.hpw : 2 * SlotLayout(num_kv_heads, head_dim, dense3).ib * a.hpw + 16;
     a.stage_bytes = kTile * a.tok_stride + 2 * a.hpw * kTile * 4;
     a.max_len = num_blocks > 0 ? (int)std::min<int64_t>(max_blocks * block_size, max_seq_len) : 0;
     a.out = out;
@@ -1286,7 +1342,7 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
         // Descriptor workgroups per sequence (y >= 1): enough that each thread writes at
         // most two steps of four tokens of the longest sequence (a fixed three made the
         // prep kernel of a 131072-token sequence take ~49 us).
-        const int pthreads = 64 * std::min(a.H, kMaxWaves);
+        const int pthreads = 64 * std::max(4, std::min(a.H, kMaxWaves));
         const int ny = std::min(64, std::max(3, (a.max_len + 8 * pthreads - 1) / (8 * pthreads)));
         const dim3 pgrid((unsigned)num_seqs, (unsigned)(1 + ny)), pblock(pthreads);
         // query staging sized by the waves launched (it bounds how many workgroups a CU holds)
@@ -1300,17 +1356,20 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
         rc = check_launch("decode_kernel");
         if (rc) return rc;
     }
-    dim3 mgrid((num_q_heads + 3) / 4, (unsigned)num_seqs);
+    // One wave per (sequence, query head): four per workgroup, or one when the batch has
+    // few (sequence, head) pairs, so that they spread over all CUs.
+    const int mw = num_seqs * (int64_t)num_q_heads >= 4LL * device_cus() ? 4 : 1;
+    dim3 mgrid((num_q_heads + mw - 1) / mw, (unsigned)num_seqs), mblock(64 * mw);
     // 32-segment passes when a sequence may span many decode workgroups (very long
     // contexts), or when all merge waves fit at once at the lower occupancy
     // (3 per SIMD); otherwise 16 (config 2: 8192 short merges).
     const bool wide = a.max_len >= 65536 || num_seqs * (int64_t)num_q_heads <= 12LL * device_cus();
     if (dtype == RQ_DTYPE_BF16) {
-        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 32>), mgrid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 16>), mgrid, dim3(256), 0, st, a);
+        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 32>), mgrid, mblock, 0, st, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 16>), mgrid, mblock, 0, st, a);
     } else {
-        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 32>), mgrid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 16>), mgrid, dim3(256), 0, st, a);
+        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 32>), mgrid, mblock, 0, st, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 16>), mgrid, mblock, 0, st, a);
     }
     return check_launch("decode_merge_kernel");
 }

@@ -76,6 +76,7 @@ def test_noalloc_refuses_oversize_without_launch():
     assert L.rq_fused_decode_workspace_bytes(2, 32, 128, huge) > SCRATCH_BYTES
     head[18] = huge           # max_seq_len
     head[15] = huge // 16     # max_blocks (the table is not read: the call is refused first)
+    t["out"].fill_(1.5)  # a known value (an empty tensor may hold NaN bit patterns, which never compare equal)
     sentinel = t["out"].clone()
     rc = L.rq_fused_decode_noalloc(*head, t["out"].data_ptr(), t["out"].stride(0), t["out"].stride(1),
                                    _lib.stream_ptr(dev))
