@@ -654,6 +654,12 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    if args.calib_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only:
         fn = {"compress": time_compress, "prefill3": time_prefill_cfg3, "decode2": lambda: decode_config(2),
               "decode4": lambda: decode_config(4), "prefill4": time_mixed_cfg4,
@@ -664,12 +670,6 @@ def main():
               "decode1_tp8": decode_config1_tp8_slice}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
-    if args.calib_copy:
-        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     lens = config1_lens()
     inp = build_decode_inputs(lens)
     torch.cuda.synchronize()
