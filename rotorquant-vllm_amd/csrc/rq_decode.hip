@@ -277,14 +277,16 @@ __device__ __forceinline__ void query_operand(const DecodeArgs &a, int64_t seq, 
     __builtin_amdgcn_wave_barrier();
 }
 
-// s_waitcnt vmcnt(min(n, MAXN)) for a wave-uniform n.
-template <int MAXN>
-__device__ __forceinline__ void wait_copies_n(int n) {
-    if constexpr (MAXN > 0) {
-        if (n >= MAXN) wait_copies<MAXN>();
-        else wait_copies_n<MAXN - 1>(n);
+// s_waitcnt vmcnt(min(n, HI)) for a wave-uniform n >= LO (binary search over the
+// immediates; a count above HI waits for more than needed, never for less).
+template <int LO, int HI>
+__device__ __forceinline__ void wait_copies_upto(int n) {
+    if constexpr (LO >= HI) {
+        wait_copies<HI>();
     } else {
-        wait_copies<0>();
+        constexpr int MID = (LO + HI + 1) / 2;
+        if (n >= MID) wait_copies_upto<MID, HI>(n);
+        else wait_copies_upto<LO, MID - 1>(n);
     }
 }
 
@@ -296,7 +298,22 @@ struct TileDesc {
 };
 static_assert(sizeof(TileDesc) == 16 + 8 * kTile, "TileDesc layout");
 constexpr int kDescPieces = (int)sizeof(TileDesc) / 16;  // 16-byte copy pieces per descriptor
-constexpr int kRing = 4;                                   // descriptors staged ahead in LDS
+
+// Pipeline depth of a decode variant (hpw kv heads per workgroup, dense layout d3):
+// NS stages, tile t + NS copied into the stage of tile t once it is consumed.  The
+// descriptor ring holds at least twice as many descriptors as there are stages: the
+// descriptor of tile t + NS is then copied before the copies of tile t, so the wait
+// for tile t covers it (and the descriptors of tiles t+1 .. t+2 read for the query
+// look-ahead).  Two stages everywhere: deeper pipelines for the small stages of one
+// or two heads per workgroup were measured slower (six stages at one head: the
+// initial copies of all workgroups, 26 MB at once, delayed every first tile by
+// ~4 us, and the loop itself is bound by one wave's latency per SIMD, not copies).
+constexpr bool decode_line_copies(int hpw, bool d3) { return (hpw == 1 || hpw == 2) && !d3; }
+constexpr int decode_stages(int hpw, bool d3) { return (void)hpw, (void)d3, 2; }
+constexpr int decode_ring(int hpw, bool d3) { return decode_stages(hpw, d3) == 2 ? 4 : decode_stages(hpw, d3) <= 4 ? 8 : 16; }
+static_assert(decode_ring(1, false) >= 2 * decode_stages(1, false) && decode_ring(2, false) >= 2 * decode_stages(2, false) &&
+                  decode_ring(8, false) >= 2 * decode_stages(8, false),
+              "descriptor ring too small for the stages");
 
 // First tile of workgroup w's range, w in [0, grid_w]: the tiles of all
 // sequences are split into contiguous ranges by weight.  With several workgroups
@@ -468,16 +485,21 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
 // each segment ends in a partial (m, l, acc) at slot w + seq, which is unique
 // because ranges are contiguous and ordered.
 //
-// Data movement: tile descriptors are copied into an LDS ring four tiles ahead
-// and each tile's K/V index runs and norms two tiles ahead, into two stages:
+// Data movement: tile descriptors are copied into an LDS ring of RING slots,
+// RING tiles ahead, and each tile's K/V index runs and norms NS tiles ahead into
+// NS stages (decode_stages: 2, or 3 / 6 for two / one kv heads per workgroup):
 //   stage layout: token t at t * tok_stride: [K idx of the hpw heads | V idx]
 //                 then the norms (2 * hpw x 32 fp32).
 // One copy instruction moves a whole token's K+V index run (8*hpw x 16 B), so
-// every request covers whole cache lines.  Iteration t: wait for tile t (tile
-// t+1 stays in flight), barrier, read this wave's index bytes and norms, build
-// the codebook tables into the wave's own K index bytes (read already), read the
-// tables and look the V operands up, barrier, copy descriptor t+4 and tile t+2,
-// compute tile t from registers.
+// every request covers whole cache lines.  Iteration t: wait for tile t (tiles
+// t+1 .. t+NS-1 stay in flight), barrier, read this wave's index bytes and
+// norms, build the codebook tables into the wave's own K index bytes (read
+// already), read the tables and look the V operands up, barrier, copy
+// descriptor t+RING and tile t+NS, compute tile t from registers.  Each wave
+// counts the copies it issues (every copy instruction has its first lane active,
+// so none is skipped); the wait for tile t lets exactly the copies issued after
+// tile t's stay in flight -- and none after the query operand of a segment that
+// starts at tile t.
 // Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
 constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
 
@@ -506,20 +528,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     // pieces are XOR-swizzled (piece p of token t at 16 (p ^ swz(t))), which keeps the
     // operand reads free of bank conflicts.  Otherwise one instruction per token and a
     // 16-byte skew per token.
-    constexpr bool kLine = (HPW == 1 || HPW == 2) && !D3;
+    constexpr bool kLine = decode_line_copies(HPW, D3);
+    constexpr int NS = decode_stages(HPW, D3), RING = decode_ring(HPW, D3);
     const int TS = kLine ? 128 * HPW : (HPW > 0 ? 2 * IB * HPW + 16 : a.tok_stride);
     const int norm_off = kTile * TS;
     const int stage_bytes = HPW > 0 ? kTile * TS + 2 * HPW * kTile * 4 : a.stage_bytes;
     const int tl_copy = lane & 31;  // token of this lane's norm copy (rows layout)
 
     extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *const stage0 = lds;
-    uint8_t *const stage1 = lds + stage_bytes;
-    const TileDesc *const ring = reinterpret_cast<const TileDesc *>(lds + 2 * stage_bytes);
+    const TileDesc *const ring = reinterpret_cast<const TileDesc *>(lds + NS * stage_bytes);
     // Query operand slot: per wave, its kv head's G columns (256 bytes each); then
     // the K and V codebooks (16 floats each, zero-padded).
     const int G = a.G;
-    uint8_t *const qarea = lds + 2 * stage_bytes + kRing * sizeof(TileDesc);
+    uint8_t *const qarea = lds + NS * stage_bytes + RING * sizeof(TileDesc);
     float *const cbarea = reinterpret_cast<float *>(qarea + hpw * G * 256);
 
     // Byte offset in a stage of byte b of 16-byte piece p of token t (pieces: K indices
@@ -529,16 +550,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     auto swz = [](int t) { return (t >> 1) & 7; };
     auto at = [&](int t, int p, int b) { return t * TS + 16 * (kLine ? (p ^ swz(t)) : p) + b; };
 
-    // Descriptor of local tile i -> ring slot i % kRing (wave 0, one copy).
+    // Descriptor of local tile i -> ring slot i % RING (wave 0, one copy).  Each
+    // issue function returns the number of copy instructions this wave issued.
     auto issue_desc = [&](int i) {
         if (wave == 0 && lane < kDescPieces)
-            copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * lane, lds_addr(reinterpret_cast<const uint8_t *>(ring + i % kRing)));
+            copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * lane, lds_addr(reinterpret_cast<const uint8_t *>(ring + (i & (RING - 1)))));
+        return wave == 0 ? 1 : 0;
     };
     // Copies of local tile i into stage sb.  Per wave and full tile: kTile / hpw
-    // token copies and, on waves < hpw / 4, one norm copy.
+    // token copies (line copies: four) and one norm copy (HPW >= 4: on waves < hpw / 4).
     auto issue = [&](int i, const uint8_t *sb) {
-        const TileDesc &d = ring[i % kRing];
+        const TileDesc &d = ring[i & (RING - 1)];
         const int valid = __builtin_amdgcn_readfirstlane(d.valid);
+        int n = 0;
         const uint64_t base = d.off[lane_now() & 31];
         const uint32_t dst = lds_addr(sb);
         constexpr int PH = IB / 16;  // 16-byte pieces per head
@@ -551,6 +575,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     #pragma unroll
             for (int j = 4 * wave; j < 4 * wave + 4; ++j) {
                 if (j * TPI >= valid) break;
+                ++n;
                 const int t = j * TPI + (int)(l / PPT);
                 const int p = (int)(l % PPT) ^ swz(t);
                 const uint32_t src = p < 4 * HPW ? (uint32_t)(SL.k_idx + 64 * h0 + 16 * p)
@@ -561,6 +586,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             for (int tt = wave; tt < valid; tt += hpw) {
                 const uint8_t *tok = a.cache + readlane64(base, tt);  // uniform slot address
                 if (lane < 2 * PH * hpw) copy16(tok, kv_src, dst + tt * TS);
+                ++n;
             }
         }
         if constexpr (HPW >= 4) {
@@ -575,6 +601,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
                 const int kind = p / NPH, sub = p % NPH;
                 const uint32_t src = (kind ? (uint32_t)SL.v_norm : (uint32_t)SL.k_norm) + 4 * h0 + 16 * sub;
                 if (t < valid) copy16v(a.cache + d.off[t] + src, dst + norm_off + 1024 * wave);
+                ++n;
             }
         } else {
             // norm rows 2*wave, 2*wave+1 (row j < hpw: K norm of head h0+j, else V norm of head h0+j-hpw)
@@ -582,7 +609,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
             const uint32_t norm_src = nrow < hpw ? (uint32_t)(SL.k_norm + 4 * (h0 + nrow))
                                                  : (uint32_t)(SL.v_norm + 4 * (h0 + nrow - hpw));
             if (tl_copy < valid) copy4(a.cache + base + norm_src, dst + norm_off + 256 * wave);
+            ++n;
         }
+        return n;
     };
     // This wave's K (kind 0) or V (kind 1) norm of token t in stage sb.
     auto norm_at = [&](const uint8_t *sb, int kind, int t) {
@@ -603,6 +632,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         const uint32_t l16 = 16u * lane_now();
         for (int j = 0; j < G * 256; j += 1024)
             if (j + l16 < (uint32_t)(G * 256)) copy16(src, j + l16, dst + j);
+        return (G + 3) / 4;
     };
 
     // The codebook loads are compiler-visible: issued before the descriptor copies
@@ -613,7 +643,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         const int e = threadIdx.x & 15;
         cbv = threadIdx.x < 16 ? (e < a.nkc ? a.kc[e] : 0.f) : (e < a.nvc ? a.vc[e] : 0.f);
     }
-    for (int i = 0; i < min(nt, kRing); ++i) issue_desc(i);
+    for (int i = 0; i < min(nt, RING); ++i) issue_desc(i);
     wait_copies<0>();
     if (threadIdx.x < 32) cbarea[threadIdx.x] = cbv;
     __syncthreads();
@@ -682,35 +712,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     // registers), before the tile copies of the same iteration, so the wait for the
     // tile that starts the new segment also covers it.
     int q_upto = 0;
-    issue_q(__builtin_amdgcn_readfirstlane(ring[0].seq));
-    issue(0, stage0);
-    if (nt > 1) issue(1, stage1);
+    // Copy accounting (wave-uniform): cnt = copy instructions this wave issued since
+    // the prologue's wait; tend[k] = cnt just after the copies of tile t + k (k < NS)
+    // at the top of iteration t; qend = cnt just after the last query-operand copies.
+    int cnt = issue_q(__builtin_amdgcn_readfirstlane(ring[0].seq));
+    int qend = cnt;
+    int tend[NS];
+    #pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        if (k < nt) cnt += issue(k, lds + k * stage_bytes);
+        tend[k] = cnt;
+    }
+    // Most copies a wave can have in flight after the ones waited for: NS - 1 tiles,
+    // their descriptors and one query operand.
+    constexpr int kTileCopies = kLine ? 5 : (HPW > 0 ? (kTile + HPW - 1) / HPW + 1 : 12);
+    constexpr int kMaxInFlight = (NS - 1) * (kTileCopies + 1) + 4 < 63 ? (NS - 1) * (kTileCopies + 1) + 4 : 63;
 
+    int si = 0;  // stage of tile t (t % NS)
     for (int t = 0; t < nt; ++t) {
-        uint8_t *const sb = (t & 1) ? stage1 : stage0;
-        // Tile t landed?  Issued after its copies, and allowed to stay in flight:
-        // this wave's copies of tile t+1 (iteration t-1) and descriptor t+3 (wave 0,
-        // iteration t-1; the prologue issues descriptors 0..3 before tile 0).  The
-        // query operand copies of an iteration precede both.
-        if (HPW > 0 && t + 1 < nt) {
-            constexpr int HP = HPW > 0 ? HPW : 8, NPH = HP / 4;
-            const int v1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].valid);
-            // token copies tt = wave, wave + HPW, ... < v1; a norm copy on the waves < NPH
-            // (16-byte pieces, HPW >= 4) or on every wave (4-byte rows, HPW < 4; its lane
-            // of token 0 always copies)
-            // (line copies: instructions 4 wave + j, j < 4, whose first token is below v1)
-            constexpr int TPI = 8 / HP;
-            const int n_tok = kLine ? min(4, max(0, (v1 + TPI - 1) / TPI - 4 * wave))
-                                    : (v1 > wave ? (v1 - wave + HP - 1) / HP : 0);
-            const int n = n_tok + (HP >= 4 ? (wave < NPH ? 1 : 0) : 1) + (wave == 0 && t >= 1 && t + 3 < nt ? 1 : 0);
-            wait_copies_n<(kLine ? 4 : kTile / HP) + 2>(n);
-        } else {
-            wait_copies<0>();
+        uint8_t *const sb = lds + si * stage_bytes;
+        // Tile t landed?  The copies issued after tile t's (those of tiles t+1 ..
+        // t+NS-1, descriptors, a query operand) may stay in flight -- except the query
+        // operand of a segment that starts at tile t.
+        {
+            const int need = q_upto == t ? max(tend[0], qend) : tend[0];
+            wait_copies_upto<0, kMaxInFlight>(cnt - need);
         }
         __syncthreads();
 
-        const int tseq = __builtin_amdgcn_readfirstlane(ring[t % kRing].seq);
-        const int valid = __builtin_amdgcn_readfirstlane(ring[t % kRing].valid);
+        const int tseq = __builtin_amdgcn_readfirstlane(ring[t & (RING - 1)].seq);
+        const int valid = __builtin_amdgcn_readfirstlane(ring[t & (RING - 1)].valid);
         if (tseq != seq) {  // a new sequence starts at this tile
             if (seq >= 0) end_segment();
             seq = tseq;
@@ -830,22 +861,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         }
         __syncthreads();  // the stage and descriptor slot t are free once every wave holds its operands
 
-        // ---- next query operand, descriptor t+4 and tile t+2 -------------------------
+        // ---- next query operand, descriptor t+RING and tile t+NS ---------------------
         if (q_upto <= t && t + 1 < nt) {
-            const int s1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) % kRing].seq);
+            const int s1 = __builtin_amdgcn_readfirstlane(ring[(t + 1) & (RING - 1)].seq);
             if (s1 != seq) {
-                issue_q(s1);
+                cnt += issue_q(s1);
+                qend = cnt;
                 q_upto = t + 1;
             } else if (t + 2 < nt) {
-                const int s2 = __builtin_amdgcn_readfirstlane(ring[(t + 2) % kRing].seq);
+                const int s2 = __builtin_amdgcn_readfirstlane(ring[(t + 2) & (RING - 1)].seq);
                 if (s2 != s1) {
-                    issue_q(s2);
+                    cnt += issue_q(s2);
+                    qend = cnt;
                     q_upto = t + 2;
                 }
             }
         }
-        if (t + kRing < nt) issue_desc(t + kRing);
-        if (t + 2 < nt) issue(t + 2, sb);
+        if (t + RING < nt) cnt += issue_desc(t + RING);
+        if (t + NS < nt) cnt += issue(t + NS, sb);
+    #pragma unroll
+        for (int k = 0; k + 1 < NS; ++k) tend[k] = tend[k + 1];
+        tend[NS - 1] = cnt;
+        si = si + 1 == NS ? 0 : si + 1;
 
         // ---- S^T = K Q^T (exact products of the q-dtype values, fp32 sums) -----------
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
@@ -1032,9 +1069,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     reinterpret_cast<uint32_t *>(dst)[lane] = packed;
 }
 
-// Bound on decode workgroups per CU (sizes the partial slots).  One-wave workgroups
-// (one kv head: a tensor-parallel slice) timed the same at 4, 8 and 16 per CU.
-constexpr int kMaxWgPerCu = 4;
+// Bound on decode workgroups per CU.  One-wave workgroups (one kv head: a
+// tensor-parallel slice) take up to 8 per CU (TP-8 slice of config 1: 32.9 us
+// against 34.1 at 4 and 36.8 at 16, where the first copies of all workgroups become
+// one burst); both index layouts fit 8 of them in LDS, so they get the same grid and
+// the same result bit for bit.  Wider ones take at most 4 (two per CU at 8 kv heads,
+// by LDS).  The partial slots of the workspace are sized by the query heads alone
+// (the workspace query does not know the kv heads): 8 per CU when num_q_heads <= 16,
+// which covers every one-head launch (its query heads are its GQA group, <= 16);
+// otherwise 4.
+constexpr int decode_wg_cap(int hpw, int64_t num_q_heads) { return hpw == 1 && num_q_heads <= 16 ? 8 : 4; }
+constexpr int decode_slot_factor(int64_t num_q_heads) { return num_q_heads <= 16 ? 8 : 4; }
 
 // Resident decode workgroups per CU for an LDS size (cached per device and size;
 // the cache of each kernel instance is guarded by a mutex, so concurrent callers
@@ -1057,7 +1102,7 @@ static int decode_per_cu(const DecodeArgs &a, size_t lds) {
             hipSuccess ||
         nb <= 0)
         nb = 1;
-    nb = std::min(nb, kMaxWgPerCu);
+    nb = std::min(nb, decode_wg_cap(a.hpw, a.HQ));
     std::lock_guard<std::mutex> lock(mu);
     for (auto &e : cache[dev]) {
         if (e[0] == (int)lds && e[1] > 0) break;  // another caller stored it meanwhile
@@ -1127,7 +1172,7 @@ struct DecodeWorkspace {
     int64_t part_acc, part_ml, qops, descs, tile_prefix, n_tiles, total;
     DecodeWorkspace(int64_t num_seqs, int64_t num_q_heads, int64_t max_seq_len) {
         auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-        const int64_t slots = (int64_t)kMaxWgPerCu * device_cus() + num_seqs;
+        const int64_t slots = (int64_t)decode_slot_factor(num_q_heads) * device_cus() + num_seqs;
         const int64_t max_tiles = num_seqs * ((max_seq_len + kTile - 1) / kTile);
         part_acc = 0;
         part_ml = al(part_acc + slots * num_q_heads * kD * 4);
@@ -1333,8 +1378,10 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
     a.split_c = 1;
     a.wt[0] = a.wt[1] = a.wt[2] = a.wt[3] = 1;
     a.split_r = UINT64_MAX;
-    // two stages, the descriptor ring, the query slot and the two codebooks
-    const size_t lds = 2 * (size_t)a.stage_bytes + kRing * sizeof(TileDesc) + (size_t)a.hpw * a.G * 256 + 128;
+    // the stages, the descriptor ring, the query slot and the two codebooks (the
+    // kernel variant of this hpw and layout places them the same way)
+    const size_t lds = (size_t)decode_stages(a.hpw, dense3) * a.stage_bytes +
+                       (size_t)decode_ring(a.hpw, dense3) * sizeof(TileDesc) + (size_t)a.hpw * a.G * 256 + 128;
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
         if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, true);
