@@ -152,12 +152,19 @@ def time_decode(inp, steps, warmup, graphs=False):
                 graphs=bool(g_list), replay_matches_eager=exact), outs[0]
 
 
-def time_events(fn, steps, warmup=2):
-    """Average ms of `fn()` over `steps` calls bracketed by events on the current stream."""
+def time_events(fn, steps, warmup=2, warm_ms=30.0):
+    """Average ms of `fn()` over `steps` calls bracketed by events on the current stream,
+    after `warmup` calls and then further calls for at least `warm_ms` of wall time (the
+    per-call time of a process settles only after some tens of milliseconds of work)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(steps):
@@ -182,7 +189,7 @@ def decode_config(cfg, steps=10):
         inp = build_decode_inputs(lens, H=4, HQ=28, cfg=4, mode="iso", iso_mode="full", copies=1, kv="kscale",
                                   kv_dtype="bfloat16")
         H, HQ = 4, 28
-    t, _ = time_decode(inp, steps, 3)
+    t, _ = time_decode(inp, steps, 50)
     nb = decode_bytes(lens, H, HQ, 128, 16)
     gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
     out = dict(batch=len(lens), sum_ctx_tokens=int(sum(lens)), us=round(t["avg_ms"] * 1e3, 1), GBps=round(gbs, 1),
@@ -260,7 +267,7 @@ def decode_config1_dense3(steps=20):
     import torch
     lens = config1_lens()
     inp = build_decode_inputs(lens, dense3=True)
-    t, _ = time_decode(inp, steps, 5)
+    t, _ = time_decode(inp, steps, 100)
     nb = decode_bytes(lens, 8, 32, 128, 16, dense3=True)
     gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
     out = dict(us=round(t["avg_ms"] * 1e3, 1), algorithmic_bytes=int(nb), GBps=round(gbs, 1),
@@ -276,8 +283,9 @@ def decode_config1_tp8_slice(steps=20):
     no exchange).  GB/s on that slice's algorithmic bytes."""
     import torch
     lens = config1_lens()
-    inp = build_decode_inputs(lens, H=1, HQ=4)
-    t, _ = time_decode(inp, steps, 5)
+    # 8 rotated cache copies (8 x 41 MB): more than the 256 MB last-level cache holds
+    inp = build_decode_inputs(lens, H=1, HQ=4, copies=8)
+    t, _ = time_decode(inp, steps, 100)
     nb = decode_bytes(lens, 1, 4, 128, 16)
     gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
     out = dict(kv_heads=1, q_heads=4, us=round(t["avg_ms"] * 1e3, 1), algorithmic_bytes=int(nb), GBps=round(gbs, 1),
@@ -292,7 +300,9 @@ def unfused_call(inp, q, cu, max_q, paged_attention=False):
     decodes -> one rq_fused_decode call (max_seq_len = the block table's capacity, as the
     backend launches it); other queries of at most 16 tokens -> one rq_paged_attention
     call; longer ones -> one rq_paged_prefill call (workspaces allocated here, outside the
-    timed calls).  paged_attention=True: rq_paged_attention for the decodes too."""
+    timed calls).  paged_attention=True: rq_paged_attention for the decodes too.  Decode
+    calls rotate over the cache copies of `inp` (call i reads copy i % copies), so that
+    the last-level cache does not serve a step from the one before."""
     import torch
 
     from rotorquant_vllm import _lib
@@ -301,20 +311,23 @@ def unfused_call(inp, q, cu, max_q, paged_attention=False):
     kc, vc, R = p.kc.to(dev), p.vc.to(dev), p.R.to(dev)
     out = torch.empty_like(q)
     args = (q, inp["caches"][0], inp["bt"], inp["lens"], cu, max_q, kc, vc, R, inp["H"], 128, inp["BS"])
+    step = [0]
     if max_q == 1 and not paged_attention:
         cap = inp["bt"].shape[1] * inp["BS"]
         B = inp["lens"].shape[0]
         ws = torch.empty(_lib.load().rq_fused_decode_workspace_bytes(B, q.shape[1], 128, cap), dtype=torch.uint8,
                          device=dev)
-        launch = K.fused_paged_rq_decode_launcher(q, inp["caches"][0], inp["bt"], inp["lens"], kc, vc, R, inp["H"],
-                                                  128, inp["BS"], out=out, max_seq_len=cap, workspace=ws)
+        launches = [K.fused_paged_rq_decode_launcher(q, c, inp["bt"], inp["lens"], kc, vc, R, inp["H"], 128, inp["BS"],
+                                                     out=out, max_seq_len=cap, workspace=ws) for c in inp["caches"]]
 
         def fn():
-            launch()
+            launches[step[0] % len(launches)]()
+            step[0] += 1
         return fn
     if max_q <= 16:
         def fn():
-            K.paged_attention(*args, out=out)
+            K.paged_attention(q, inp["caches"][step[0] % len(inp["caches"])], *args[2:], out=out)
+            step[0] += 1
         return fn
     B = inp["lens"].shape[0]
     mx = int(inp["lens"].max())
@@ -333,7 +346,7 @@ def time_unfused(cfg, steps=5):
     import torch
     if cfg == 1:
         lens = config1_lens()
-        inp = build_decode_inputs(lens, copies=1)
+        inp = build_decode_inputs(lens)  # three cache copies, rotated
         B = len(lens)
         cu = torch.arange(B + 1, dtype=torch.int32, device="cuda")
         ms = time_events(unfused_call(inp, inp["q"], cu, 1), max(steps, 20))
@@ -402,13 +415,22 @@ def time_compress(n_tokens=32768, H=8, D=128, steps=20):
     p = Params("iso", 3, 3)
     BS = 16
     NB = n_tokens // BS + 8
-    cache = torch.zeros(NB, BS, 256 * H, dtype=torch.uint8, device=dev)
     slots = torch.randperm(NB * BS, generator=torch.Generator().manual_seed(5))[:n_tokens].to(dev)
     g = torch.Generator(device=dev).manual_seed(0)
-    k = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
-    v = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
-    args = (k, v, cache, slots, p.rte.to(dev), p.rto.to(dev), p.kb.to(dev), p.vb.to(dev))
-    ms = time_events(lambda: K.compress_store(*args, rot_block=4), steps, warmup=3)
+    # three input sets and caches, rotated (3 x 201 MB): the last-level cache (256 MB)
+    # does not serve a call's reads from the call before
+    sets = []
+    for _ in range(3):
+        cache = torch.zeros(NB, BS, 256 * H, dtype=torch.uint8, device=dev)
+        k = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
+        v = torch.randn(n_tokens, H, D, generator=g, device=dev).to(torch.float16)
+        sets.append((k, v, cache, slots, p.rte.to(dev), p.rto.to(dev), p.kb.to(dev), p.vb.to(dev)))
+    step = [0]
+
+    def call():
+        K.compress_store(*sets[step[0] % 3], rot_block=4)
+        step[0] += 1
+    ms = time_events(call, steps, warmup=3)
     alg = n_tokens * (2 * H * D * 2 + 136 * H + 8)
     gbs = alg / (ms * 1e-3) / 1e9
     return dict(tokens=n_tokens, us=round(ms * 1e3, 1), GBps=round(gbs, 1),
@@ -635,7 +657,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=10)
+    # 300 warm-up calls (~30 ms): the per-call time falls for the first ~100-300 calls
+    # of a process (config 1: ~105 us after 10 calls, ~89 from 300 calls on) and is
+    # flat after that (1000 calls: the same)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
