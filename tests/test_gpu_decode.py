@@ -100,6 +100,17 @@ def test_decode_tensor_parallel_slices(H, HQ):
     check(decode_case(14, 8, H, HQ, lens), f"tp-slice H={H} HQ={HQ}")
 
 
+@pytest.mark.parametrize("H,HQ,dtype", [(2, 32, torch.bfloat16), (1, 12, torch.bfloat16), (4, 40, torch.float16),
+                                         (3, 12, torch.bfloat16), (6, 12, torch.float16), (5, 40, torch.bfloat16)])
+def test_decode_head_layouts(H, HQ, dtype):
+    """Head layouts beyond the benchmark ones: GQA groups above 8 (two MFMAs per pair of
+    head dims; 16, 12 and 10 query heads per kv head) with one, two and four kv heads per
+    workgroup, and kv-head counts without a power-of-two divisor up to 8 (3, 6, 5 waves per
+    workgroup: the variant with the head count taken at run time)."""
+    lens = [1, 31, 33, 700, 2500]
+    check(decode_case(16 + H, len(lens), H, HQ, lens, dtype=dtype), f"heads H={H} HQ={HQ} {dtype}")
+
+
 @pytest.mark.parametrize("BS", [1, 12, 64, 128])
 def test_decode_block_sizes(BS):
     """Block sizes other than 16: one token per block, a non-power of two (division

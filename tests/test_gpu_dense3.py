@@ -78,10 +78,11 @@ def test_paged_decompress_dense_equals_nibble():
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("H,HQ", [(8, 32), (4, 28), (2, 16)])
+@pytest.mark.parametrize("H,HQ", [(8, 32), (4, 28), (2, 16), (2, 32), (3, 12)])
 def test_fused_decode_dense_equals_nibble(H, HQ):
-    """8, 4 and 2 kv heads: the three decode workgroup shapes (8 / 4 heads per
-    workgroup, and the generic one)."""
+    """8, 4, 2 and 3 kv heads: the decode workgroup shapes (8 / 4 / 2 heads per
+    workgroup and the one with the head count taken at run time), and a GQA group of
+    16 (two MFMAs per pair of head dims)."""
     from rotorquant_vllm import kernels as K
     p = Params("iso", 3, 3, iso_mode="full" if H == 4 else "fast")
     lens = [1, 17, 33, 1000, 4099, 64]
