@@ -27,7 +27,9 @@ __device__ __forceinline__ void store8(void *out, int64_t elem_off, const float 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             w[i] = Elem<DT>::from_f32(v[2 * i]) | (Elem<DT>::from_f32(v[2 * i + 1]) << 16);
-        *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + elem_off) = make_uint4(w[0], w[1], w[2], w[3]);
+        typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+        __builtin_nontemporal_store((u32x4_t){w[0], w[1], w[2], w[3]},
+                                    reinterpret_cast<u32x4_t *>(reinterpret_cast<uint16_t *>(out) + elem_off));
     }
 }
 
@@ -146,21 +148,42 @@ __global__ __launch_bounds__(256) void expand_kernel(const uint8_t *__restrict__
     SlotLayout L(H, D, dense3 != 0);
     // Rows are (component, token, head); a row has D / 8 packed dwords.  The launch
     // uses a multiple of D / 8 threads, so each thread keeps one dword position w and
-    // steps over rows: one division (by H) per row instead of three per dword.
+    // steps over rows: one division (by H) per row instead of three per dword.  The
+    // rows go in batches of kBatch per thread whose index and norm loads are all issued
+    // before any is used: one row at a time, every row waited out a full load latency.
+    constexpr int kBatch = 16;
     const int words = D / 8;
-    const int rows_per_comp = block_size * H;
+    const int rows_per_comp = block_size * H, nrows = 2 * rows_per_comp;
     const int w = threadIdx.x % words, rstep = blockDim.x / words;
-    for (int r = threadIdx.x / words; r < 2 * rows_per_comp; r += rstep) {
-        const int comp = r >= rows_per_comp ? 1 : 0;  // 0 = K, 1 = V
-        const int rr = r - comp * rows_per_comp;
-        const int tok = (int)((uint32_t)rr / (uint32_t)H), h = rr - tok * H;
-        const uint8_t *slot = cache + p * stride_block + (int64_t)tok * stride_token;
-        const uint32_t word = idx_dword(slot + (comp ? L.v_idx : L.k_idx) + h * L.ib, w, dense3 != 0);
-        float norm = *reinterpret_cast<const float *>(slot + (comp ? L.v_norm : L.k_norm) + 4 * h);
-        float v[8];
-        unpack8(word, comp ? cbv : cbk, norm, v);
-        int64_t off = (((c * block_size + tok) * H + h) * (int64_t)D) + w * 8;
-        store8<DT>(comp ? out_v : out_k, off, v);
+    for (int r0 = threadIdx.x / words; r0 < nrows; r0 += kBatch * rstep) {
+        uint32_t word[kBatch];
+        float norm[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int r = r0 + u * rstep;
+            word[u] = 0u;
+            norm[u] = 0.f;
+            if (r < nrows) {
+                const int comp = r >= rows_per_comp ? 1 : 0;  // 0 = K, 1 = V
+                const int rr = r - comp * rows_per_comp;
+                const int tok = (int)((uint32_t)rr / (uint32_t)H), h = rr - tok * H;
+                const uint8_t *slot = cache + p * stride_block + (int64_t)tok * stride_token;
+                word[u] = idx_dword(slot + (comp ? L.v_idx : L.k_idx) + h * L.ib, w, dense3 != 0);
+                norm[u] = *reinterpret_cast<const float *>(slot + (comp ? L.v_norm : L.k_norm) + 4 * h);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int r = r0 + u * rstep;
+            if (r < nrows) {
+                const int comp = r >= rows_per_comp ? 1 : 0;
+                const int rr = r - comp * rows_per_comp;
+                float v[8];
+                unpack8(word[u], comp ? cbv : cbk, norm[u], v);
+                const int64_t off = (c * rows_per_comp + rr) * (int64_t)D + w * 8;  // row (c, tok, h) of the output
+                store8<DT>(comp ? out_v : out_k, off, v);
+            }
+        }
     }
 }
 
