@@ -1,6 +1,6 @@
 """Benchmark: fused paged decode over the packed RotorQuant cache on one MI355X.
 
-Workload: Llama-3-8B attention-layer shape (32 query / 8 kv
+Workload (benchmark config 1): Llama-3-8B attention-layer shape (32 query / 8 kv
 heads, head_dim 128), IsoQuant fast 3-bit K and V, 64 sequences with context
 lengths uniform in [1024, 8192], block_size 16, seeded random block table; K/V
 drawn as N(0,1) * (1 + |N(0,3)|) per (head, channel) and pre-compressed into
@@ -175,7 +175,7 @@ def time_events(fn, steps, warmup=2, warm_ms=30.0):
 
 
 def decode_config(cfg, steps=10):
-    """Decode throughput on BASELINE config 2 (planar K4/V3, B 256, L log-uniform [2048, 32768])
+    """Decode throughput on benchmark config 2 (planar K4/V3, B 256, L log-uniform [2048, 32768])
     or the decode part of config 4 (Qwen2.5-7B layout, iso full 3-bit, 1 x 131072 + 127 x U[512, 16384])."""
     import torch
 
@@ -222,7 +222,7 @@ def causal_macs(q_lens, ctx_lens, HQ, D=128):
 
 
 def time_prefill_cfg3(steps=5):
-    """8 x 4096 new tokens, causal, 32 q / 8 kv, iso fast 4-bit, int8 MFMA.
+    """benchmark config 3: 8 x 4096 new tokens, causal, 32 q / 8 kv, iso fast 4-bit, int8 MFMA.
 
     Algorithmic int8 ops = 2 x (Q K^T + P V multiply-adds over the causal band);
     the kernel issues three int8 MFMAs per product (hi.hi, hi.lo, lo.hi parts),
@@ -244,7 +244,7 @@ def time_prefill_cfg3(steps=5):
 
 
 def time_mixed_cfg4(steps=5):
-    """BASELINE config 4's chunked-prefill part: 4 chunks of 2048 new tokens, each after a seeded
+    """benchmark config 4's chunked-prefill part: 4 chunks of 2048 new tokens, each after a seeded
     prefix of U{0..14336} cached tokens (Qwen2.5-7B layout, iso full 3-bit)."""
     import torch
     pre = torch.randint(0, 14336 + 1, (4,), generator=torch.Generator().manual_seed(4005)).tolist()
@@ -441,7 +441,7 @@ def time_compress(n_tokens=32768, H=8, D=128, steps=20):
 
 
 def config0_roundtrip(budget_s=10.0):
-    """2048 tokens x 8 kv heads x 128 of fp16 K and V, N(0,1) * (1 + |N(0,3)|)
+    """benchmark config 0: 2048 tokens x 8 kv heads x 128 of fp16 K and V, N(0,1) * (1 + |N(0,3)|)
     per (head, channel), iso fast 3-bit, one sequence of 128 blocks in a pool of 256
     (seeded permutation).  GPU: rq_compress_store into the cache, rq_paged_decompress back
     to fp16.  CPU baseline (reported, on the host cores): the reference's CPU fallback op
@@ -561,7 +561,7 @@ def cpu_baseline(inp, gpu_out, budget_s=15.0):
 
 
 def time_config4_one_forward(steps=5):
-    """BASELINE config 4 as ONE RQAttentionImpl.forward (RQ_USE_FUSED_PAGED=1): 128 decodes
+    """benchmark config 4 as ONE RQAttentionImpl.forward (RQ_USE_FUSED_PAGED=1): 128 decodes
     (1 x 131072 + 127 x U[512, 16384] context) then 4 chunks of 2048 tokens after prefixes
     U{0..14336}, Qwen2.5-7B layout (28 q / 4 kv), iso full 3-bit, bf16.  The call stores the
     132 + 8192 new tokens' K/V, runs the fused decode on the decodes and the int8 prefill on

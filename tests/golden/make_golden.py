@@ -134,7 +134,7 @@ def decompress_cpu(packed, norms, centroids, dtype):
 
 
 def config0_kv(n_tokens, seed_base, dtype=torch.float16):
-    """BASELINE config 0 values: N(0,1) * (1 + |N(0,3)|) per (head, channel)."""
+    """benchmark config 0 values: N(0,1) * (1 + |N(0,3)|) per (head, channel)."""
     out = []
     for stream in (0, 1):
         g = torch.Generator().manual_seed(seed_base + stream)

@@ -48,7 +48,7 @@ def test_compress_golden(mode, bits, name):
 @pytest.mark.parametrize("n_tokens", [2048, 32768])
 @pytest.mark.parametrize("mode,bits", [("iso", 3), ("iso", 4), ("planar", 4)])
 def test_compress_config0_full_size(n_tokens, mode, bits):
-    """BASELINE config 0 (2048 x 8 x 128 fp16, K and V) and a 32768-token run: bit-exact vs oracle."""
+    """benchmark config 0 (2048 x 8 x 128 fp16, K and V) and a 32768-token run: bit-exact vs oracle."""
     K = _kernels()
     p = Params(mode, bits, bits)
     pn = p.np()

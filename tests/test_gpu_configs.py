@@ -1,4 +1,4 @@
-"""GPU parity at the benchmark configurations' full sizes.
+"""GPU parity at the benchmark configurations' full sizes (benchmark configs 1-4).
 
 Each case builds its cache on the device with the library's compress kernel
 (bit-exact against the oracle in test_gpu_compress.py, up to 32768 tokens),

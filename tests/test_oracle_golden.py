@@ -1,7 +1,7 @@
 """Pin the CPU oracle and the init-time parameters (no GPU).
 
 * rq_oracle.c vs the golden vectors of the reference's CPU path (bit-exact).
-* rq_oracle.c vs the reference's torch op sequence at BASELINE config-0 size.
+* rq_oracle.c vs the reference's torch op sequence at benchmark config-0 size.
 * Lloyd-Max codebooks vs the scipy fixture, the closed form, and Max (1960).
 * Rotation parameters / matrices vs the fixture and quaternion algebra.
 """
@@ -55,7 +55,7 @@ def test_planted_mistake_is_caught():
 
 
 def test_oracle_matches_reference_ops_config0_full_size():
-    """2048 tokens x 8 heads x 128, K and V, iso fast 3-bit, vs the torch op sequence."""
+    """benchmark config 0: 2048 tokens x 8 heads x 128, K and V, iso fast 3-bit, vs the torch op sequence."""
     import make_golden as MG
 
     k, v = MG.config0_kv(2048, 0)
