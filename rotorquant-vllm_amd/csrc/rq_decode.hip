@@ -553,8 +553,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
     // Descriptor of local tile i -> ring slot i % RING (wave 0, one copy).  Each
     // issue function returns the number of copy instructions this wave issued.
     auto issue_desc = [&](int i) {
-        if (wave == 0 && lane < kDescPieces)
-            copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * lane, lds_addr(reinterpret_cast<const uint8_t *>(ring + (i & (RING - 1)))));
+        const uint32_t l = lane_now();  // rebuilt here, not kept live across the loop
+        if (wave == 0 && l < (uint32_t)kDescPieces)
+            copy16(reinterpret_cast<const uint8_t *>(a.descs + k0 + i), 16 * l, lds_addr(reinterpret_cast<const uint8_t *>(ring + (i & (RING - 1)))));
         return wave == 0 ? 1 : 0;
     };
     // Copies of local tile i into stage sb.  Per wave and full tile: kTile / hpw
@@ -735,8 +736,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
         // t+NS-1, descriptors, a query operand) may stay in flight -- except the query
         // operand of a segment that starts at tile t.
         {
+            // (the count is wave-uniform: read into a scalar register, the search over
+            // the immediates is scalar compares and branches, not VALU compares and exec masks)
             const int need = q_upto == t ? max(tend[0], qend) : tend[0];
-            wait_copies_upto<0, kMaxInFlight>(cnt - need);
+            wait_copies_upto<0, kMaxInFlight>(__builtin_amdgcn_readfirstlane(cnt - need));
         }
         __syncthreads();
 
