@@ -277,6 +277,23 @@ def decode_config1_dense3(steps=20):
     return out
 
 
+def decode_config1_4bit(steps=20):
+    """Config 1's decode batch with 4-bit K and V (RQ_BITS=4, iso fast): the same
+    nibble layout and bytes as the headline line (the bits change only the
+    codebooks), with 16-entry lookups instead of 8."""
+    import torch
+    lens = config1_lens()
+    inp = build_decode_inputs(lens, k_bits=4, v_bits=4)
+    t, _ = time_decode(inp, steps, 100)
+    nb = decode_bytes(lens, 8, 32, 128, 16)
+    gbs = nb / (t["avg_ms"] * 1e-3) / 1e9
+    out = dict(k_bits=4, v_bits=4, us=round(t["avg_ms"] * 1e3, 1), algorithmic_bytes=int(nb), GBps=round(gbs, 1),
+               pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 2), decode_tok_per_s=round(len(lens) / (t["avg_ms"] * 1e-3), 1))
+    del inp
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_config1_tp8_slice(steps=20):
     """One GPU's share of config 1 under tensor parallelism 8: the same 64 sequences
     with 1 kv head and 4 query heads (the layout a TP-8 rank holds; attention needs
@@ -665,7 +682,7 @@ def main():
     ap.add_argument("--no-compress", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2/3/4 side measurements")
     ap.add_argument("--only", choices=["compress", "prefill3", "decode2", "decode4", "prefill4", "paged_decompress",
-                                       "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3",
+                                       "config0", "config4_forward", "unfused1", "unfused3", "decode1_dense3", "decode1_4bit",
                                        "hbm_probe", "decode1_tp8"],
                     help="run one side measurement alone and print its JSON (for profiling)")
     ap.add_argument("--graphs", action="store_true", help="replay HIP graphs of the decode call instead of direct launches")
@@ -691,7 +708,7 @@ def main():
               "paged_decompress": lambda: time_paged_decompress(build_decode_inputs(config1_lens(), copies=1)),
               "config0": config0_roundtrip, "config4_forward": time_config4_one_forward,
               "unfused1": lambda: time_unfused(1), "unfused3": lambda: time_unfused(3),
-              "decode1_dense3": decode_config1_dense3, "hbm_probe": hbm_read_probe,
+              "decode1_dense3": decode_config1_dense3, "decode1_4bit": decode_config1_4bit, "hbm_probe": hbm_read_probe,
               "decode1_tp8": decode_config1_tp8_slice}[args.only]
         print(json.dumps({"only": args.only, **fn()}), flush=True)
         return
@@ -751,6 +768,7 @@ def main():
         result["prefill_config4_chunks"] = time_mixed_cfg4()
         result["config4_one_forward"] = time_config4_one_forward()
         result["decode_config1_dense3"] = decode_config1_dense3()
+        result["decode_config1_4bit"] = decode_config1_4bit()
         result["decode_config1_tp8_slice"] = decode_config1_tp8_slice()
         result["unfused_config1_decode"] = time_unfused(1)
         result["unfused_config3_prefill"] = time_unfused(3)

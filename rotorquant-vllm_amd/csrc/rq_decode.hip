@@ -1369,6 +1369,11 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
             a.hpw = d;
             break;
         }
+    // 4-bit V: the 16-entry lookups need more registers than 128 (no cap: 140-150 VGPRs,
+    // one 8-wave workgroup per CU) or spill at 128; four-head workgroups fit three per
+    // CU instead (config-1 shape, mean per call: V4/K4 143.8 -> 130.3 us, V4/K3 122.4 ->
+    // 115.2; 3-bit V keeps eight heads: 88.5 against 100.9 us at four).
+    if (n_v_centroids == 16 && a.hpw == 8) a.hpw = 4;
     // token stride in a stage: 128 bytes per head, unpadded (swizzled) for one or two heads
     // per workgroup in the nibble layout; else the index runs plus a 16-byte skew
     a.tok_stride = (a.hpw <= 2 && !dense3) ? 128 * a.hpw : 2 * SlotLayout(num_kv_heads, head_dim, dense3).ib * a.hpw + 16;

@@ -119,6 +119,14 @@ def test_decode_block_sizes(BS):
     check(decode_case(15, len(lens), 8, 32, lens, block_size=BS), f"bs{BS}")
 
 
+@pytest.mark.parametrize("mode", ["iso", "planar"])
+def test_decode_4bit_kv_config1_heads(mode):
+    """RQ_BITS=4 on the config-1 head layout (32 q / 8 kv heads): 4-bit V takes
+    workgroups of four kv heads (two per kv-head set), with 16-entry K and V tables."""
+    lens = [1, 33, 700, 2500, 8000, 4096]
+    check(decode_case(21, len(lens), 8, 32, lens, p=Params(mode, 4, 4)), f"4bit {mode}")
+
+
 def test_decode_k3_v4_and_block_size_32():
     p = Params("iso", 3, 4)
     lens = [700, 33, 64]
