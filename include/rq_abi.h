@@ -34,9 +34,9 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 6  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
+#define RQ_ABI_VERSION 7  /* 2: rq_int8_prefill takes max_seq_len and a workspace; 3: rq_fused_decode_noalloc;
                               4: rq_paged_attention; 5: index_layout on the entry points that touch slots;
-                              6: rq_paged_prefill */
+                              6: rq_paged_prefill; 7: rq_fused_decode_timed */
 
 enum rq_status {
     RQ_OK = 0,
@@ -207,6 +207,28 @@ int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_
                     const float *rotation, int32_t rot_block, float sm_scale,
                     void *out, int64_t out_stride_seq, int64_t out_stride_head,
                     void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * rq_fused_decode that also records event_start and event_stop (hipEvent_t,
+ * created by the caller, or NULL) at the start and the end of its decode
+ * kernel -- the kernel that streams the cache -- rather than around the whole
+ * call, so hipEventElapsedTime gives that kernel's own duration (measurement:
+ * the roofline of the dominant kernel).  No counterpart in the reference.
+ * Everything else, results included, is as for rq_fused_decode.
+ */
+int rq_fused_decode_timed(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                          int64_t q_stride_seq, int64_t q_stride_head,
+                          const uint8_t *kv_cache, int64_t num_blocks, int32_t block_size,
+                          int64_t stride_block, int64_t stride_token,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t index_layout,
+                          const int32_t *block_table, int64_t max_blocks, int64_t bt_stride_seq,
+                          const int32_t *seq_lens, int64_t max_seq_len,
+                          const float *k_centroids, int32_t n_k_centroids,
+                          const float *v_centroids, int32_t n_v_centroids,
+                          const float *rotation, int32_t rot_block, float sm_scale,
+                          void *out, int64_t out_stride_seq, int64_t out_stride_head,
+                          void *workspace, int64_t workspace_bytes, void *stream,
+                          void *event_start, void *event_stop);
 
 /*
  * rq_fused_decode without a workspace argument, for callers that cannot

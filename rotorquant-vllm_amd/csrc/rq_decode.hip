@@ -41,6 +41,8 @@
 #include <algorithm>
 #include <mutex>
 
+#include <hip/hip_ext.h>
+
 #include "rq_common.h"
 
 namespace rq {
@@ -1118,13 +1120,22 @@ static int decode_per_cu(const DecodeArgs &a, size_t lds) {
     return nb;
 }
 
+// Events recorded at the decode kernel's own start and end (rq_fused_decode_timed), or none.
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
 // configure: set the grid and range split only (before the prep kernel, which
 // needs them); otherwise launch.
 template <int DT, int KB, int VB, int HPW, bool D3, bool WIDE>
-static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
+static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool configure, KernelEvents ev) {
     if (!configure) {
-        hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3, WIDE>), dim3((unsigned)a.grid_w, 1, a.H / a.hpw),
-                           dim3(64 * a.hpw), lds, st, a);
+        const dim3 grid((unsigned)a.grid_w, 1, a.H / a.hpw), block(64 * a.hpw);
+        if (ev.start != nullptr || ev.stop != nullptr)  // events at this kernel's own start and end
+            hipExtLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3, WIDE>), grid, block, lds, st, ev.start, ev.stop, 0,
+                                  a);
+        else
+            hipLaunchKernelGGL((decode_kernel<DT, KB, VB, HPW, D3, WIDE>), grid, block, lds, st, a);
         return;
     }
     // as many workgroups per kv-head group as are resident at once
@@ -1146,28 +1157,28 @@ static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool conf
 }
 
 template <int DT, int KB, int VB, bool D3, bool WIDE>
-static void launch_decode_w(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
-    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3, WIDE>(a, lds, st, configure);
-    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3, WIDE>(a, lds, st, configure);
-    else if (a.hpw == 2) launch_decode_h<DT, KB, VB, 2, D3, WIDE>(a, lds, st, configure);
-    else if (a.hpw == 1) launch_decode_h<DT, KB, VB, 1, D3, WIDE>(a, lds, st, configure);
-    else launch_decode_h<DT, KB, VB, 0, D3, WIDE>(a, lds, st, configure);
+static void launch_decode_w(DecodeArgs &a, size_t lds, hipStream_t st, bool configure, KernelEvents ev) {
+    if (a.hpw == 8) launch_decode_h<DT, KB, VB, 8, D3, WIDE>(a, lds, st, configure, ev);
+    else if (a.hpw == 4) launch_decode_h<DT, KB, VB, 4, D3, WIDE>(a, lds, st, configure, ev);
+    else if (a.hpw == 2) launch_decode_h<DT, KB, VB, 2, D3, WIDE>(a, lds, st, configure, ev);
+    else if (a.hpw == 1) launch_decode_h<DT, KB, VB, 1, D3, WIDE>(a, lds, st, configure, ev);
+    else launch_decode_h<DT, KB, VB, 0, D3, WIDE>(a, lds, st, configure, ev);
 }
 
 template <int DT, int KB, int VB, bool D3 = false>
-static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st, bool configure) {
-    if (a.G > 8) launch_decode_w<DT, KB, VB, D3, true>(a, lds, st, configure);
-    else launch_decode_w<DT, KB, VB, D3, false>(a, lds, st, configure);
+static void launch_decode(DecodeArgs &a, size_t lds, hipStream_t st, bool configure, KernelEvents ev) {
+    if (a.G > 8) launch_decode_w<DT, KB, VB, D3, true>(a, lds, st, configure, ev);
+    else launch_decode_w<DT, KB, VB, D3, false>(a, lds, st, configure, ev);
 }
 
 template <int DT>
 static void launch_decode_bits(DecodeArgs &a, size_t lds, int kb, int vb, bool dense3, hipStream_t st,
-                               bool configure) {
-    if (dense3) launch_decode<DT, 3, 3, true>(a, lds, st, configure);  // the layout holds 3-bit indices only
-    else if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st, configure);
-    else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st, configure);
-    else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st, configure);
-    else launch_decode<DT, 4, 4>(a, lds, st, configure);
+                               bool configure, KernelEvents ev) {
+    if (dense3) launch_decode<DT, 3, 3, true>(a, lds, st, configure, ev);  // the layout holds 3-bit indices only
+    else if (kb == 3 && vb == 3) launch_decode<DT, 3, 3>(a, lds, st, configure, ev);
+    else if (kb == 3) launch_decode<DT, 3, 4>(a, lds, st, configure, ev);
+    else if (vb == 3) launch_decode<DT, 4, 3>(a, lds, st, configure, ev);
+    else launch_decode<DT, 4, 4>(a, lds, st, configure, ev);
 }
 
 // Workspace layout (256-byte aligned regions).
@@ -1206,7 +1217,7 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
                              const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                              int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
                              void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
-                             int64_t workspace_bytes, void *stream);
+                             int64_t workspace_bytes, void *stream, KernelEvents ev = {});
 
 extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
                                int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
@@ -1224,6 +1235,26 @@ extern "C" int rq_fused_decode(const void *q, int32_t dtype, int64_t num_seqs, i
                              bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids, v_centroids,
                              n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq, out_stride_head,
                              workspace, workspace_bytes, stream);
+}
+
+extern "C" int rq_fused_decode_timed(const void *q, int32_t dtype, int64_t num_seqs, int32_t num_q_heads,
+                                     int64_t q_stride_seq, int64_t q_stride_head, const uint8_t *kv_cache,
+                                     int64_t num_blocks, int32_t block_size, int64_t stride_block,
+                                     int64_t stride_token, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t index_layout, const int32_t *block_table, int64_t max_blocks,
+                                     int64_t bt_stride_seq, const int32_t *seq_lens, int64_t max_seq_len,
+                                     const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
+                                     int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
+                                     void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
+                                     int64_t workspace_bytes, void *stream, void *event_start, void *event_stop) {
+    KernelEvents ev;
+    ev.start = (hipEvent_t)event_start;
+    ev.stop = (hipEvent_t)event_stop;
+    return fused_decode_impl(q, dtype, num_seqs, num_q_heads, q_stride_seq, q_stride_head, kv_cache, num_blocks,
+                             block_size, stride_block, stride_token, num_kv_heads, head_dim, index_layout, block_table,
+                             max_blocks, bt_stride_seq, seq_lens, max_seq_len, k_centroids, n_k_centroids,
+                             v_centroids, n_v_centroids, rotation, rot_block, sm_scale, out, out_stride_seq,
+                             out_stride_head, workspace, workspace_bytes, stream, ev);
 }
 
 // ---------------------------------------------------------------------------
@@ -1302,7 +1333,7 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
                              const float *k_centroids, int32_t n_k_centroids, const float *v_centroids,
                              int32_t n_v_centroids, const float *rotation, int32_t rot_block, float sm_scale,
                              void *out, int64_t out_stride_seq, int64_t out_stride_head, void *workspace,
-                             int64_t workspace_bytes, void *stream) {
+                             int64_t workspace_bytes, void *stream, KernelEvents ev) {
     RQ_CHECK_ARG(dtype == RQ_DTYPE_BF16 || dtype == RQ_DTYPE_F16, "decode dtype must be f16 or bf16");
     RQ_CHECK_ARG(head_dim == kD, "head_dim %d unsupported (only %d)", head_dim, kD);
     RQ_CHECK_ARG(num_kv_heads >= 1 && num_kv_heads <= kMaxKvHeads, "num_kv_heads %d must be 1..%d", num_kv_heads,
@@ -1392,8 +1423,8 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
                        (size_t)decode_ring(a.hpw, dense3) * sizeof(TileDesc) + (size_t)a.hpw * a.G * 256 + 128;
     int kb = n_k_centroids == 8 ? 3 : 4, vb = n_v_centroids == 8 ? 3 : 4;
     if (a.max_len > 0) {
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, true);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, true);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, true, {});
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, true, {});
         // Descriptor workgroups per sequence (y >= 1): enough that each thread writes at
         // most two steps of four tokens of the longest sequence (a fixed three made the
         // prep kernel of a 131072-token sequence take ~49 us).
@@ -1406,8 +1437,8 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
         else hipLaunchKernelGGL(decode_prep_kernel<RQ_DTYPE_F16>, pgrid, pblock, plds, st, a);
         int rc = check_launch("decode_prep_kernel");
         if (rc) return rc;
-        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, false);
-        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, false);
+        if (dtype == RQ_DTYPE_BF16) launch_decode_bits<RQ_DTYPE_BF16>(a, lds, kb, vb, dense3, st, false, ev);
+        else launch_decode_bits<RQ_DTYPE_F16>(a, lds, kb, vb, dense3, st, false, ev);
         rc = check_launch("decode_kernel");
         if (rc) return rc;
     }

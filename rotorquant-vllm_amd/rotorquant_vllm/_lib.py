@@ -36,6 +36,10 @@ _SIGNATURES = {
     "rq_fused_decode": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64, _c_i64,
                                  _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i32, _c_p,
                                  _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
+    "rq_fused_decode_timed": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64,
+                                       _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
+                                       _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p,
+                                       _c_i64, _c_p, _c_p, _c_p]),
     "rq_fused_decode_noalloc": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i64,
                                          _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
                                          _c_i32, _c_p, _c_i32, _c_p, _c_i32, _c_f32, _c_p, _c_i64, _c_i64, _c_p]),

@@ -359,20 +359,31 @@ def fused_paged_rq_decode_launcher(q: torch.Tensor, kv_cache: torch.Tensor, bloc
                                    rotation: torch.Tensor, num_kv_heads: int, head_dim: int, block_size: int,
                                    sm_scale: float | None = None, out: torch.Tensor | None = None,
                                    max_seq_len: int | None = None, workspace: torch.Tensor | None = None,
-                                   dense3: bool = False):
+                                   dense3: bool = False, kernel_events=None):
     """Validate once and return a zero-argument callable that re-issues the same
     rq_fused_decode call (same buffers, the stream current now) without
     per-call Python work -- for loops over static buffers such as a benchmark.
-    The callable returns `out`; the tensors must outlive it."""
+    The callable returns `out`; the tensors must outlive it.
+
+    kernel_events: optional (start, stop) torch.cuda.Event pair (enable_timing=True)
+    recorded at the start and the end of the call's decode kernel alone
+    (rq_fused_decode_timed), for measuring that kernel's own duration."""
     L, args, out, keep = _fused_decode_call(q, kv_cache, block_table, seq_lens, centroids_k, centroids_v, rotation,
                                             num_kv_heads, head_dim, block_size, sm_scale, out, max_seq_len, workspace,
                                             dense3)
-    fn = L.rq_fused_decode
+    fn, name = L.rq_fused_decode, "rq_fused_decode"
+    if kernel_events is not None:
+        for ev in kernel_events:
+            if not ev.cuda_event:  # torch creates the HIP event at its first record
+                ev.record()
+        args = args + tuple(ev._as_parameter_ for ev in kernel_events)
+        fn, name = L.rq_fused_decode_timed, "rq_fused_decode_timed"
+        keep = keep + tuple(kernel_events)
 
     def launch():
         rc = fn(*args)
         if rc:
-            _lib.check(rc, "rq_fused_decode")
+            _lib.check(rc, name)
         return out
 
     launch.keep = keep

@@ -179,6 +179,34 @@ def test_decode_deterministic_and_batch_consistent():
     assert excess <= 0 and cs >= 0.9999
 
 
+def test_decode_timed_entry_point():
+    """rq_fused_decode_timed gives rq_fused_decode's output bit for bit and records
+    its events around the decode kernel: a positive time, shorter than the whole
+    call timed by events on the stream around it."""
+    from rotorquant_vllm import kernels as K
+    lens = [3000, 700, 5000, 64]
+    case = decode_case(22, 4, 8, 32, lens)
+    p = case["p"]
+    dev = torch.device("cuda")
+    args = (case["q"].to(dev), torch.from_numpy(case["cache"]).to(dev), torch.from_numpy(case["bt"]).to(dev),
+            torch.from_numpy(case["lens"]).to(dev), p.kc.to(dev), p.vc.to(dev), p.R.to(dev), 8, 128, 16)
+    plain = K.fused_paged_rq_decode_launcher(*args, sm_scale=case["sm_scale"])
+    ref = plain().clone()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timed = K.fused_paged_rq_decode_launcher(*args, sm_scale=case["sm_scale"], kernel_events=(k0, k1))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        c0.record()
+        got = timed()
+        c1.record()
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+        t_kernel, t_call = k0.elapsed_time(k1), c0.elapsed_time(c1)
+        print(f"decode kernel {t_kernel * 1e3:.1f} us, call {t_call * 1e3:.1f} us")
+        assert 0 < t_kernel < t_call
+
+
 def test_decode_graph_replay_matches_eager():
     """rq_fused_decode captured in a HIP graph: each of several replays, with eager
     calls on other inputs in between, reproduces the eager result bit for bit."""

@@ -84,7 +84,7 @@ class TestABI:
         assert set(syms) == set(_lib.EXPORTED)
 
     def test_version(self):
-        assert _lib.load().rq_abi_version() == 6
+        assert _lib.load().rq_abi_version() == 7
 
     def test_argument_validation_without_gpu(self):
         """Bad arguments are rejected before any device work, with a message."""
