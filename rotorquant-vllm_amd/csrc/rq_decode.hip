@@ -40,6 +40,7 @@
 // With more heads (WIDE), two MFMAs per pair, (p, 0) and (0, p).
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include <hip/hip_ext.h>
 
@@ -992,14 +993,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_wave
 // rotate back by R in fp32 and round again (:308).  One wave per query head,
 // two head dims per lane; per pass of kMergePass segments, the (m, l) of each segment
 // and the lane's accumulator entries of all of them are loaded together.
-template <int DT, int kMergePass>
+// kSplit == 1: a workgroup holds up to four query heads, one wave each.  kSplit > 1
+// (few (sequence, head) pairs, each with many segments): the kSplit waves of a
+// workgroup share one query head, wave i taking segment passes i, i + kSplit, ...,
+// and wave 0 combines their (max, sum, accumulator) states through LDS -- one
+// round of loads instead of a chain of passes, on kSplit times as many waves.
+template <int DT, int kMergePass, int kSplit>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+    static_assert(kSplit == 1 || kSplit == 4, "one wave per head, or four (the 256-thread block)");
     const int64_t seq = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hq = blockIdx.x * (blockDim.x >> 6) + wave;
+    const int hq = kSplit == 1 ? blockIdx.x * (blockDim.x >> 6) + wave : blockIdx.x;
+    const int share = kSplit == 1 ? 0 : wave;  // first segment pass of this wave
     __shared__ float orot_all[4][kD];
     float *orot = orot_all[wave];
-    if (hq >= a.HQ) return;
+    if (hq >= a.HQ) return;  // (kSplit > 1: the whole workgroup or none of it)
     // R entries for this lane's two output dims (issued first; independent of the partials)
     float rr[2][4];
     #pragma unroll
@@ -1007,7 +1015,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         const int d = 2 * lane + e;
         const int k0 = (d / a.rot_block) * a.rot_block;
     #pragma unroll
-        for (int i = 0; i < 4; ++i) rr[e][i] = i < a.rot_block ? a.R[(k0 + i) * kD + d] : 0.f;
+        for (int i = 0; i < 4; ++i) rr[e][i] = i < a.rot_block && share == 0 ? a.R[(k0 + i) * kD + d] : 0.f;
     }
     // Workgroups whose tile ranges cover the sequence (found by the prep kernel):
     // partials sit at slots w + seq for w in [w_lo, w_lo + nch); workgroups with an
@@ -1026,7 +1034,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const float *pa = a.part_acc + (w_lo + seq) * (int64_t)a.HQ * kD + hq * kD;
     const int64_t cs_ml = (int64_t)a.HQ * 2, cs_acc = (int64_t)a.HQ * kD;
     float lsum = 0.f, o0 = 0.f, o1 = 0.f, M = -INFINITY;
-    for (int c0 = 0; c0 < nch; c0 += kMergePass) {
+    for (int c0 = share * kMergePass; c0 < nch; c0 += kSplit * kMergePass) {
         // lane c (< kMergePass) loads segment c0 + c's (m, l); every lane loads its two
         // dims of up to kMergePass segments' accumulators -- all issued before any is used
         const int c = c0 + (lane & (kMergePass - 1));
@@ -1041,7 +1049,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         for (int o = kMergePass / 2; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
         pm = __shfl(pm, 0);
         const float Mn = fmaxf(M, pm);
-        const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // -inf - finite -> 0 on the first pass
+        // -inf - finite -> 0 on the first pass; 1 while every segment seen has an empty
+        // range (M = Mn = -inf: a wave whose passes begin among such segments)
+        const float alpha = M == Mn ? 1.f : __builtin_amdgcn_exp2f(M - Mn);
         o0 *= alpha;
         o1 *= alpha;
         lsum *= alpha;
@@ -1055,6 +1065,32 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
             const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
             o0 += wu * x[u].x;
             o1 += wu * x[u].y;
+        }
+    }
+    if constexpr (kSplit > 1) {
+        // each wave's state relative to its own max M_i (-inf, sum 0, accumulator 0 for a
+        // wave without segments); wave 0 rescales them to the overall max and adds them up
+        __shared__ float2 st_acc[kSplit][kD / 2];
+        __shared__ float2 st_ml[kSplit];
+        st_acc[wave][lane] = make_float2(o0, o1);
+        if (lane == 0) st_ml[wave] = make_float2(M, lsum);
+        __syncthreads();
+        if (wave != 0) return;
+        float2 ml[kSplit];
+        float Mt = -INFINITY;
+    #pragma unroll
+        for (int i = 0; i < kSplit; ++i) {
+            ml[i] = st_ml[i];
+            Mt = fmaxf(Mt, ml[i].x);
+        }
+        lsum = o0 = o1 = 0.f;
+    #pragma unroll
+        for (int i = 0; i < kSplit; ++i) {
+            const float f = ml[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[i].x - Mt);
+            const float2 x = st_acc[i][lane];
+            lsum += f * ml[i].y;
+            o0 += f * x.x;
+            o1 += f * x.y;
         }
     }
     const float inv = nch > 0 ? 1.f / lsum : 0.f;  // empty context -> zeros (reference: acc 0, l 1)
@@ -1445,17 +1481,25 @@ static int fused_decode_impl(const void *q, int32_t dtype, int64_t num_seqs, int
     // One wave per (sequence, query head): four per workgroup, or one when the batch has
     // few (sequence, head) pairs, so that they spread over all CUs.
     const int mw = num_seqs * (int64_t)num_q_heads >= 4LL * device_cus() ? 4 : 1;
-    dim3 mgrid((num_q_heads + mw - 1) / mw, (unsigned)num_seqs), mblock(64 * mw);
+    // Few pairs whose sequences span many decode workgroups each (at least 8 on
+    // average: a tensor-parallel slice, a small batch of long contexts): four waves
+    // per pair, each taking every fourth segment pass.
+    const bool split = mw == 1 && a.grid_w >= 8 * num_seqs;
+    dim3 mgrid(split ? num_q_heads : (num_q_heads + mw - 1) / mw, (unsigned)num_seqs), mblock(64 * (split ? 4 : mw));
     // 32-segment passes when a sequence may span many decode workgroups (very long
     // contexts), or when all merge waves fit at once at the lower occupancy
-    // (3 per SIMD); otherwise 16 (config 2: 8192 short merges).
-    const bool wide = a.max_len >= 65536 || num_seqs * (int64_t)num_q_heads <= 12LL * device_cus();
-    if (dtype == RQ_DTYPE_BF16) {
-        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 32>), mgrid, mblock, 0, st, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_BF16, 16>), mgrid, mblock, 0, st, a);
-    } else {
-        if (wide) hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 32>), mgrid, mblock, 0, st, a);
-        else hipLaunchKernelGGL((decode_merge_kernel<RQ_DTYPE_F16, 16>), mgrid, mblock, 0, st, a);
-    }
+    // (3 per SIMD); otherwise 16 (config 2: 8192 short merges).  Split merges take
+    // 16 while the four waves' first passes cover the average sequence's segments.
+    const bool wide = split ? a.grid_w >= 48 * num_seqs
+                            : a.max_len >= 65536 || num_seqs * (int64_t)num_q_heads <= 12LL * device_cus();
+    auto launch_merge = [&](auto dt) {
+        constexpr int DT = decltype(dt)::value;
+        if (split && wide) hipLaunchKernelGGL((decode_merge_kernel<DT, 32, 4>), mgrid, mblock, 0, st, a);
+        else if (split) hipLaunchKernelGGL((decode_merge_kernel<DT, 16, 4>), mgrid, mblock, 0, st, a);
+        else if (wide) hipLaunchKernelGGL((decode_merge_kernel<DT, 32, 1>), mgrid, mblock, 0, st, a);
+        else hipLaunchKernelGGL((decode_merge_kernel<DT, 16, 1>), mgrid, mblock, 0, st, a);
+    };
+    if (dtype == RQ_DTYPE_BF16) launch_merge(std::integral_constant<int, RQ_DTYPE_BF16>{});
+    else launch_merge(std::integral_constant<int, RQ_DTYPE_F16>{});
     return check_launch("decode_merge_kernel");
 }

@@ -100,6 +100,16 @@ def test_decode_tensor_parallel_slices(H, HQ):
     check(decode_case(14, 8, H, HQ, lens), f"tp-slice H={H} HQ={HQ}")
 
 
+def test_decode_tp8_slice_many_sequences():
+    """The TP-8 slice's head layout (1 kv / 4 q heads) with 64 short sequences: each
+    sequence spans ~32 one-wave decode workgroups, and the merge gives each (sequence,
+    query head) four waves that take every fourth 16-segment pass (most of them with
+    empty ranges here: 64 sequences of 1..400 tokens hold far fewer tiles than there
+    are workgroups)."""
+    lens = lens_uniform(64, 1, 400, cfg=23)
+    check(decode_case(23, len(lens), 1, 4, lens), "tp8-many")
+
+
 @pytest.mark.parametrize("H,HQ,dtype", [(2, 32, torch.bfloat16), (1, 12, torch.bfloat16), (4, 40, torch.float16),
                                          (3, 12, torch.bfloat16), (6, 12, torch.float16), (5, 40, torch.bfloat16)])
 def test_decode_head_layouts(H, HQ, dtype):
