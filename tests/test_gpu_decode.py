@@ -110,6 +110,14 @@ def test_decode_tp8_slice_many_sequences():
     check(decode_case(23, len(lens), 1, 4, lens), "tp8-many")
 
 
+@pytest.mark.parametrize("H,HQ,lens", [(2, 8, [60000, 3000, 1]), (1, 4, [40000])])
+def test_decode_long_context_few_sequences(H, HQ, lens):
+    """A long context in a small batch: the sequence spans ~1000 two-wave or ~2000
+    one-wave decode workgroups, so each of the four merge waves of a (sequence, head)
+    pair runs several 32-segment passes before their states are combined."""
+    check(decode_case(24 + H, len(lens), H, HQ, lens), f"long-few H={H} lens={lens}")
+
+
 @pytest.mark.parametrize("H,HQ,dtype", [(2, 32, torch.bfloat16), (1, 12, torch.bfloat16), (4, 40, torch.float16),
                                          (3, 12, torch.bfloat16), (6, 12, torch.float16), (5, 40, torch.bfloat16)])
 def test_decode_head_layouts(H, HQ, dtype):
