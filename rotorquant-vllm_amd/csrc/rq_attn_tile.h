@@ -89,19 +89,35 @@ __device__ __forceinline__ void rotate_q8(const float *xin, int base, const floa
 
 // Work item of a workgroup in a grid (query blocks, kv heads, sequences).
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.
-// When the (sequence, kv head) pairs divide into 8, XCD j takes pairs j, j + 8,
-// ... one after another, so all query blocks that stream one pair's keys share
-// one L2; within a pair the last (heaviest) query blocks go first.  Any other
-// grid keeps the plain order.  Both are bijections of the grid onto
-// (query block, kv head, sequence).
+// Each (sequence, kv head) pair's query blocks are cut into S slices (S = 8 / kv
+// heads when that divides both 8 and the query blocks, else 1), and the
+// (pair, slice) units are dealt to the XCDs in order: XCD j takes units j, j + 8,
+// ... one after another.  So the query blocks that stream one pair's keys share
+// S L2s, and each sequence's work is spread over all 8 XCDs: with whole pairs
+// (S = 1) and 4 kv heads, the XCDs 0-3 would hold the even and 4-7 the odd
+// sequences, whatever their lengths.  Slice c of a pair holds its query blocks
+// c, c + S, ... (causal blocks grow heavier with the position), and within a slice
+// the last (heaviest) query blocks go first.  When the units do not divide into 8,
+// the plain order.  Both are bijections of the grid onto (query block, kv head,
+// sequence).
 __device__ __forceinline__ void attn_work_item(int &qblk, int &h, int64_t &seq) {
     const uint32_t nx = gridDim.x, ny = gridDim.y;
     const uint32_t lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
     uint32_t pair = blockIdx.y + ny * blockIdx.z, xo = blockIdx.x;
-    if ((ny * gridDim.z) % 8u == 0) {
-        const uint32_t k = lin >> 3;  // rank of this workgroup on its XCD
-        pair = (lin & 7u) + 8u * (k / nx);
-        xo = k % nx;
+    // S: 2, 4 or 8 (a power of two) for 4, 2 or 1 kv heads; 1 otherwise
+    const uint32_t S = (ny == 1u || ny == 2u || ny == 4u) && nx % (8u / ny) == 0 ? 8u / ny : 1u;
+    const uint32_t k = lin >> 3;  // rank of this workgroup on its XCD
+    if (S == 1u) {
+        if ((ny * gridDim.z) % 8u == 0) {
+            pair = (lin & 7u) + 8u * (k / nx);
+            xo = k % nx;
+        }
+    } else {  // 8 units per sequence: always a multiple of 8
+        const uint32_t sh = __builtin_ctz(S);
+        const uint32_t len = nx >> sh;                   // query blocks per slice
+        const uint32_t u = (lin & 7u) + 8u * (k / len);  // (pair, slice) unit
+        pair = u >> sh;
+        xo = ((k % len) << sh) + (u & (S - 1u));  // slice c: query blocks c, c + S, ... (heavy and light mixed)
     }
     qblk = (int)(nx - 1 - xo);
     h = (int)(pair % ny);
