@@ -82,6 +82,7 @@ struct PrefillArgs {
     int causal;         // 0: every query sees all seq_lens[b] keys
     int qb;             // query positions per workgroup (= 16 * position groups)
     int npg;            // position groups per workgroup
+    int flat;           // 1: workgroups of 8 waves over the sequence's (position group, query head) units
     int64_t max_tiles;  // tile images per (sequence, kv head) in the workspace
     uint8_t *ws;        // tile images [num_seqs][H][max_tiles][kImBytes]
     void *out;
@@ -293,19 +294,36 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     const int L = a.seq_lens[seq];
     const int pos_base = L - T;  // position of query 0
     const int L_eff = visible_keys(a, seq);
-    if (qblk * a.qb >= T || T <= 0) return;
-
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nwaves = nthr >> 6;
+    // This wave's query head inside the GQA group (gh) and first query index (i0), and
+    // the workgroup's last query index.  Plain: wave = (gh, position group pg) of the
+    // workgroup's npg groups.  Flat (GQA groups whose G * npg waves would not spread
+    // evenly over a CU's four SIMDs, e.g. 7): the sequence's (position group, query
+    // head) units in position-group-major order, nwaves consecutive units per
+    // workgroup (at most two position groups when G < 8).
+    int gh, i0, last_i;
+    if (a.flat) {
+        const int units = T > 0 ? (T + kPQ - 1) / kPQ * a.G : 0;
+        const int f0 = qblk * nwaves;
+        if (f0 >= units) return;
+        const int f = f0 + wave;
+        gh = f % a.G;
+        i0 = f < units ? f / a.G * kPQ : T;  // units past the end: inactive
+        last_i = min(T, (min(f0 + nwaves, units) - 1) / a.G * kPQ + kPQ) - 1;
+    } else {
+        if (qblk * a.qb >= T || T <= 0) return;
+        gh = wave / a.npg;
+        const int pg = wave - gh * a.npg;  // 16-position group
+        i0 = qblk * a.qb + pg * kPQ;
+        last_i = min(T, (qblk + 1) * a.qb) - 1;
+    }
     const int g = lane >> 4, col = lane & 15;
     // this lane's operand pieces in a tile image: key col, pieces g and 4 + g; dim col, piece g
     const int koff0 = k_piece(col, g), koff1 = k_piece(col, 4 + g);
     const int ones_off = kImOnes + (col == 0 ? 0 : 16);  // the row-sum operand (MFMA row 0 = col 0)
-    const int gh = wave / a.npg;            // query head inside the GQA group
-    const int pg = wave - gh * a.npg;       // 16-position group
     const int hq = h * a.G + gh;
-    const int i0 = qblk * a.qb + pg * kPQ;  // first query index of this wave
     const bool wave_active = i0 < T;
     const int my_i = i0 + col;              // query index of this lane's column
     const int my_pos = pos_base + my_i;
@@ -314,7 +332,6 @@ __global__ __launch_bounds__(1024) void prefill_attn_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
 
     // ---- key range: causal bound of the whole workgroup --------------------------
-    const int last_i = min(T, (qblk + 1) * a.qb) - 1;
     const bool causal = KQ == kKqInt8 || a.causal;  // the int8 prefill is always causal
     const int kv_end = causal ? min(L_eff, pos_base + last_i + 1) : L_eff;  // keys [0, kv_end) may be visible
     const int n_tiles = (kv_end + kKT - 1) / kKT;
@@ -510,7 +527,8 @@ static void launch_pack(const PrefillArgs &a, int64_t num_seqs, hipStream_t st) 
 template <int DT, int KQ>
 static void launch_attn(const PrefillArgs &a, int64_t num_seqs, int64_t max_q_len, int nwaves, hipStream_t st) {
     const size_t lds = 2 * (size_t)kImBytes;
-    dim3 grid((unsigned)((max_q_len + a.qb - 1) / a.qb), (unsigned)a.H, (unsigned)num_seqs);
+    const int64_t nx = a.flat ? ((max_q_len + kPQ - 1) / kPQ * a.G + nwaves - 1) / nwaves : (max_q_len + a.qb - 1) / a.qb;
+    dim3 grid((unsigned)nx, (unsigned)a.H, (unsigned)num_seqs);
     hipLaunchKernelGGL((prefill_attn_kernel<DT, KQ>), grid, dim3(64 * nwaves), lds, st, a);
 }
 
@@ -593,12 +611,17 @@ int prefill_call(int kq, int causal, const void *q, int32_t dtype, int64_t total
     a.causal = causal != 0;
     a.npg = std::max(1, 8 / a.G);
     a.qb = kPQ * a.npg;
+    // GQA groups of 3, 5, 6 or 7 query heads: G * npg waves (6, 5, 6, 7) per workgroup
+    // would load a CU's four SIMDs unevenly (two 7-wave workgroups: 4, 4, 3, 3 waves,
+    // and each tile's barrier paces a workgroup by its busiest SIMD); they take
+    // workgroups of 8 waves over the flattened (position group, query head) units.
+    a.flat = a.G < 8 && (a.G * a.npg) % 4 != 0;
     a.max_tiles = prefill_tiles(max_seq_len);
     a.ws = static_cast<uint8_t *>(workspace);
     a.out = out;
     a.o_st = out_stride_tok;
     a.o_sh = out_stride_head;
-    const int nwaves = a.G * a.npg;
+    const int nwaves = a.flat ? 8 : a.G * a.npg;
     hipStream_t st = (hipStream_t)stream;
     const bool bf = dtype == RQ_DTYPE_BF16;
     if (kq == kKqInt8) {
