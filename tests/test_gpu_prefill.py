@@ -99,10 +99,26 @@ def test_prefill_block_sizes(BS):
 
 def test_prefill_gqa16_one_kv_head():
     """16 query heads on one kv head: the widest workgroup (16 waves), where the per-wave
-    output staging buffers fill the tile area; two (sequence, kv head) pairs also take
-    the plain work order (the XCD-aware one needs a multiple of 8 pairs)."""
+    output staging buffers fill the tile area; it also takes the plain work order (13
+    query blocks do not cut into the 8 XCD slices of a single kv head, and two
+    (sequence, kv head) pairs do not divide into the 8 XCDs)."""
     p = Params("iso", 4, 3)
     check(prefill_case(9, [200, 77], [260, 77], 1, 16, p), "gqa16")
+
+
+@pytest.mark.parametrize("H,HQ,q_lens,ctx_lens", [
+    (4, 12, [256, 33, 100], [256 + 300, 33, 100 + 1000]),  # GQA 3: 6 workgroups per pair, 2 XCD slices
+    (2, 10, [512, 300], [512 + 200, 300]),                 # GQA 5: 20 workgroups per pair, 4 XCD slices
+    (2, 12, [96, 40], [96 + 64, 40 + 513]),                # GQA 6: 36 units in 5 workgroups, plain order
+])
+def test_prefill_gqa_flattened_workgroups(H, HQ, q_lens, ctx_lens):
+    """GQA groups of 3, 5 and 6 query heads: 8-wave workgroups over the sequence's
+    (16-position group, query head) units in position-group-major order, so a
+    workgroup's waves span two position groups (different causal limits) and the last
+    workgroup of a sequence has waves with no unit; ragged query lengths, chunks after
+    prefixes, with and without the XCD slices of the work order."""
+    p = Params("iso", 3, 3, iso_mode="full")
+    check(prefill_case(37 + HQ // H, q_lens, ctx_lens, H, HQ, p), f"gqa{HQ // H}-flat H={H}")
 
 
 def test_prefill_multi_sequence_requires_cu_seqlens():
