@@ -1180,7 +1180,10 @@ static void launch_decode_h(DecodeArgs &a, size_t lds, hipStream_t st, bool conf
     a.grid_w = std::max(1, per_cu * device_cus() / groups);
     // rank weights by workgroups per CU (workgroups [r CUs, (r+1) CUs) are
     // dispatched r-th onto each CU)
-    static const int kRankWt[5][4] = {{1, 1, 1, 1}, {1, 1, 1, 1}, {65, 35, 35, 35}, {1, 1, 1, 1}, {1, 1, 1, 1}};
+    // (two per CU: 65:35, the best of a sweep on config 1; three: 44:28:28, on config 4's
+    // decodes 202.8-206.8 us against 213.4-215.1 at equal weights, 40:30:30 206.9-210.5,
+    // 50:25:25 214.9-216.1)
+    static const int kRankWt[5][4] = {{1, 1, 1, 1}, {1, 1, 1, 1}, {65, 35, 35, 35}, {44, 28, 28, 28}, {1, 1, 1, 1}};
     const int pc = groups == 1 ? std::min(per_cu, 4) : 1;
     a.split_c = pc > 1 ? a.grid_w / pc : a.grid_w;
     uint64_t tot = 0;
