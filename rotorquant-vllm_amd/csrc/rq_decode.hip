@@ -503,8 +503,13 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecodeArgs a) {
 // so none is skipped); the wait for tile t lets exactly the copies issued after
 // tile t's stay in flight -- and none after the query operand of a segment that
 // starts at tile t.
-// Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.
-constexpr int decode_waves_per_eu(int kb, int vb, int hpw) { return (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1; }
+// Occupancy 4 (128 VGPRs) where the compiler fits the kernel without spilling.  One-
+// and two-head workgroups (at most 8 and 4 per CU) put at most two waves on a SIMD,
+// so they take 2 (256 VGPRs): at 4 their 4-bit variants spilled 20-116 bytes per lane
+// into the loop.
+constexpr int decode_waves_per_eu(int kb, int vb, int hpw) {
+    return hpw == 1 || hpw == 2 ? 2 : (kb + vb == 6 || (kb + vb == 7 && hpw != 4)) ? 4 : 1;
+}
 
 // D3: the cache holds the dense 3-bit index layout (48 index bytes per head).
 // WIDE: more than 8 query heads per kv head.
