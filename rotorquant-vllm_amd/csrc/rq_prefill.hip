@@ -204,11 +204,27 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         }
     }
     __syncthreads();
+    // This thread's index dwords -- K: (key, dword) w = tid + 256 r, r < 4; V: dword
+    // tid >> 4 of the keys of quad tid & 15 -- all loaded before the first image store:
+    // a load issued after a store would wait for it (the compiler cannot rule out that
+    // they alias, and the memory counter completes in order), one round per loop step.
+    static_assert(kKT * 16 == 4 * 256, "four K index dwords per thread");
+    uint32_t xk[4], xv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int w = tid + 256 * r;
+        xk[r] = idx_dword(a.cache + toff[w >> 4] + SL.k_idx + h * SL.ib, w & 15, a.dense3 != 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        xv[i] = idx_dword(a.cache + toff[4 * (tid & 15) + i] + SL.v_idx + h * SL.ib, tid >> 4, a.dense3 != 0);
     if constexpr (KQ == kKqDtype) {
         // K rows in the q dtype: dims 8 dw .. 8 dw + 7 of key tk, one 16-byte piece
-        for (int w = tid; w < kKT * 16; w += 256) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int w = tid + 256 * r;
             const int tk = w >> 4, dw = w & 15;
-            const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
+            const uint32_t x = xk[r];
             const float nrm = knorm[tk];
             uint32_t pr[4];
 #pragma unroll
@@ -222,9 +238,11 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
         }
     } else
     // K rows (dims permuted per 8 as e0 e2 e4 e6 e1 e3 e5 e7), hi and lo
-    for (int w = tid; w < kKT * 16; w += 256) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int w = tid + 256 * r;
         const int tk = w >> 4, dw = w & 15;  // token, dword of the head's 64 index bytes
-        const uint32_t x = idx_dword(a.cache + toff[tk] + SL.k_idx + h * SL.ib, dw, a.dense3 != 0);
+        const uint32_t x = xk[r];
         const float nrm = knorm[tk], inv = kinv;
         uint32_t hw[2], lw[2];  // [0]: even dims (high nibbles), [1]: odd dims (low nibbles)
 #pragma unroll
@@ -253,10 +271,7 @@ __global__ __launch_bounds__(256) void prefill_pack_kernel(PrefillArgs a) {
     // dword) writes 4 consecutive keys = 8 bytes.
     {
         const int tq = tid & 15, dw = tid >> 4;  // key quad (4 consecutive keys), dword position
-        uint32_t x[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            x[i] = idx_dword(a.cache + toff[4 * tq + i] + SL.v_idx + h * SL.ib, dw, a.dense3 != 0);
+        const uint32_t(&x)[4] = xv;
         const int t0 = 4 * tq;
         const int b = t0 >> 4, gg = (t0 >> 2) & 3;
         const int piece = 4 * (b >> 1) + gg, elem_off = 8 * (b & 1);
